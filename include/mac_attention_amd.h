@@ -1,0 +1,209 @@
+/*
+ * mac_attention_amd.h -- C ABI of the MI355X (gfx950) MAC-Attention decode
+ * library (libmac_hip.so).
+ *
+ * Every entry point takes plain pointers, sizes and scalars; no framework
+ * types cross this boundary.  All device pointers must be device memory of the
+ * current HIP device; `stream` is a hipStream_t passed as void* (NULL = the
+ * null stream).  No entry point allocates device memory or synchronises the
+ * host, so every call may be captured into a hipGraph.
+ *
+ * Return value: 0 on success, otherwise a MAC_ERR_* code; mac_last_error()
+ * then returns a NUL-terminated message for the calling thread.
+ *
+ * Reference paths are relative to the reference repository root.  "DECODE"
+ * stands for attention/src/mac_attention/integrations/sglang/csrc/
+ * mac_decode_persistent.cu and "PREFILL" for .../csrc/mac_prefill_update_cache.cu.
+ */
+#ifndef MAC_ATTENTION_AMD_H_
+#define MAC_ATTENTION_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MAC_ABI_VERSION 1
+
+#if defined(__GNUC__)
+#define MAC_API __attribute__((visibility("default")))
+#else
+#define MAC_API
+#endif
+
+enum {
+  MAC_OK = 0,
+  MAC_ERR_INVALID_ARGUMENT = 1, /* shape/size/parameter check failed */
+  MAC_ERR_HIP = 2,              /* a HIP runtime call failed */
+  MAC_ERR_UNSUPPORTED = 3       /* valid input outside what this build supports */
+};
+
+/* Group modes written to group_mode (DECODE:41-43). */
+enum { MAC_GROUP_MAC_HIT = 0, MAC_GROUP_FULL_FALLBACK = 1, MAC_GROUP_MIXED = 2 };
+
+/*
+ * Arguments of one fused MAC decode step.  Field order follows the 68
+ * positional arguments of the reference's Python binding
+ * mac_persistent_decode_bf16 (DECODE:4962-5030); tensor arguments become a
+ * pointer plus the sizes the reference reads from tensor shapes.
+ *
+ * Tensors (row-major, contiguous):
+ *   q_post, q_pre      bf16 [N, Hq, D]        post-/pre-RoPE decode queries
+ *   k_buffer, v_buffer bf16 [pool_tokens, Hkv, D]  paged KV pool
+ *   req_to_token       i32  [req_to_token_rows, req_to_token_stride]
+ *   req_ids, past_lens i32  [>= N]
+ *   out_cache_loc      i32 or i64 [>= N] (out_cache_loc_is_i64)
+ *   query_cache, attn_cache bf16 [R, M, Hq, D]; lse_cache f32 [R, M, Hq]
+ *   out                bf16 [N, Hq, D]; out_lse f32 [N, Hq] or NULL
+ * Workspaces (caller-owned, any content on entry):
+ *   match_dist f32, match_pos/match_slot i32 [N, Hq, max_match_tiles]
+ *   head_* i32 [N, Hq]; group_* i32 [N, Hkv] (leading dimension may exceed N)
+ *   complete_task_go/tile i32 [complete_task_len]
+ *   task_counts i32 [>= 9]
+ *   partial_o (f32, or bf16 if partial_o_is_bf16) [>= N, Hkv, max_tiles_context, G, D]
+ *   partial_lse f32 [>= N, Hkv, max_tiles_context, G]
+ * Readiness gate (DECODE:208-230): cache_ready (u8/bool [R]) NULL disables the
+ * gate; cache_epoch/request_epoch (i64 [R]) are compared only when both are
+ * non-NULL.
+ */
+typedef struct MacDecodeArgs {
+  uint32_t struct_size; /* sizeof(MacDecodeArgs) */
+  uint32_t abi_version; /* MAC_ABI_VERSION */
+
+  const void* q_post;
+  const void* q_pre;
+  const void* k_buffer;
+  const void* v_buffer;
+  const int32_t* req_to_token;
+  const int32_t* req_ids;
+  const int32_t* past_lens;
+  const void* out_cache_loc;
+  void* query_cache;
+  void* attn_cache;
+  float* lse_cache;
+  void* out;
+  float* out_lse;
+
+  float* match_dist;
+  int32_t* match_pos;
+  int32_t* match_slot;
+  int32_t* head_hit;
+  int32_t* head_match_slot;
+  int32_t* head_match_pos;
+  int32_t* head_prefix_end;
+  int32_t* head_rect_start;
+  int32_t* head_new_end;
+  int32_t* group_rect_begin;
+  int32_t* group_rect_end;
+  int32_t* group_rect_tiles;
+  int32_t* group_tail_begin;
+  int32_t* group_tail_end;
+  int32_t* group_tail_tiles;
+  int32_t* group_mode;
+  int32_t* complete_task_go;
+  int32_t* complete_task_tile;
+  int32_t* task_counts;
+  void* partial_o;
+  float* partial_lse;
+
+  const uint8_t* cache_ready;
+  const int64_t* cache_epoch;
+  const int64_t* request_epoch;
+
+  /* shapes */
+  int32_t N, Hq, Hkv, D;
+  int32_t M, R;
+  int64_t pool_tokens;
+  int32_t req_to_token_rows, req_to_token_stride;
+  int32_t out_cache_loc_is_i64;
+  int32_t max_match_tiles;
+  int32_t max_tiles_context; /* partial_o / partial_lse dim 2 */
+  int32_t partial_o_is_bf16;
+  int64_t complete_task_len; /* numel of complete_task_go and complete_task_tile */
+  int32_t workspace_rows;    /* leading dim of head_/group_ workspaces (>= N) */
+
+  /* scalar arguments, same meaning as the reference */
+  int32_t max_context;
+  int32_t tile_tokens;
+  int32_t match_tile_slots;
+  int32_t semantic_pos_ahead;
+  int32_t front_sink_tokens;
+  int32_t gen_min_limit;
+  int32_t lookback_right;
+  int32_t candidate_mode;
+  double threshold;
+  double sm_scale;
+  int32_t debug_enabled;
+  int32_t bench_mode;
+  double bench_hit_rate;
+  double bench_hit_rate_std;
+  double bench_skip_ratio;
+  double bench_skip_ratio_std;
+  double bench_match_lag_mean;
+  double bench_match_lag_std;
+  int32_t bench_seed;
+  int32_t bench_miss_mask;
+  int32_t bench_layer_id;
+  /* Result-affecting switches the reference reads from the environment:
+   * MAC_PERSISTENT_MIXED_GROUP_FALLBACK (DECODE:5229, default 1) and
+   * MAC_BENCH_EXACT_QUOTA (DECODE:5334, default 1). */
+  int32_t mixed_group_fallback;
+  int32_t bench_exact_quota;
+} MacDecodeArgs;
+
+/* Replaces mac_persistent_decode_bf16 (DECODE:4962-5524, pybind DECODE:5526-5529).
+ * Writes out/out_lse, one ring row per (request, query head) at past_len % M
+ * (skipped for requests failing the readiness gate), and the decision
+ * workspaces head_hit ([3] in the reference's workspace list), head_match_pos
+ * ([5]), group_mode ([15]) and task_counts ([22]). */
+MAC_API int mac_persistent_decode_bf16(const MacDecodeArgs* args, void* stream);
+
+/* Replaces mac_prefill_update_cache (PREFILL:324-372, pybind PREFILL:500-502).
+ * q_cache/attn_cache bf16 [R, M, H, D]; lse_cache f32 [R, M, H];
+ * request_length i32 [request_length_len] with request_length_len == R
+ * (indexed by request, bumped by lens[b]) or == B (indexed by batch row, not
+ * bumped; this form wins when R == B, as in the reference); src_q/src_attn bf16
+ * [src_rows, H, D]; src_lse f32 [src_rows, H]; offsets i32 [B+1]; lens i32 [B];
+ * q_post_cache bf16 [R, M, H, D] or NULL (rows written get bf16 NaN 0x7fc0). */
+MAC_API int mac_prefill_update_cache(void* q_cache, void* attn_cache, float* lse_cache,
+                             int32_t* request_length, int32_t request_length_len,
+                             const int32_t* req_ids, int32_t B, const void* src_q,
+                             const void* src_attn, const float* src_lse, int32_t src_rows,
+                             const int32_t* offsets, const int32_t* lens, int32_t R,
+                             int32_t capacity, int32_t num_heads, int32_t head_dim,
+                             void* q_post_cache, void* stream);
+
+/* Replaces mac_mark_persistent_ready (PREFILL:374-409):
+ * cache_epoch[req] = request_epoch[req]; ready[req] = 1 for req in req_ids[0:B]. */
+MAC_API int mac_mark_persistent_ready(uint8_t* ready, int64_t* cache_epoch,
+                              const int64_t* request_epoch, const int32_t* req_ids, int32_t B,
+                              int32_t R, void* stream);
+
+/* Replaces mac_invalidate_persistent_ready (PREFILL:411-446):
+ * ready[req] = 0; cache_epoch[req] = -1; request_epoch[req] += 1. */
+MAC_API int mac_invalidate_persistent_ready(uint8_t* ready, int64_t* cache_epoch,
+                                    int64_t* request_epoch, const int32_t* req_ids, int32_t B,
+                                    int32_t R, void* stream);
+
+/* Replaces mac_update_request_state (PREFILL:448-497):
+ * cache_lens[i] = max(seq_lens[i] - cur_lens[i], 0); req_len[req] = seq_lens[i];
+ * match_req_len[req] = cache_lens[i]. */
+MAC_API int mac_update_request_state(int32_t* req_len, int32_t* match_req_len, int32_t* cache_lens,
+                             const int32_t* req_ids, const int32_t* seq_lens,
+                             const int32_t* cur_lens, int32_t B, int32_t R, void* stream);
+
+/* Message of the last failed call on this thread ("" if none).  No reference
+ * counterpart: the reference raises through TORCH_CHECK instead. */
+MAC_API const char* mac_last_error(void);
+
+/* ABI version of the loaded library (MAC_ABI_VERSION it was built with).  No
+ * reference counterpart. */
+MAC_API int mac_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAC_ATTENTION_AMD_H_ */

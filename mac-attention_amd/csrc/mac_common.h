@@ -1,0 +1,89 @@
+// mac_common.h -- device helpers shared by the gfx950 MAC kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mac {
+
+constexpr int kHeadDim = 128;      // the only head size the reference supports (DECODE:5081)
+constexpr int kMaxGroup = 8;       // largest GQA group (DECODE:5086, kMaxWarps)
+constexpr int kBlock = 256;        // threads per workgroup for every decode kernel
+constexpr int kWaves = kBlock / 64;
+constexpr int kMaxPlanGroups = 4096;  // N * Hkv handled by the in-workgroup task planner
+
+// bf16 <-> f32.  A 32-bit word holds two bf16 values, low element first.
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+// Round to nearest even; NaN stays NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ void unpack8(const uint4& w, float* f) {
+  f[0] = bf16_lo(w.x); f[1] = bf16_hi(w.x);
+  f[2] = bf16_lo(w.y); f[3] = bf16_hi(w.y);
+  f[4] = bf16_lo(w.z); f[5] = bf16_hi(w.z);
+  f[6] = bf16_lo(w.w); f[7] = bf16_hi(w.w);
+}
+
+// DPP lane exchange within a row of 16 lanes.
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xf, 0xf, false));
+}
+// Sum over the 16 lanes of a DPP row; every lane of the row receives the total.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp<0x141>(x);  // row_half_mirror
+  x += dpp<0x140>(x);  // row_mirror
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+// Finite "minus infinity" for running maxima: exp2(kNegBig - finite) == 0 and
+// exp2(kNegBig - kNegBig) == 1, so empty states merge without NaNs.
+constexpr float kNegBig = -1.0e30f;
+
+__device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// DECODE:713-716
+__device__ __forceinline__ int cache_end_for_pos(int p, int s) {
+  int e = p + 1 - s;
+  return e > 0 ? e : 0;
+}
+
+// DECODE:798-807
+__device__ __forceinline__ int ring_slot_to_pos(int past_len, int m, int slot) {
+  if (past_len < m) return slot;
+  int order = slot - past_len % m;
+  if (order < 0) order += m;
+  return past_len - m + order;
+}
+
+// DECODE:837-848
+__device__ __forceinline__ int pos_to_ring_slot(int past_len, int m, int pos) {
+  if (past_len < m) return pos;
+  int slot = pos - (past_len - m) + past_len % m;
+  if (slot >= m) slot -= m;
+  if (slot < 0) slot += m;
+  return slot;
+}
+
+// DECODE:809-811: smaller distance wins, ties go to the smaller logical position.
+__device__ __forceinline__ bool better_pair(float d, int pos, float best_d, int best_pos) {
+  return d < best_d || (d == best_d && pos < best_pos);
+}
+
+}  // namespace mac

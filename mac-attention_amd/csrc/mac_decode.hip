@@ -1,0 +1,1183 @@
+// mac_decode.hip -- MAC-Attention fused decode step for MI355X (gfx950).
+//
+// One decode step is three kernels on the caller's stream (graph-capturable,
+// no host synchronisation, no allocation):
+//
+//  1. match_decide  (one workgroup per (request, KV head) group)
+//     Scans the request's ring of cached pre-RoPE queries for every query head
+//     of the group (squared L2, best = smallest distance, ties to the smaller
+//     logical position), applies the readiness gate and the optional synthetic
+//     bench override, and turns the per-head results into the group's mode and
+//     its KV spans: sink [0, min(F, new_end)), band [rect_begin, new_end) and
+//     tail [new_end, kv_len).  Reference: DECODE:942-1099, :1101-1402.
+//
+//  2. span_attention  (persistent grid sized to the device's residency)
+//     Every workgroup plans the same task list from the group spans: the
+//     spans are cut into chunks of C tokens (C picked from the total token
+//     count so that the grid gets ~4 tasks per workgroup), and workgroup w
+//     takes tasks w, w+W, ...  A task streams the K/V rows of its chunk once
+//     for all G query heads of the group (16 lanes per token row, 16-byte
+//     loads, two tokens per row in flight plus a one-iteration prefetch),
+//     masks band positions that precede a head's own band start, and keeps an
+//     online log2-domain softmax per head.  The task writes one partial
+//     (o, lse) per head.  Reference producers: DECODE:1870-3423.
+//
+//  3. merge_write  (one workgroup per group)
+//     Per head: cached entry (hit heads) + band partials -> ring row at
+//     past_len % M (only for ready requests) -> + sink and tail partials ->
+//     out / out_lse.  Reference: DECODE:4280-4685.
+//
+// Workspace use (caller-owned, reference names):
+//   head_*, group_mode, group_rect_begin/end, group_tail_begin/end: same
+//     meaning as in the reference (DECODE:1270-1402);
+//   group_rect_tiles / group_tail_tiles: number of band / tail tasks;
+//   complete_task_go[g]: chunk size C_g of group g; complete_task_tile[g]:
+//     number of tasks of group g (written by workgroup 0 of span_attention);
+//   match_dist/pos/slot[..., 0]: best (distance, position, slot) of the scan;
+//   partial_o / partial_lse: one (o, lse) partial per task and head;
+//   task_counts: [0] tasks, [1] tail tasks, [3] non-hit groups whose band needs
+//     more than one task, [4] chunk C, [5] non-hit groups, [6] full-fallback
+//     groups, [7]/[8] max band tasks of full-fallback / mixed groups.
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "mac_attention_amd.h"
+#include "mac_common.h"
+
+namespace mac {
+
+struct Shape {
+  int N, Hq, Hkv, M, R;
+  int64_t pool_tokens;
+  int r2t_rows, r2t_stride;
+  int out_cache_loc_is_i64;
+  int max_match_tiles;
+  int ws_rows;
+};
+
+struct DecideParams {
+  Shape s;
+  const uint16_t* q_pre;
+  const uint16_t* query_cache;
+  const float* lse_cache;
+  const int32_t* req_ids;
+  const int32_t* past_lens;
+  const uint8_t* cache_ready;
+  const int64_t* cache_epoch;
+  const int64_t* request_epoch;
+  float* match_dist;
+  int32_t* match_pos;
+  int32_t* match_slot;
+  int32_t* head_hit;
+  int32_t* head_match_slot;
+  int32_t* head_match_pos;
+  int32_t* head_prefix_end;
+  int32_t* head_rect_start;
+  int32_t* head_new_end;
+  int32_t* group_rect_begin;
+  int32_t* group_rect_end;
+  int32_t* group_tail_begin;
+  int32_t* group_tail_end;
+  int32_t* group_mode;
+  int S, F, gen_min_limit, lookback_right, candidate_mode;
+  float thr_dist;
+  int mixed_group_fallback;
+  int bench_mode, bench_exact_quota, bench_seed, bench_miss_mask, bench_layer_id;
+  float bench_hit_rate, bench_hit_rate_std, bench_skip_ratio, bench_skip_ratio_std;
+  float bench_match_lag_mean, bench_match_lag_std;
+};
+
+struct AttnParams {
+  Shape s;
+  const uint16_t* q_post;
+  const uint16_t* k_buffer;
+  const uint16_t* v_buffer;
+  const int32_t* req_to_token;
+  const int32_t* req_ids;
+  const int32_t* past_lens;
+  const void* out_cache_loc;
+  const int32_t* head_rect_start;
+  const int32_t* group_rect_begin;
+  const int32_t* group_rect_end;
+  const int32_t* group_tail_end;
+  const int32_t* group_mode;
+  int32_t* group_rect_tiles;
+  int32_t* group_tail_tiles;
+  int32_t* group_chunk;   // complete_task_go
+  int32_t* group_ntasks;  // complete_task_tile
+  int32_t* task_counts;
+  void* partial_o;
+  float* partial_lse;
+  int partial_bf16;
+  int64_t o_group_stride;  // elements of partial_o per group
+  int cap;                 // task slots per group
+  int F;
+  float q_scale;  // sm_scale * log2(e)
+};
+
+struct MergeParams {
+  Shape s;
+  const uint16_t* q_pre;
+  uint16_t* query_cache;
+  uint16_t* attn_cache;
+  float* lse_cache;
+  uint16_t* out;
+  float* out_lse;
+  const int32_t* req_ids;
+  const int32_t* past_lens;
+  const uint8_t* cache_ready;
+  const int64_t* cache_epoch;
+  const int64_t* request_epoch;
+  const int32_t* head_hit;
+  const int32_t* head_match_slot;
+  const int32_t* group_rect_begin;
+  const int32_t* group_rect_end;
+  const int32_t* group_tail_end;
+  const int32_t* group_chunk;
+  const void* partial_o;
+  const float* partial_lse;
+  int partial_bf16;
+  int64_t o_group_stride;
+  int cap;
+  int F;
+};
+
+// DECODE:221-230.  A request id outside [0, R) is never ready: its ring rows
+// cannot be addressed, so it must not be matched against or written.
+__device__ __forceinline__ bool request_ready(const uint8_t* ready, const int64_t* ce,
+                                              const int64_t* re, int req, int R) {
+  if (req < 0 || req >= R) return false;
+  if (ready == nullptr) return true;
+  if (ready[req] == 0) return false;
+  if (ce != nullptr && re != nullptr && ce[req] != re[req]) return false;
+  return true;
+}
+
+// ---------------------------------------------------------------- hashing --
+// DECODE:817-835 and :375-388, used only by the synthetic bench override.
+__device__ __forceinline__ uint32_t mix_u32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+__device__ __forceinline__ float uniform01_u32(uint32_t x) {
+  return static_cast<float>(mix_u32(x) & 0x00ffffffu) * (1.0f / 16777216.0f);
+}
+__device__ __forceinline__ float pseudo_normal_u32(uint32_t x) {
+  float s = uniform01_u32(x) + uniform01_u32(x ^ 0x9e3779b9u) + uniform01_u32(x ^ 0x85ebca6bu) +
+            uniform01_u32(x ^ 0xc2b2ae35u);
+  return (s - 2.0f) * 1.7320508075688772f;
+}
+__device__ __forceinline__ float clampf(float v, float lo, float hi) { return fminf(fmaxf(v, lo), hi); }
+
+// =========================================================== 1. decide ====
+
+// Lanes of a wave form four rows of 16; row r of pass p scans query head
+// r + 4p of the group, lane c of the row owns dims [8c, 8c+8).  Each wave
+// takes slots wave, wave+4, ... in batches of kSlotBatch whose 16-byte loads
+// are all issued before any reduction (the scan is latency-bound).
+template <int G>
+__global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
+  constexpr int kPasses = (G + 3) / 4;
+  constexpr int kSlotBatch = 8;
+  const int g = blockIdx.x;
+  const int n = g / p.s.Hkv;
+  const int hkv = g - n * p.s.Hkv;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int row = lane >> 4;
+  const int c = lane & 15;
+  const int M = p.s.M;
+  const int Hq = p.s.Hq;
+
+  const int P = p.past_lens[n];
+  const int req = p.req_ids[n];
+  const bool ready = request_ready(p.cache_ready, p.cache_epoch, p.request_epoch, req, p.s.R);
+  // DECODE:974-981
+  const int cand_begin = max(0, P - M);
+  int cand_end = P;
+  if (p.candidate_mode == 1) cand_end = max(cand_begin, P - p.lookback_right);
+  const bool eligible = P >= p.gen_min_limit && cand_end > cand_begin && ready;
+
+  __shared__ float s_d[kWaves][kMaxGroup];
+  __shared__ int s_p[kWaves][kMaxGroup];
+  __shared__ int s_s[kWaves][kMaxGroup];
+
+  float best_d[kPasses];
+  int best_p[kPasses], best_s[kPasses];
+  float q[kPasses][8];
+#pragma unroll
+  for (int ps = 0; ps < kPasses; ++ps) {
+    best_d[ps] = INFINITY;
+    best_p[ps] = INT_MAX;
+    best_s[ps] = -1;
+    const int hl = row + 4 * ps;
+    uint4 w = make_uint4(0, 0, 0, 0);
+    if (hl < G) {
+      const int64_t off = (static_cast<int64_t>(n) * Hq + hkv * G + hl) * kHeadDim + c * 8;
+      w = *reinterpret_cast<const uint4*>(p.q_pre + off);
+    }
+    unpack8(w, q[ps]);
+  }
+
+  if (eligible) {
+    const int64_t cache_req = static_cast<int64_t>(req) * M;
+    for (int s0 = wave; s0 < M; s0 += kWaves * kSlotBatch) {
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps) {
+        const int hl = row + 4 * ps;
+        uint4 w[kSlotBatch];
+        int pos[kSlotBatch];
+        bool ok[kSlotBatch];
+#pragma unroll
+        for (int u = 0; u < kSlotBatch; ++u) {
+          const int slot = s0 + u * kWaves;
+          pos[u] = ring_slot_to_pos(P, M, slot);
+          ok[u] = slot < M && pos[u] >= cand_begin && pos[u] < cand_end && hl < G;
+          w[u] = make_uint4(0, 0, 0, 0);
+          if (ok[u]) {
+            const int64_t off =
+                ((cache_req + slot) * Hq + hkv * G + hl) * kHeadDim + c * 8;
+            w[u] = *reinterpret_cast<const uint4*>(p.query_cache + off);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kSlotBatch; ++u) {
+          float cf[8];
+          unpack8(w[u], cf);
+          float acc = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float df = q[ps][i] - cf[i];
+            acc = fmaf(df, df, acc);
+          }
+          acc = row16_sum(acc);
+          if (ok[u] && better_pair(acc, pos[u], best_d[ps], best_p[ps])) {
+            best_d[ps] = acc;
+            best_p[ps] = pos[u];
+            best_s[ps] = s0 + u * kWaves;
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int ps = 0; ps < kPasses; ++ps) {
+    const int hl = row + 4 * ps;
+    if (c == 0 && hl < G) {
+      s_d[wave][hl] = best_d[ps];
+      s_p[wave][hl] = best_p[ps];
+      s_s[wave][hl] = best_s[ps];
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+
+  // ---- per-head decisions (lanes 0..G-1 of wave 0), DECODE:1147-1299 ----
+  const int h = lane;
+  const bool head_lane = h < G;
+  const int hq = hkv * G + (head_lane ? h : 0);
+  float bd = INFINITY;
+  int bp = INT_MAX, bs = -1;
+  if (head_lane) {
+    for (int w = 0; w < kWaves; ++w) {
+      if (better_pair(s_d[w][h], s_p[w][h], bd, bp)) {
+        bd = s_d[w][h];
+        bp = s_p[w][h];
+        bs = s_s[w][h];
+      }
+    }
+  }
+  const int64_t ho = static_cast<int64_t>(n) * Hq + hq;
+  if (head_lane) {
+    const int64_t mo = ho * p.s.max_match_tiles;
+    p.match_dist[mo] = bd;
+    p.match_pos[mo] = bp;
+    p.match_slot[mo] = bs;
+  }
+  bool hit = eligible && bs >= 0 && bd < p.thr_dist;
+  const int S = p.S;
+  const int F = p.F;
+  if (p.bench_mode != 0 || p.bench_miss_mask >= 0) {  // DECODE:1184-1269
+    const int lane_i = h;
+    const uint32_t unit_id = p.bench_mode == 2 ? static_cast<uint32_t>(hkv) : static_cast<uint32_t>(hq);
+    const uint32_t base_key = static_cast<uint32_t>(p.bench_seed) ^
+                              (static_cast<uint32_t>(p.bench_layer_id) * 0x9e3779b9u) ^
+                              (static_cast<uint32_t>(P) * 0x85ebca6bu);
+    const uint32_t key = base_key ^ (static_cast<uint32_t>(n) * 0xc2b2ae35u) ^ (unit_id * 0x27d4eb2fu);
+    const float hit_rate = clampf(
+        p.bench_hit_rate + p.bench_hit_rate_std * pseudo_normal_u32(key ^ 0x4cf5ad43u), 0.0f, 1.0f);
+    if (p.bench_miss_mask >= 0) {
+      const bool miss = lane_i < 30 && ((p.bench_miss_mask >> lane_i) & 1) != 0;
+      hit = eligible && P > 0 && M > 0 && !miss;
+    } else if (p.bench_exact_quota != 0 && p.bench_hit_rate_std == 0.0f) {
+      const int unit_total = p.bench_mode == 2 ? p.s.N * p.s.Hkv : p.s.N * Hq;
+      const int unit = p.bench_mode == 2 ? n * p.s.Hkv + hkv : n * Hq + hq;
+      float miss_rate = fminf(fmaxf(1.0f - p.bench_hit_rate, 0.0f), 1.0f);
+      int miss_units = unit_total > 0 ? static_cast<int>(floorf(miss_rate * static_cast<float>(unit_total) + 0.5f)) : 0;
+      miss_units = min(max(miss_units, 0), unit_total);
+      const int offset = unit_total > 0 ? static_cast<int>(base_key % static_cast<uint32_t>(unit_total)) : 0;
+      int rotated = unit + offset;
+      if (rotated >= unit_total) rotated -= unit_total;
+      hit = eligible && P > 0 && M > 0 && !(rotated < miss_units);
+    } else {
+      hit = eligible && P > 0 && M > 0 && uniform01_u32(key ^ 0x165667b1u) < hit_rate;
+    }
+    if (hit) {
+      const int max_lag = min(M, P);
+      const int ne = cache_end_for_pos(P, S);
+      float lag_f = p.bench_match_lag_mean + p.bench_match_lag_std * pseudo_normal_u32(key ^ 0xd3a2646cu);
+      bool req_skip = false;
+      if (p.bench_skip_ratio >= 0.0f) {
+        req_skip = true;
+        const float sr = clampf(p.bench_skip_ratio + p.bench_skip_ratio_std * pseudo_normal_u32(key ^ 0xfd7046c5u),
+                                0.0f, 0.999999f);
+        int tpe = static_cast<int>(roundf(sr * static_cast<float>(P)));
+        if (tpe > ne - 1) tpe = ne - 1;
+        if (tpe < 0) tpe = 0;
+        lag_f = static_cast<float>(ne - tpe);
+      }
+      int lag = static_cast<int>(roundf(lag_f));
+      if (lag < 1) lag = 1;
+      if (req_skip) {
+        if (lag > P) lag = P;
+      } else if (lag > max_lag) {
+        lag = max_lag;
+      }
+      if (max_lag <= 0 || ne <= 0) {
+        hit = false;
+        bp = INT_MAX;
+        bs = -1;
+      } else {
+        bp = max(P - lag, 0);
+        bs = pos_to_ring_slot(P, M, bp);
+      }
+    } else {
+      bp = INT_MAX;
+      bs = -1;
+    }
+  }
+  int prefix_end = 0, mpos = -1, mslot = -1;
+  if (hit) {
+    mpos = bp;
+    mslot = bs;
+    prefix_end = cache_end_for_pos(mpos, S);
+  }
+  if (hit && F > 0 && prefix_end < F) {  // front-sink demotion, DECODE:1285-1291
+    hit = false;
+    mpos = mslot = -1;
+    prefix_end = 0;
+  }
+  const int new_end = cache_end_for_pos(P, S);
+  const int fs_begin = min(F, new_end);
+  // DECODE:1315-1328 validity of a hit head for MAC reuse
+  bool valid = false;
+  if (head_lane && hit && mslot >= 0) {
+    const float pl = p.lse_cache[(static_cast<int64_t>(req) * M + mslot) * Hq + hq];
+    const int clen = new_end - prefix_end;
+    valid = isfinite(pl) && clen >= 0 && clen <= M;
+  }
+  const uint64_t vmask = __ballot(valid);
+  const int valid_count = __popcll(vmask);
+  int mode = MAC_GROUP_FULL_FALLBACK;
+  if (valid_count == G)
+    mode = MAC_GROUP_MAC_HIT;
+  else if (valid_count > 0 && p.mixed_group_fallback != 0)
+    mode = MAC_GROUP_MIXED;
+  const bool keep = mode == MAC_GROUP_MAC_HIT || (mode == MAC_GROUP_MIXED && valid);
+  int rect_start = keep ? prefix_end : fs_begin;
+  if (!keep) {
+    hit = false;
+    mpos = mslot = -1;
+    prefix_end = 0;
+  }
+  // group band begins at the smallest head band start
+  int rb = head_lane ? rect_start : INT_MAX;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) rb = min(rb, __shfl_xor(rb, off));
+  if (mode != MAC_GROUP_MAC_HIT) rb = fs_begin;
+  rb = max(0, min(rb, new_end));
+  if (head_lane) {
+    p.head_hit[ho] = hit ? 1 : 0;
+    p.head_match_slot[ho] = mslot;
+    p.head_match_pos[ho] = mpos;
+    p.head_prefix_end[ho] = prefix_end;
+    p.head_rect_start[ho] = rect_start;
+    p.head_new_end[ho] = new_end;
+  }
+  if (lane == 0) {
+    const int64_t go = static_cast<int64_t>(n) * p.s.Hkv + hkv;
+    p.group_mode[go] = mode;
+    p.group_rect_begin[go] = rb;
+    p.group_rect_end[go] = new_end;
+    p.group_tail_begin[go] = new_end;
+    p.group_tail_end[go] = P + 1;
+  }
+}
+
+// ========================================================= 2. attention ====
+
+struct GroupSpans {
+  int sink_end, band_begin, new_end, kv_len;
+  int chunk, n_sink, n_band, n_tail;
+};
+
+__device__ __forceinline__ int group_tokens(int sink_end, int band_begin, int new_end, int kv_len) {
+  return sink_end + (new_end - band_begin) + (kv_len - new_end);
+}
+
+// Chunk of a group: the launch-wide chunk, enlarged (to a multiple of 64) when
+// the group would otherwise need more task slots than its workspace holds.
+__device__ __forceinline__ int group_chunk(int tokens, int chunk, int cap) {
+  int need = ceil_div(tokens, max(cap - 3, 1));
+  need = ceil_div(need, 64) * 64;
+  return max(chunk, need);
+}
+
+__device__ __forceinline__ GroupSpans load_spans(const int32_t* rect_begin, const int32_t* rect_end,
+                                                 const int32_t* tail_end, int g, int F, int chunk,
+                                                 int cap) {
+  GroupSpans s;
+  s.band_begin = rect_begin[g];
+  s.new_end = rect_end[g];
+  s.kv_len = tail_end[g];
+  s.sink_end = min(F, s.new_end);
+  s.chunk = group_chunk(group_tokens(s.sink_end, s.band_begin, s.new_end, s.kv_len), chunk, cap);
+  s.n_sink = ceil_div(s.sink_end, s.chunk);
+  s.n_band = ceil_div(s.new_end - s.band_begin, s.chunk);
+  s.n_tail = ceil_div(s.kv_len - s.new_end, s.chunk);
+  return s;
+}
+
+// Block-wide exclusive scan of per-thread values (256 threads).
+__device__ __forceinline__ int block_exclusive_scan(int v, int* s_tmp, int& total) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    int y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) s_tmp[wave] = x;
+  __syncthreads();
+  int base = 0;
+  total = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    if (w < wave) base += s_tmp[w];
+    total += s_tmp[w];
+  }
+  __syncthreads();
+  return base + x - v;
+}
+
+template <int G>
+__global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
+  constexpr int U = 2;                 // tokens per row per iteration
+  constexpr int kStep = kWaves * 4 * U;  // tokens per workgroup iteration
+  __shared__ int s_off[kMaxPlanGroups + 1];
+  __shared__ int s_tmp[kWaves];
+  __shared__ float s_o[kWaves][G][kHeadDim];
+  __shared__ float s_ml[kWaves][G][2];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int row = lane >> 4;
+  const int c = lane & 15;
+  const int NG = p.s.N * p.s.Hkv;
+  const int W = gridDim.x;
+
+  // ---- plan: launch-wide chunk from the total token count ----
+  const int per_thread = ceil_div(NG, kBlock);
+  const int g_lo = min(tid * per_thread, NG);
+  const int g_hi = min(g_lo + per_thread, NG);
+  long long tok = 0;
+  for (int g = g_lo; g < g_hi; ++g) {
+    const int ne = p.group_rect_end[g];
+    tok += group_tokens(min(p.F, ne), p.group_rect_begin[g], ne, p.group_tail_end[g]);
+  }
+  // reduce token count (64-bit) across the block
+  {
+    long long x = tok;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+    __shared__ long long s_tok[kWaves];
+    if (lane == 0) s_tok[wave] = x;
+    __syncthreads();
+    tok = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) tok += s_tok[w];
+    __syncthreads();
+  }
+  const long long target_tasks = 4LL * W;
+  int chunk = static_cast<int>((tok + target_tasks - 1) / target_tasks);
+  chunk = ceil_div(max(chunk, 64), 64) * 64;
+  chunk = min(chunk, 16384);
+  int my_tasks = 0;
+  for (int g = g_lo; g < g_hi; ++g) {
+    GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, g, p.F, chunk, p.cap);
+    s_off[g] = sp.n_sink + sp.n_band + sp.n_tail;
+    my_tasks += s_off[g];
+  }
+  int total_tasks = 0;
+  int base = block_exclusive_scan(my_tasks, s_tmp, total_tasks);
+  for (int g = g_lo; g < g_hi; ++g) {
+    const int cnt = s_off[g];
+    s_off[g] = base;
+    base += cnt;
+  }
+  if (tid == 0) s_off[NG] = total_tasks;
+  __syncthreads();
+
+  if (blockIdx.x == 0) {
+    // descriptors for merge_write and the reference's task counters
+    int nonhit = 0, ff = 0, red = 0, max_ff = 0, max_mixed = 0, tails = 0;
+    for (int g = tid; g < NG; g += kBlock) {
+      GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, g, p.F, chunk, p.cap);
+      p.group_chunk[g] = sp.chunk;
+      p.group_ntasks[g] = sp.n_sink + sp.n_band + sp.n_tail;
+      p.group_rect_tiles[g] = sp.n_band;
+      p.group_tail_tiles[g] = sp.n_tail;
+      const int mode = p.group_mode[g];
+      tails += sp.n_tail;
+      if (mode != MAC_GROUP_MAC_HIT) {
+        ++nonhit;
+        if (sp.n_band > 1) ++red;
+      }
+      if (mode == MAC_GROUP_FULL_FALLBACK) {
+        ++ff;
+        max_ff = max(max_ff, sp.n_band);
+      }
+      if (mode == MAC_GROUP_MIXED) max_mixed = max(max_mixed, sp.n_band);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      nonhit += __shfl_xor(nonhit, off);
+      ff += __shfl_xor(ff, off);
+      red += __shfl_xor(red, off);
+      tails += __shfl_xor(tails, off);
+      max_ff = max(max_ff, __shfl_xor(max_ff, off));
+      max_mixed = max(max_mixed, __shfl_xor(max_mixed, off));
+    }
+    __shared__ int s_cnt[kWaves][6];
+    if (lane == 0) {
+      s_cnt[wave][0] = nonhit;
+      s_cnt[wave][1] = ff;
+      s_cnt[wave][2] = red;
+      s_cnt[wave][3] = tails;
+      s_cnt[wave][4] = max_ff;
+      s_cnt[wave][5] = max_mixed;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int a[6] = {0, 0, 0, 0, 0, 0};
+      for (int w = 0; w < kWaves; ++w) {
+        for (int i = 0; i < 4; ++i) a[i] += s_cnt[w][i];
+        a[4] = max(a[4], s_cnt[w][4]);
+        a[5] = max(a[5], s_cnt[w][5]);
+      }
+      p.task_counts[0] = total_tasks;
+      p.task_counts[1] = a[3];
+      p.task_counts[2] = 0;
+      p.task_counts[3] = a[2];
+      p.task_counts[4] = chunk;
+      p.task_counts[5] = a[0];
+      p.task_counts[6] = a[1];
+      p.task_counts[7] = a[4];
+      p.task_counts[8] = a[5];
+    }
+  }
+
+  // ---- tasks ----
+  const int Hq = p.s.Hq;
+  const int Hkv = p.s.Hkv;
+  const int my_tok = wave * 4 + row;  // token offset inside each 16-token sub-block
+  for (int t = blockIdx.x; t < total_tasks; t += W) {
+    // group of task t: last g with s_off[g] <= t
+    int lo = 0, hi = NG - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_off[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    const int g = lo;
+    const int j = t - s_off[g];
+    const int n = g / Hkv;
+    const int hkv = g - n * Hkv;
+    const GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, g, p.F, chunk, p.cap);
+    int a, b;
+    bool band = false;
+    if (j < sp.n_sink) {
+      a = j * sp.chunk;
+      b = min(a + sp.chunk, sp.sink_end);
+    } else if (j < sp.n_sink + sp.n_band) {
+      a = sp.band_begin + (j - sp.n_sink) * sp.chunk;
+      b = min(a + sp.chunk, sp.new_end);
+      band = true;
+    } else {
+      a = sp.new_end + (j - sp.n_sink - sp.n_band) * sp.chunk;
+      b = min(a + sp.chunk, sp.kv_len);
+    }
+    const int P = p.past_lens[n];
+    const int req = p.req_ids[n];
+    const bool req_ok = req >= 0 && req < p.s.r2t_rows;
+    int64_t cur_loc;
+    if (p.s.out_cache_loc_is_i64)
+      cur_loc = static_cast<const int64_t*>(p.out_cache_loc)[n];
+    else
+      cur_loc = static_cast<const int32_t*>(p.out_cache_loc)[n];
+    const int32_t* r2t = p.req_to_token + static_cast<int64_t>(req_ok ? req : 0) * p.s.r2t_stride;
+
+    // per-head band start (positions before it are masked for that head)
+    int mb[G];
+    float q[G][8];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const int hq = hkv * G + h;
+      mb[h] = band ? p.head_rect_start[static_cast<int64_t>(n) * Hq + hq] : 0;
+      const uint4 w = *reinterpret_cast<const uint4*>(p.q_post + (static_cast<int64_t>(n) * Hq + hq) * kHeadDim + c * 8);
+      unpack8(w, q[h]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) q[h][i] *= p.q_scale;
+    }
+    float m[G], l[G], o[G][8];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      m[h] = kNegBig;
+      l[h] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[h][i] = 0.0f;
+    }
+
+    auto phys_of = [&](int pos) -> int64_t {
+      if (pos >= b || !req_ok) return -1;
+      const int64_t ph = pos == P ? cur_loc : static_cast<int64_t>(r2t[pos]);
+      return (ph >= 0 && ph < p.s.pool_tokens) ? ph : -1;
+    };
+    const int64_t kv_stride = static_cast<int64_t>(Hkv) * kHeadDim;
+    const uint16_t* kbase = p.k_buffer + static_cast<int64_t>(hkv) * kHeadDim + c * 8;
+    const uint16_t* vbase = p.v_buffer + static_cast<int64_t>(hkv) * kHeadDim + c * 8;
+
+    int64_t ph0[U], ph1[U];
+    uint4 k0[U], v0[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) ph0[u] = phys_of(a + u * 16 + my_tok);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      k0[u] = make_uint4(0, 0, 0, 0);
+      v0[u] = make_uint4(0, 0, 0, 0);
+      if (ph0[u] >= 0) {
+        k0[u] = *reinterpret_cast<const uint4*>(kbase + ph0[u] * kv_stride);
+        v0[u] = *reinterpret_cast<const uint4*>(vbase + ph0[u] * kv_stride);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) ph1[u] = phys_of(a + kStep + u * 16 + my_tok);
+
+    for (int base_pos = a; base_pos < b; base_pos += kStep) {
+      // prefetch the next iteration's rows and the one after's indices
+      uint4 k1[U], v1[U];
+      int64_t ph2[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        k1[u] = make_uint4(0, 0, 0, 0);
+        v1[u] = make_uint4(0, 0, 0, 0);
+        if (ph1[u] >= 0) {
+          k1[u] = *reinterpret_cast<const uint4*>(kbase + ph1[u] * kv_stride);
+          v1[u] = *reinterpret_cast<const uint4*>(vbase + ph1[u] * kv_stride);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) ph2[u] = phys_of(base_pos + 2 * kStep + u * 16 + my_tok);
+
+      float s[G][U];
+      float vf[U][8];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float kf[8];
+        unpack8(k0[u], kf);
+        unpack8(v0[u], vf[u]);
+        const int pos = base_pos + u * 16 + my_tok;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc = fmaf(q[h][i], kf[i], acc);
+          acc = row16_sum(acc);
+          s[h][u] = (ph0[u] >= 0 && pos >= mb[h]) ? acc : -INFINITY;
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float mx = s[h][0];
+#pragma unroll
+        for (int u = 1; u < U; ++u) mx = fmaxf(mx, s[h][u]);
+        const float m_new = fmaxf(m[h], mx);
+        const float alpha = fast_exp2(m[h] - m_new);
+        float pu[U];
+        float psum = 0.0f;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          pu[u] = fast_exp2(s[h][u] - m_new);
+          psum += pu[u];
+        }
+        l[h] = fmaf(l[h], alpha, psum);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float acc = o[h][i] * alpha;
+#pragma unroll
+          for (int u = 0; u < U; ++u) acc = fmaf(pu[u], vf[u][i], acc);
+          o[h][i] = acc;
+        }
+        m[h] = m_new;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        k0[u] = k1[u];
+        v0[u] = v1[u];
+        ph0[u] = ph1[u];
+        ph1[u] = ph2[u];
+      }
+    }
+
+    // ---- combine the four rows of the wave, then the waves ----
+#pragma unroll
+    for (int msk = 16; msk <= 32; msk <<= 1) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float mo = __shfl_xor(m[h], msk);
+        const float lo2 = __shfl_xor(l[h], msk);
+        const float m_new = fmaxf(m[h], mo);
+        const float a1 = fast_exp2(m[h] - m_new);
+        const float a2 = fast_exp2(mo - m_new);
+        l[h] = l[h] * a1 + lo2 * a2;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float oo = __shfl_xor(o[h][i], msk);
+          o[h][i] = o[h][i] * a1 + oo * a2;
+        }
+        m[h] = m_new;
+      }
+    }
+    if (row == 0) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s_o[wave][h][c * 8 + i] = o[h][i];
+        if (c == 0) {
+          s_ml[wave][h][0] = m[h];
+          s_ml[wave][h][1] = l[h];
+        }
+      }
+    }
+    __syncthreads();
+    const int64_t slot = static_cast<int64_t>(g) * p.cap + j;
+    for (int e = tid; e < G * kHeadDim; e += kBlock) {
+      const int h = e / kHeadDim;
+      const int d = e - h * kHeadDim;
+      float mm = kNegBig;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, s_ml[w][h][0]);
+      float ll = 0.0f, oo = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float sc = fast_exp2(s_ml[w][h][0] - mm);
+        ll += s_ml[w][h][1] * sc;
+        oo += s_o[w][h][d] * sc;
+      }
+      const bool nonempty = ll > 0.0f;
+      const float ov = nonempty ? oo / ll : 0.0f;
+      const int64_t oi = static_cast<int64_t>(g) * p.o_group_stride + (static_cast<int64_t>(j) * G + h) * kHeadDim + d;
+      if (p.partial_bf16)
+        static_cast<uint16_t*>(p.partial_o)[oi] = f32_to_bf16(ov);
+      else
+        static_cast<float*>(p.partial_o)[oi] = ov;
+      if (d == 0) p.partial_lse[slot * G + h] = nonempty ? (mm + log2f(ll)) * kLn2 : -INFINITY;
+    }
+    __syncthreads();
+  }
+}
+
+// ============================================================ 3. merge ====
+
+template <int G>
+__global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
+  constexpr int kElems = (G * kHeadDim + kBlock - 1) / kBlock;
+  const int g = blockIdx.x;
+  const int n = g / p.s.Hkv;
+  const int hkv = g - n * p.s.Hkv;
+  const int tid = threadIdx.x;
+  const int M = p.s.M;
+  const int Hq = p.s.Hq;
+  const int P = p.past_lens[n];
+  const int req = p.req_ids[n];
+  const bool ready = request_ready(p.cache_ready, p.cache_epoch, p.request_epoch, req, p.s.R);
+  const int dest = P % M;
+
+  const int band_begin = p.group_rect_begin[g];
+  const int new_end = p.group_rect_end[g];
+  const int kv_len = p.group_tail_end[g];
+  const int sink_end = min(p.F, new_end);
+  const int chunk = p.group_chunk[g];
+  const int n_sink = ceil_div(sink_end, chunk);
+  const int n_band = ceil_div(new_end - band_begin, chunk);
+  const int n_tail = ceil_div(kv_len - new_end, chunk);
+
+  float acc[kElems], lse[kElems];
+  int hh[kElems], dd[kElems];
+  bool own[kElems];
+#pragma unroll
+  for (int k = 0; k < kElems; ++k) {
+    const int e = tid + k * kBlock;
+    own[k] = e < G * kHeadDim;
+    hh[k] = own[k] ? e / kHeadDim : 0;
+    dd[k] = e - hh[k] * kHeadDim;
+    acc[k] = 0.0f;
+    lse[k] = -INFINITY;
+    if (own[k]) {
+      const int hq = hkv * G + hh[k];
+      const int64_t ho = static_cast<int64_t>(n) * Hq + hq;
+      const int mslot = p.head_match_slot[ho];
+      if (p.head_hit[ho] != 0 && mslot >= 0 && req >= 0 && req < p.s.R) {
+        const int64_t rowi = (static_cast<int64_t>(req) * M + mslot) * Hq + hq;
+        const float pl = p.lse_cache[rowi];
+        if (isfinite(pl)) {
+          lse[k] = pl;
+          acc[k] = bf16_to_f32(p.attn_cache[rowi * kHeadDim + dd[k]]);
+        }
+      }
+    }
+  }
+
+  auto merge_task = [&](int j) {
+    const int64_t slot = static_cast<int64_t>(g) * p.cap + j;
+#pragma unroll
+    for (int k = 0; k < kElems; ++k) {
+      if (!own[k]) continue;
+      const float ol = p.partial_lse[slot * G + hh[k]];
+      if (!isfinite(ol)) continue;  // DECODE:866-890: an empty partial is skipped
+      const int64_t oi = static_cast<int64_t>(g) * p.o_group_stride + (static_cast<int64_t>(j) * G + hh[k]) * kHeadDim + dd[k];
+      const float ov = p.partial_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p.partial_o)[oi])
+                                      : static_cast<const float*>(p.partial_o)[oi];
+      if (!isfinite(lse[k])) {
+        lse[k] = ol;
+        acc[k] = ov;
+        continue;
+      }
+      const float mx = fmaxf(lse[k], ol);
+      const float w1 = __expf(lse[k] - mx);
+      const float w2 = __expf(ol - mx);
+      const float den = w1 + w2;
+      acc[k] = (w1 * acc[k] + w2 * ov) / den;
+      lse[k] = mx + __logf(den);
+    }
+  };
+
+  for (int j = n_sink; j < n_sink + n_band; ++j) merge_task(j);
+  __syncthreads();  // every entry read above precedes the ring write below
+
+  if (ready) {
+#pragma unroll
+    for (int k = 0; k < kElems; ++k) {
+      if (!own[k]) continue;
+      const int hq = hkv * G + hh[k];
+      const int64_t rowi = (static_cast<int64_t>(req) * M + dest) * Hq + hq;
+      const bool valid = isfinite(lse[k]);
+      p.query_cache[rowi * kHeadDim + dd[k]] = p.q_pre[(static_cast<int64_t>(n) * Hq + hq) * kHeadDim + dd[k]];
+      p.attn_cache[rowi * kHeadDim + dd[k]] = valid ? f32_to_bf16(acc[k]) : static_cast<uint16_t>(0);
+      if (dd[k] == 0) p.lse_cache[rowi] = valid ? lse[k] : -INFINITY;
+    }
+  }
+
+  for (int j = 0; j < n_sink; ++j) merge_task(j);
+  for (int j = n_sink + n_band; j < n_sink + n_band + n_tail; ++j) merge_task(j);
+
+#pragma unroll
+  for (int k = 0; k < kElems; ++k) {
+    if (!own[k]) continue;
+    const int hq = hkv * G + hh[k];
+    const int64_t ho = static_cast<int64_t>(n) * Hq + hq;
+    const bool valid = isfinite(lse[k]);
+    p.out[ho * kHeadDim + dd[k]] = valid ? f32_to_bf16(acc[k]) : static_cast<uint16_t>(0);
+    if (p.out_lse != nullptr && dd[k] == 0) p.out_lse[ho] = valid ? lse[k] : -INFINITY;
+  }
+}
+
+// ============================================================ host side ====
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+#define MAC_REQUIRE(cond, ...) \
+  do {                         \
+    if (!(cond)) return fail(MAC_ERR_INVALID_ARGUMENT, __VA_ARGS__); \
+  } while (0)
+
+#define MAC_HIP(call)                                                               \
+  do {                                                                              \
+    hipError_t e_ = (call);                                                         \
+    if (e_ != hipSuccess) return fail(MAC_ERR_HIP, "%s: %s", #call, hipGetErrorString(e_)); \
+  } while (0)
+
+struct DeviceInfo {
+  int cus = 0;
+  int attn_blocks_per_cu[kMaxGroup + 1] = {};
+};
+
+std::mutex g_dev_mu;
+DeviceInfo g_dev[64];
+
+template <int G>
+void* attn_kernel_ptr() { return reinterpret_cast<void*>(&span_attention_kernel<G>); }
+
+int attn_residency(int dev, int G, int* cus, int* per_cu) {
+  std::lock_guard<std::mutex> lk(g_dev_mu);
+  if (dev < 0 || dev >= 64) return fail(MAC_ERR_UNSUPPORTED, "device index %d out of range", dev);
+  DeviceInfo& di = g_dev[dev];
+  if (di.cus == 0) {
+    MAC_HIP(hipDeviceGetAttribute(&di.cus, hipDeviceAttributeMultiprocessorCount, dev));
+  }
+  if (di.attn_blocks_per_cu[G] == 0) {
+    void* fn = nullptr;
+    switch (G) {
+      case 1: fn = attn_kernel_ptr<1>(); break;
+      case 2: fn = attn_kernel_ptr<2>(); break;
+      case 3: fn = attn_kernel_ptr<3>(); break;
+      case 4: fn = attn_kernel_ptr<4>(); break;
+      case 5: fn = attn_kernel_ptr<5>(); break;
+      case 6: fn = attn_kernel_ptr<6>(); break;
+      case 7: fn = attn_kernel_ptr<7>(); break;
+      default: fn = attn_kernel_ptr<8>(); break;
+    }
+    int blocks = 0;
+    MAC_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kBlock, 0));
+    di.attn_blocks_per_cu[G] = blocks > 0 ? blocks : 1;
+  }
+  *cus = di.cus;
+  *per_cu = di.attn_blocks_per_cu[G];
+  return MAC_OK;
+}
+
+template <int G>
+int launch_all(const DecideParams& dp, const AttnParams& ap, const MergeParams& mp, int attn_grid,
+               hipStream_t stream) {
+  const int NG = dp.s.N * dp.s.Hkv;
+  hipLaunchKernelGGL(match_decide_kernel<G>, dim3(NG), dim3(kBlock), 0, stream, dp);
+  MAC_HIP(hipGetLastError());
+  hipLaunchKernelGGL(span_attention_kernel<G>, dim3(attn_grid), dim3(kBlock), 0, stream, ap);
+  MAC_HIP(hipGetLastError());
+  hipLaunchKernelGGL(merge_write_kernel<G>, dim3(NG), dim3(kBlock), 0, stream, mp);
+  MAC_HIP(hipGetLastError());
+  return MAC_OK;
+}
+
+}  // namespace mac
+
+using namespace mac;
+
+extern "C" const char* mac_last_error(void) { return g_err; }
+extern "C" int mac_abi_version(void) { return MAC_ABI_VERSION; }
+
+extern "C" int mac_persistent_decode_bf16(const MacDecodeArgs* a, void* stream_ptr) {
+  g_err[0] = '\0';
+  MAC_REQUIRE(a != nullptr, "args must not be NULL");
+  MAC_REQUIRE(a->struct_size == sizeof(MacDecodeArgs) && a->abi_version == MAC_ABI_VERSION,
+              "MacDecodeArgs size/version mismatch (got %u/%u, library expects %zu/%d)",
+              a->struct_size, a->abi_version, sizeof(MacDecodeArgs), MAC_ABI_VERSION);
+  const int N = a->N, Hq = a->Hq, Hkv = a->Hkv, D = a->D, M = a->M;
+  // checks mirror DECODE:5031-5153
+  MAC_REQUIRE(D == kHeadDim, "persistent decode v1 supports D=128 only");
+  MAC_REQUIRE(Hkv > 0 && Hq % Hkv == 0, "Hq must be divisible by Hkv");
+  const int G = Hq / Hkv;
+  MAC_REQUIRE(G > 0 && G <= kMaxGroup, "unsupported GQA group size");
+  MAC_REQUIRE(N >= 0, "batch must be non-negative");
+  MAC_REQUIRE(M > 0, "query_cache capacity M must be positive");
+  MAC_REQUIRE(a->R > 0, "query_cache must hold at least one request");
+  MAC_REQUIRE(a->workspace_rows >= N, "group_mode workspace too small");
+  MAC_REQUIRE(a->tile_tokens > 0 && a->match_tile_slots > 0, "tile sizes must be positive");
+  MAC_REQUIRE(a->max_match_tiles >= (M + a->match_tile_slots - 1) / a->match_tile_slots && a->max_match_tiles > 0,
+              "match workspace too small");
+  MAC_REQUIRE(a->max_tiles_context >= (a->max_context + a->tile_tokens - 1) / a->tile_tokens,
+              "rect workspace too small");
+  MAC_REQUIRE(a->max_tiles_context >= 4,
+              "rect workspace too small: this build needs at least 4 partial slots per group");
+  MAC_REQUIRE(a->semantic_pos_ahead >= 0, "semantic_pos_ahead must be non-negative");
+  MAC_REQUIRE(a->bench_mode == 0 || a->bench_mode == 1 || a->bench_mode == 2,
+              "unsupported synthetic MAC bench mode");
+  MAC_REQUIRE(static_cast<int64_t>(N) * Hkv <= kMaxPlanGroups,
+              "N * Hkv = %lld exceeds the %d groups one launch can plan", static_cast<long long>(N) * Hkv,
+              kMaxPlanGroups);
+  MAC_REQUIRE(a->complete_task_len >= static_cast<int64_t>(N) * Hkv, "complete task workspace too small");
+  MAC_REQUIRE(a->req_to_token_rows > 0 && a->req_to_token_stride >= 0, "req_to_token must be 2-D");
+  if (N == 0) return MAC_OK;
+  MAC_REQUIRE(a->q_post && a->q_pre && a->k_buffer && a->v_buffer && a->req_to_token && a->req_ids &&
+                  a->past_lens && a->out_cache_loc && a->query_cache && a->attn_cache && a->lse_cache &&
+                  a->out && a->match_dist && a->match_pos && a->match_slot && a->head_hit &&
+                  a->head_match_slot && a->head_match_pos && a->head_prefix_end && a->head_rect_start &&
+                  a->head_new_end && a->group_rect_begin && a->group_rect_end && a->group_rect_tiles &&
+                  a->group_tail_begin && a->group_tail_end && a->group_tail_tiles && a->group_mode &&
+                  a->complete_task_go && a->complete_task_tile && a->task_counts && a->partial_o &&
+                  a->partial_lse,
+              "a required pointer is NULL");
+
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  int dev = 0;
+  MAC_HIP(hipGetDevice(&dev));
+  int cus = 0, per_cu = 0;
+  int rc = attn_residency(dev, G, &cus, &per_cu);
+  if (rc != MAC_OK) return rc;
+
+  Shape s{};
+  s.N = N;
+  s.Hq = Hq;
+  s.Hkv = Hkv;
+  s.M = M;
+  s.R = a->R;
+  s.pool_tokens = a->pool_tokens;
+  s.r2t_rows = a->req_to_token_rows;
+  s.r2t_stride = a->req_to_token_stride;
+  s.out_cache_loc_is_i64 = a->out_cache_loc_is_i64 ? 1 : 0;
+  s.max_match_tiles = a->max_match_tiles;
+  s.ws_rows = a->workspace_rows;
+
+  // group_* arrays are indexed n * Hkv + hkv; head_* arrays n * Hq + hq.
+  DecideParams dp{};
+  dp.s = s;
+  dp.q_pre = static_cast<const uint16_t*>(a->q_pre);
+  dp.query_cache = static_cast<const uint16_t*>(a->query_cache);
+  dp.lse_cache = a->lse_cache;
+  dp.req_ids = a->req_ids;
+  dp.past_lens = a->past_lens;
+  dp.cache_ready = a->cache_ready;
+  dp.cache_epoch = a->cache_ready ? a->cache_epoch : nullptr;
+  dp.request_epoch = a->cache_ready ? a->request_epoch : nullptr;
+  dp.match_dist = a->match_dist;
+  dp.match_pos = a->match_pos;
+  dp.match_slot = a->match_slot;
+  dp.head_hit = a->head_hit;
+  dp.head_match_slot = a->head_match_slot;
+  dp.head_match_pos = a->head_match_pos;
+  dp.head_prefix_end = a->head_prefix_end;
+  dp.head_rect_start = a->head_rect_start;
+  dp.head_new_end = a->head_new_end;
+  dp.group_rect_begin = a->group_rect_begin;
+  dp.group_rect_end = a->group_rect_end;
+  dp.group_tail_begin = a->group_tail_begin;
+  dp.group_tail_end = a->group_tail_end;
+  dp.group_mode = a->group_mode;
+  dp.S = a->semantic_pos_ahead;
+  dp.F = a->front_sink_tokens > 0 ? a->front_sink_tokens : 0;
+  dp.gen_min_limit = a->gen_min_limit;
+  dp.lookback_right = a->lookback_right;
+  dp.candidate_mode = a->candidate_mode;
+  {
+    const float thr = static_cast<float>(a->threshold);
+    dp.thr_dist = 2.0f * static_cast<float>(D) * (1.0f - thr) * (1.0f - thr);  // DECODE:5342
+  }
+  dp.mixed_group_fallback = a->mixed_group_fallback;
+  dp.bench_mode = a->bench_mode;
+  dp.bench_exact_quota = a->bench_exact_quota;
+  dp.bench_seed = a->bench_seed;
+  dp.bench_miss_mask = a->bench_miss_mask;
+  dp.bench_layer_id = a->bench_layer_id;
+  dp.bench_hit_rate = static_cast<float>(a->bench_hit_rate);
+  dp.bench_hit_rate_std = static_cast<float>(a->bench_hit_rate_std);
+  dp.bench_skip_ratio = static_cast<float>(a->bench_skip_ratio);
+  dp.bench_skip_ratio_std = static_cast<float>(a->bench_skip_ratio_std);
+  dp.bench_match_lag_mean = static_cast<float>(a->bench_match_lag_mean);
+  dp.bench_match_lag_std = static_cast<float>(a->bench_match_lag_std);
+
+  const int cap = a->max_tiles_context;
+  const int64_t o_group_stride = static_cast<int64_t>(cap) * G * kHeadDim;
+
+  AttnParams ap{};
+  ap.s = s;
+  ap.q_post = static_cast<const uint16_t*>(a->q_post);
+  ap.k_buffer = static_cast<const uint16_t*>(a->k_buffer);
+  ap.v_buffer = static_cast<const uint16_t*>(a->v_buffer);
+  ap.req_to_token = a->req_to_token;
+  ap.req_ids = a->req_ids;
+  ap.past_lens = a->past_lens;
+  ap.out_cache_loc = a->out_cache_loc;
+  ap.head_rect_start = a->head_rect_start;
+  ap.group_rect_begin = a->group_rect_begin;
+  ap.group_rect_end = a->group_rect_end;
+  ap.group_tail_end = a->group_tail_end;
+  ap.group_mode = a->group_mode;
+  ap.group_rect_tiles = a->group_rect_tiles;
+  ap.group_tail_tiles = a->group_tail_tiles;
+  ap.group_chunk = a->complete_task_go;
+  ap.group_ntasks = a->complete_task_tile;
+  ap.task_counts = a->task_counts;
+  ap.partial_o = a->partial_o;
+  ap.partial_lse = a->partial_lse;
+  ap.partial_bf16 = a->partial_o_is_bf16 ? 1 : 0;
+  ap.o_group_stride = o_group_stride;
+  ap.cap = cap;
+  ap.F = dp.F;
+  ap.q_scale = static_cast<float>(a->sm_scale) * kLog2e;
+
+  MergeParams mp{};
+  mp.s = s;
+  mp.q_pre = dp.q_pre;
+  mp.query_cache = static_cast<uint16_t*>(a->query_cache);
+  mp.attn_cache = static_cast<uint16_t*>(a->attn_cache);
+  mp.lse_cache = a->lse_cache;
+  mp.out = static_cast<uint16_t*>(a->out);
+  mp.out_lse = a->out_lse;
+  mp.req_ids = a->req_ids;
+  mp.past_lens = a->past_lens;
+  mp.cache_ready = dp.cache_ready;
+  mp.cache_epoch = dp.cache_epoch;
+  mp.request_epoch = dp.request_epoch;
+  mp.head_hit = a->head_hit;
+  mp.head_match_slot = a->head_match_slot;
+  mp.group_rect_begin = a->group_rect_begin;
+  mp.group_rect_end = a->group_rect_end;
+  mp.group_tail_end = a->group_tail_end;
+  mp.group_chunk = a->complete_task_go;
+  mp.partial_o = a->partial_o;
+  mp.partial_lse = a->partial_lse;
+  mp.partial_bf16 = ap.partial_bf16;
+  mp.o_group_stride = o_group_stride;
+  mp.cap = cap;
+  mp.F = dp.F;
+
+  // Persistent grid: what the device keeps resident, but no more workgroups
+  // than the largest task count the caller's max_context allows.
+  const int NG = N * Hkv;
+  const long long max_tokens = static_cast<long long>(a->max_context) + dp.F + 1;
+  const long long max_tasks = static_cast<long long>(NG) * ((max_tokens + 63) / 64 + 3);
+  long long grid = static_cast<long long>(cus) * per_cu;
+  if (grid > max_tasks) grid = max_tasks;
+  if (grid < 1) grid = 1;
+
+  switch (G) {
+    case 1: return launch_all<1>(dp, ap, mp, static_cast<int>(grid), stream);
+    case 2: return launch_all<2>(dp, ap, mp, static_cast<int>(grid), stream);
+    case 3: return launch_all<3>(dp, ap, mp, static_cast<int>(grid), stream);
+    case 4: return launch_all<4>(dp, ap, mp, static_cast<int>(grid), stream);
+    case 5: return launch_all<5>(dp, ap, mp, static_cast<int>(grid), stream);
+    case 6: return launch_all<6>(dp, ap, mp, static_cast<int>(grid), stream);
+    case 7: return launch_all<7>(dp, ap, mp, static_cast<int>(grid), stream);
+    default: return launch_all<8>(dp, ap, mp, static_cast<int>(grid), stream);
+  }
+}

@@ -1,0 +1,517 @@
+"""Loader and Python binding for the gfx950 MAC kernels.
+
+Replaces attention/src/mac_attention/integrations/sglang/bridge.py of the
+reference: same loader names, same call signatures, same errors
+(``RuntimeError`` for every failed check), but instead of JIT-compiling CUDA
+with ``torch.utils.cpp_extension`` it binds the prebuilt C-ABI library
+``libmac_hip.so`` (declared in ``include/mac_attention_amd.h``) with ctypes.
+
+PyTorch is used only to read tensor metadata (pointer, dtype, shape) and the
+current HIP stream; every kernel runs from the library.  If the library is
+missing the loaders raise -- there is no fallback implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from functools import lru_cache
+from typing import Any
+
+import torch  # loads the HIP runtime the library must share
+
+_PKG_ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))))
+LIB_PATH = os.environ.get("MAC_HIP_LIBRARY", os.path.join(_PKG_ROOT, "libmac_hip.so"))
+
+ABI_VERSION = 1
+_MAX_GROUP = 8
+_HEAD_DIM = 128
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_u32 = ctypes.c_uint32
+_f64 = ctypes.c_double
+
+
+class MacDecodeArgs(ctypes.Structure):
+    """ctypes mirror of ``MacDecodeArgs`` in include/mac_attention_amd.h."""
+
+    _fields_ = [
+        ("struct_size", _u32), ("abi_version", _u32),
+        ("q_post", _p), ("q_pre", _p), ("k_buffer", _p), ("v_buffer", _p),
+        ("req_to_token", _p), ("req_ids", _p), ("past_lens", _p), ("out_cache_loc", _p),
+        ("query_cache", _p), ("attn_cache", _p), ("lse_cache", _p), ("out", _p), ("out_lse", _p),
+        ("match_dist", _p), ("match_pos", _p), ("match_slot", _p),
+        ("head_hit", _p), ("head_match_slot", _p), ("head_match_pos", _p),
+        ("head_prefix_end", _p), ("head_rect_start", _p), ("head_new_end", _p),
+        ("group_rect_begin", _p), ("group_rect_end", _p), ("group_rect_tiles", _p),
+        ("group_tail_begin", _p), ("group_tail_end", _p), ("group_tail_tiles", _p),
+        ("group_mode", _p), ("complete_task_go", _p), ("complete_task_tile", _p),
+        ("task_counts", _p), ("partial_o", _p), ("partial_lse", _p),
+        ("cache_ready", _p), ("cache_epoch", _p), ("request_epoch", _p),
+        ("N", _i32), ("Hq", _i32), ("Hkv", _i32), ("D", _i32), ("M", _i32), ("R", _i32),
+        ("pool_tokens", _i64),
+        ("req_to_token_rows", _i32), ("req_to_token_stride", _i32),
+        ("out_cache_loc_is_i64", _i32), ("max_match_tiles", _i32), ("max_tiles_context", _i32),
+        ("partial_o_is_bf16", _i32),
+        ("complete_task_len", _i64),
+        ("workspace_rows", _i32),
+        ("max_context", _i32), ("tile_tokens", _i32), ("match_tile_slots", _i32),
+        ("semantic_pos_ahead", _i32), ("front_sink_tokens", _i32), ("gen_min_limit", _i32),
+        ("lookback_right", _i32), ("candidate_mode", _i32),
+        ("threshold", _f64), ("sm_scale", _f64),
+        ("debug_enabled", _i32), ("bench_mode", _i32),
+        ("bench_hit_rate", _f64), ("bench_hit_rate_std", _f64), ("bench_skip_ratio", _f64),
+        ("bench_skip_ratio_std", _f64), ("bench_match_lag_mean", _f64),
+        ("bench_match_lag_std", _f64),
+        ("bench_seed", _i32), ("bench_miss_mask", _i32), ("bench_layer_id", _i32),
+        ("mixed_group_fallback", _i32), ("bench_exact_quota", _i32),
+    ]
+
+
+EXPORTED_SYMBOLS = (
+    "mac_persistent_decode_bf16",
+    "mac_prefill_update_cache",
+    "mac_mark_persistent_ready",
+    "mac_invalidate_persistent_ready",
+    "mac_update_request_state",
+    "mac_last_error",
+    "mac_abi_version",
+)
+
+
+@lru_cache(maxsize=1)
+def load_library(path: str | None = None) -> ctypes.CDLL:
+    """Open libmac_hip.so and declare its C signatures (no GPU work)."""
+    path = path or LIB_PATH
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"MAC HIP library not found at {path}; build it with `python -c "
+            f"'import __graft_entry__ as g; g.build()'` from the repository root"
+        )
+    lib = ctypes.CDLL(path)
+    lib.mac_last_error.restype = ctypes.c_char_p
+    lib.mac_abi_version.restype = ctypes.c_int
+    lib.mac_persistent_decode_bf16.argtypes = [ctypes.POINTER(MacDecodeArgs), _p]
+    lib.mac_persistent_decode_bf16.restype = ctypes.c_int
+    lib.mac_prefill_update_cache.argtypes = [
+        _p, _p, _p, _p, _i32, _p, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i32, _p, _p,
+    ]
+    lib.mac_prefill_update_cache.restype = ctypes.c_int
+    for name in ("mac_mark_persistent_ready", "mac_invalidate_persistent_ready"):
+        fn = getattr(lib, name)
+        fn.argtypes = [_p, _p, _p, _p, _i32, _i32, _p]
+        fn.restype = ctypes.c_int
+    lib.mac_update_request_state.argtypes = [_p, _p, _p, _p, _p, _p, _i32, _i32, _p]
+    lib.mac_update_request_state.restype = ctypes.c_int
+    if lib.mac_abi_version() != ABI_VERSION:
+        raise RuntimeError(
+            f"{path} has ABI version {lib.mac_abi_version()}, binding expects {ABI_VERSION}"
+        )
+    return lib
+
+
+def _raise_on(lib: ctypes.CDLL, rc: int) -> None:
+    if rc != 0:
+        msg = lib.mac_last_error().decode(errors="replace")
+        raise RuntimeError(msg or f"MAC HIP call failed with code {rc}")
+
+
+# ------------------------------------------------------------- checks ----
+# Messages follow the reference's TORCH_CHECKs (mac_decode_persistent.cu:4932-4945).
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _check_tensor(t: torch.Tensor, name: str, dtype: torch.dtype, dim: int) -> None:
+    _check(t.is_cuda, f"{name} must be CUDA")
+    _check(t.is_contiguous(), f"{name} must be contiguous")
+    _check(t.dtype == dtype, f"{name} has wrong dtype")
+    _check(t.dim() == dim, f"{name} has wrong rank")
+
+
+def _check_partial_o(t: torch.Tensor, name: str) -> None:
+    _check(t.is_cuda, f"{name} must be CUDA")
+    _check(t.is_contiguous(), f"{name} must be contiguous")
+    _check(t.dtype in (torch.float32, torch.bfloat16), f"{name} must be float32 or bfloat16")
+    _check(t.dim() == 5, f"{name} has wrong rank")
+
+
+def _env_flag(name: str, default: int) -> int:
+    raw = os.environ.get(name)
+    if raw is None:
+        return default
+    try:
+        return 1 if int(raw) != 0 else 0
+    except ValueError:
+        return 0
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    if t is None or t.numel() == 0:
+        return None
+    return t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class PersistentDecodeExtension:
+    """Object returned by :func:`load_mac_persistent_decode_extension`."""
+
+    def __init__(self, lib: ctypes.CDLL):
+        self._lib = lib
+
+    def mac_persistent_decode_bf16(
+        self,
+        q_post, q_pre, k_buffer, v_buffer, req_to_token, req_ids, past_lens, out_cache_loc,
+        query_cache, attn_cache, lse_cache, out, optional_lse,
+        match_dist, match_pos, match_slot,
+        head_hit, head_match_slot, head_match_pos, head_prefix_end, head_rect_start, head_new_end,
+        group_rect_begin, group_rect_end, group_rect_tiles, group_tail_begin, group_tail_end,
+        group_tail_tiles, group_mode,
+        complete_task_go, complete_task_tile, tail_task_go, tail_task_tile, hit_tail_task_ho,
+        hit_tail_task_tile, task_counts,
+        partial_rect_o, partial_rect_lse, partial_rect_reduced_o, partial_rect_reduced_lse,
+        partial_tail_o, partial_tail_lse, phase_cycles,
+        max_context, tile_tokens, match_tile_slots, semantic_pos_ahead, front_sink_tokens,
+        gen_min_limit, lookback_right, candidate_mode,
+        threshold, sm_scale, debug_enabled, bench_mode,
+        bench_hit_rate, bench_hit_rate_std, bench_skip_ratio, bench_skip_ratio_std,
+        bench_match_lag_mean, bench_match_lag_std, bench_seed, bench_miss_mask, bench_layer_id,
+        query_post_cache, mac_cache_ready, mac_cache_epoch, mac_request_epoch,
+    ) -> None:
+        """One fused MAC decode step (reference: mac_decode_persistent.cu:4962-5524).
+
+        Same 68 positional arguments, same in-place outputs, returns None.
+        ``query_post_cache`` is accepted and ignored, as in the reference
+        (:5045-5049).  ``MAC_PERSISTENT_MIXED_GROUP_FALLBACK`` and
+        ``MAC_BENCH_EXACT_QUOTA`` are read from the environment on every call.
+        """
+        bf16, f32, i32, i64 = torch.bfloat16, torch.float32, torch.int32, torch.int64
+        _check_tensor(q_post, "q_post", bf16, 3)
+        _check_tensor(q_pre, "q_pre", bf16, 3)
+        _check_tensor(k_buffer, "k_buffer", bf16, 3)
+        _check_tensor(v_buffer, "v_buffer", bf16, 3)
+        _check_tensor(req_to_token, "req_to_token", i32, 2)
+        _check_tensor(req_ids, "req_ids", i32, 1)
+        _check_tensor(past_lens, "past_lens", i32, 1)
+        _check(out_cache_loc.is_cuda, "out_cache_loc must be CUDA")
+        _check(out_cache_loc.is_contiguous(), "out_cache_loc must be contiguous")
+        _check(out_cache_loc.dim() == 1, "out_cache_loc has wrong rank")
+        _check(out_cache_loc.dtype in (i32, i64), "out_cache_loc must be int32 or int64")
+        _check_tensor(query_cache, "query_cache", bf16, 4)
+        if query_post_cache is not None and query_post_cache.numel() > 0:
+            _check_tensor(query_post_cache, "query_post_cache", bf16, 4)
+        _check_tensor(attn_cache, "attn_cache", bf16, 4)
+        _check_tensor(lse_cache, "lse_cache", f32, 3)
+        _check_tensor(out, "out", bf16, 3)
+        _check(optional_lse.is_cuda, "optional_lse must be CUDA")
+        _check(optional_lse.is_contiguous(), "optional_lse must be contiguous")
+        _check(optional_lse.numel() == 0 or optional_lse.dtype == f32,
+               "optional_lse must be empty or float32")
+        _check(phase_cycles.is_cuda, "phase_cycles must be CUDA")
+        _check(phase_cycles.dtype == i64, "phase_cycles must be int64")
+        _check(phase_cycles.numel() >= 6, "phase_cycles must have at least 6 elements")
+        _check_tensor(match_dist, "match_dist", f32, 3)
+        _check_tensor(match_pos, "match_pos", i32, 3)
+        _check_tensor(match_slot, "match_slot", i32, 3)
+        for name, t in (("head_hit", head_hit), ("head_match_slot", head_match_slot),
+                        ("head_match_pos", head_match_pos), ("head_prefix_end", head_prefix_end),
+                        ("head_rect_start", head_rect_start), ("head_new_end", head_new_end),
+                        ("group_rect_begin", group_rect_begin), ("group_rect_end", group_rect_end),
+                        ("group_rect_tiles", group_rect_tiles),
+                        ("group_tail_begin", group_tail_begin), ("group_tail_end", group_tail_end),
+                        ("group_tail_tiles", group_tail_tiles), ("group_mode", group_mode)):
+            _check_tensor(t, name, i32, 2)
+        for name, t in (("complete_task_go", complete_task_go),
+                        ("complete_task_tile", complete_task_tile),
+                        ("tail_task_go", tail_task_go), ("tail_task_tile", tail_task_tile),
+                        ("hit_tail_task_ho", hit_tail_task_ho),
+                        ("hit_tail_task_tile", hit_tail_task_tile), ("task_counts", task_counts)):
+            _check_tensor(t, name, i32, 1)
+        _check_partial_o(partial_rect_o, "partial_rect_o")
+        _check_tensor(partial_rect_lse, "partial_rect_lse", f32, 4)
+        _check_partial_o(partial_rect_reduced_o, "partial_rect_reduced_o")
+        _check_tensor(partial_rect_reduced_lse, "partial_rect_reduced_lse", f32, 4)
+        _check_partial_o(partial_tail_o, "partial_tail_o")
+        _check_tensor(partial_tail_lse, "partial_tail_lse", f32, 4)
+        _check(partial_rect_reduced_o.dtype == partial_rect_o.dtype
+               and partial_tail_o.dtype == partial_rect_o.dtype,
+               "all partial output workspaces must use the same dtype")
+
+        N, Hq, D = (int(x) for x in q_post.shape)
+        Hkv = int(k_buffer.shape[1])
+        _check(D == _HEAD_DIM, "persistent decode v1 supports D=128 only")
+        _check(tuple(q_pre.shape) == tuple(q_post.shape), "q_pre/q_post shape mismatch")
+        _check(tuple(v_buffer.shape) == tuple(k_buffer.shape), "k/v shape mismatch")
+        _check(int(k_buffer.shape[2]) == D, "k/v head_dim mismatch")
+        _check(Hkv > 0 and Hq % Hkv == 0, "Hq must be divisible by Hkv")
+        G = Hq // Hkv
+        _check(0 < G <= _MAX_GROUP, "unsupported GQA group size")
+        _check(req_ids.shape[0] >= N and past_lens.shape[0] >= N and out_cache_loc.shape[0] >= N,
+               "batch metadata too small")
+        _check(tuple(out.shape) == tuple(q_post.shape), "out shape mismatch")
+        _check(optional_lse.numel() == 0 or optional_lse.numel() >= N * Hq,
+               "optional_lse too small")
+        R, M = int(query_cache.shape[0]), int(query_cache.shape[1])
+        _check(query_cache.shape[2] == Hq and query_cache.shape[3] == D,
+               "query_cache shape mismatch")
+        _check(tuple(attn_cache.shape) == tuple(query_cache.shape), "attn_cache shape mismatch")
+        _check(tuple(lse_cache.shape) == (R, M, Hq), "lse_cache shape mismatch")
+        max_match_tiles = int(match_dist.shape[2])
+        mtc = int(partial_rect_lse.shape[2])
+        mtr = int(partial_rect_reduced_lse.shape[2])
+        mtt = int(partial_tail_lse.shape[2])
+        tile_tokens = int(tile_tokens)
+        match_tile_slots = int(match_tile_slots)
+        _check(tile_tokens > 0 and match_tile_slots > 0, "tile sizes must be positive")
+        _check(max_match_tiles >= (M + match_tile_slots - 1) // match_tile_slots,
+               "match workspace too small")
+        _check(mtc >= (int(max_context) + tile_tokens - 1) // tile_tokens,
+               "rect workspace too small")
+        _check(mtr >= (int(max_context) + tile_tokens * 32 - 1) // (tile_tokens * 32),
+               "reduced rect workspace too small")
+        _check(mtt >= (int(semantic_pos_ahead) + tile_tokens - 1) // tile_tokens,
+               "tail workspace too small")
+        for name, t, tiles in (("rect output", partial_rect_o, mtc),
+                               ("reduced rect output", partial_rect_reduced_o, mtr),
+                               ("tail output", partial_tail_o, mtt)):
+            _check(t.shape[0] >= N and t.shape[1] == Hkv and t.shape[2] == tiles
+                   and t.shape[3] == G and t.shape[4] == D, f"{name} workspace has wrong shape")
+        for name, t, tiles in (("rect lse", partial_rect_lse, mtc),
+                               ("reduced rect lse", partial_rect_reduced_lse, mtr),
+                               ("tail lse", partial_tail_lse, mtt)):
+            _check(t.shape[0] >= N and t.shape[1] == Hkv and t.shape[2] == tiles
+                   and t.shape[3] == G, f"{name} workspace has wrong shape")
+        _check(group_mode.shape[0] >= N and group_mode.shape[1] >= Hkv,
+               "group_mode workspace too small")
+        _check(complete_task_tile.numel() == complete_task_go.numel(),
+               "complete task shape mismatch")
+        _check(tail_task_tile.numel() == tail_task_go.numel(), "tail task shape mismatch")
+        _check(hit_tail_task_tile.numel() == hit_tail_task_ho.numel(),
+               "hit tail task shape mismatch")
+        _check(task_counts.numel() >= 9, "task_counts must have at least nine elements")
+        _check(int(bench_mode) in (0, 1, 2), "unsupported synthetic MAC bench mode")
+        _check(complete_task_go.numel() >= N * Hq * mtc, "complete task workspace too small")
+        _check(tail_task_go.numel() >= N * Hkv * mtt, "tail task workspace too small")
+        _check(hit_tail_task_ho.numel() >= N * Hq * mtt, "hit tail task workspace too small")
+        ws_rows = min(int(t.shape[0]) for t in (
+            head_hit, head_match_slot, head_match_pos, head_prefix_end, head_rect_start,
+            head_new_end, group_rect_begin, group_rect_end, group_rect_tiles, group_tail_begin,
+            group_tail_end, group_tail_tiles, group_mode, match_dist, match_pos, match_slot))
+        for t in (head_hit, head_match_slot, head_match_pos, head_prefix_end, head_rect_start,
+                  head_new_end, match_dist, match_pos, match_slot):
+            _check(t.shape[1] == Hq, "head workspace must have Hq columns")
+        for t in (group_rect_begin, group_rect_end, group_rect_tiles, group_tail_begin,
+                  group_tail_end, group_tail_tiles, group_mode):
+            _check(t.shape[1] == Hkv, "group workspace must have Hkv columns")
+        _check(ws_rows >= N, "head/group workspace has fewer rows than the batch")
+
+        ready = epoch = req_epoch = None
+        if mac_cache_ready is not None and mac_cache_ready.numel() > 0:
+            _check(mac_cache_ready.is_cuda, "mac_cache_ready must be CUDA")
+            _check(mac_cache_ready.is_contiguous(), "mac_cache_ready must be contiguous")
+            _check(mac_cache_ready.dtype in (torch.bool, torch.uint8),
+                   "mac_cache_ready must be bool or uint8")
+            _check(mac_cache_ready.numel() >= R, "mac_cache_ready must cover every request slot")
+            ready = mac_cache_ready
+            if (mac_cache_epoch is not None and mac_cache_epoch.numel() > 0
+                    and mac_request_epoch is not None and mac_request_epoch.numel() > 0):
+                _check_tensor(mac_cache_epoch, "mac_cache_epoch", i64, 1)
+                _check_tensor(mac_request_epoch, "mac_request_epoch", i64, 1)
+                _check(mac_cache_epoch.numel() >= R and mac_request_epoch.numel() >= R,
+                       "epoch tensors must cover every request slot")
+                epoch, req_epoch = mac_cache_epoch, mac_request_epoch
+
+        a = MacDecodeArgs()
+        a.struct_size = ctypes.sizeof(MacDecodeArgs)
+        a.abi_version = ABI_VERSION
+        for name, t in (("q_post", q_post), ("q_pre", q_pre), ("k_buffer", k_buffer),
+                        ("v_buffer", v_buffer), ("req_to_token", req_to_token),
+                        ("req_ids", req_ids), ("past_lens", past_lens),
+                        ("out_cache_loc", out_cache_loc), ("query_cache", query_cache),
+                        ("attn_cache", attn_cache), ("lse_cache", lse_cache), ("out", out),
+                        ("out_lse", optional_lse), ("match_dist", match_dist),
+                        ("match_pos", match_pos), ("match_slot", match_slot),
+                        ("head_hit", head_hit), ("head_match_slot", head_match_slot),
+                        ("head_match_pos", head_match_pos), ("head_prefix_end", head_prefix_end),
+                        ("head_rect_start", head_rect_start), ("head_new_end", head_new_end),
+                        ("group_rect_begin", group_rect_begin), ("group_rect_end", group_rect_end),
+                        ("group_rect_tiles", group_rect_tiles),
+                        ("group_tail_begin", group_tail_begin), ("group_tail_end", group_tail_end),
+                        ("group_tail_tiles", group_tail_tiles), ("group_mode", group_mode),
+                        ("complete_task_go", complete_task_go),
+                        ("complete_task_tile", complete_task_tile), ("task_counts", task_counts),
+                        ("partial_o", partial_rect_o), ("partial_lse", partial_rect_lse),
+                        ("cache_ready", ready), ("cache_epoch", epoch),
+                        ("request_epoch", req_epoch)):
+            setattr(a, name, _ptr(t))
+        a.N, a.Hq, a.Hkv, a.D, a.M, a.R = N, Hq, Hkv, D, M, R
+        a.pool_tokens = int(k_buffer.shape[0])
+        a.req_to_token_rows = int(req_to_token.shape[0])
+        a.req_to_token_stride = int(req_to_token.shape[1])
+        a.out_cache_loc_is_i64 = 1 if out_cache_loc.dtype == i64 else 0
+        a.max_match_tiles = max_match_tiles
+        a.max_tiles_context = mtc
+        a.partial_o_is_bf16 = 1 if partial_rect_o.dtype == bf16 else 0
+        a.complete_task_len = int(complete_task_go.numel())
+        a.workspace_rows = ws_rows
+        a.max_context = int(max_context)
+        a.tile_tokens = tile_tokens
+        a.match_tile_slots = match_tile_slots
+        a.semantic_pos_ahead = int(semantic_pos_ahead)
+        a.front_sink_tokens = int(front_sink_tokens)
+        a.gen_min_limit = int(gen_min_limit)
+        a.lookback_right = int(lookback_right)
+        a.candidate_mode = int(candidate_mode)
+        a.threshold = float(threshold)
+        a.sm_scale = float(sm_scale)
+        a.debug_enabled = int(debug_enabled)
+        a.bench_mode = int(bench_mode)
+        a.bench_hit_rate = float(bench_hit_rate)
+        a.bench_hit_rate_std = float(bench_hit_rate_std)
+        a.bench_skip_ratio = float(bench_skip_ratio)
+        a.bench_skip_ratio_std = float(bench_skip_ratio_std)
+        a.bench_match_lag_mean = float(bench_match_lag_mean)
+        a.bench_match_lag_std = float(bench_match_lag_std)
+        a.bench_seed = int(bench_seed)
+        a.bench_miss_mask = int(bench_miss_mask)
+        a.bench_layer_id = int(bench_layer_id)
+        a.mixed_group_fallback = _env_flag("MAC_PERSISTENT_MIXED_GROUP_FALLBACK", 1)
+        a.bench_exact_quota = _env_flag("MAC_BENCH_EXACT_QUOTA", 1)
+        with torch.cuda.device(q_post.device):
+            rc = self._lib.mac_persistent_decode_bf16(ctypes.byref(a), _stream(q_post.device))
+        _raise_on(self._lib, rc)
+
+
+class PrefillUpdateCacheExtension:
+    """Object returned by :func:`load_mac_prefill_update_cache_extension`
+    (reference: mac_prefill_update_cache.cu:324-512)."""
+
+    def __init__(self, lib: ctypes.CDLL):
+        self._lib = lib
+
+    def mac_prefill_update_cache(self, q_cache, attn_cache, lse_cache, request_length, req_ids,
+                                 src_q, src_attn, src_lse, offsets, lens, capacity, num_heads,
+                                 head_dim, q_post_cache) -> None:
+        capacity, num_heads, head_dim = int(capacity), int(num_heads), int(head_dim)
+        if capacity <= 0 or req_ids.shape[0] == 0:
+            return
+        for name, t, dt in (("q_cache", q_cache, torch.bfloat16),
+                            ("attn_cache", attn_cache, torch.bfloat16),
+                            ("lse_cache", lse_cache, torch.float32),
+                            ("request_length", request_length, torch.int32),
+                            ("req_ids", req_ids, torch.int32), ("lens", lens, torch.int32),
+                            ("offsets", offsets, torch.int32), ("src_q", src_q, torch.bfloat16),
+                            ("src_attn", src_attn, torch.bfloat16),
+                            ("src_lse", src_lse, torch.float32)):
+            _check(t.is_cuda, f"{name} must be a CUDA tensor")
+            _check(t.is_contiguous(), f"{name} must be contiguous")
+            _check(t.dtype == dt, f"{name} has wrong dtype")
+        R = int(q_cache.shape[0])
+        _check(R > 0, "R must be > 0")
+        _check(q_cache.dim() == 4, "q_cache must be [R,M,H,D]")
+        _check(q_cache.shape[1] == capacity, "capacity (M) mismatch")
+        _check(q_cache.shape[2] == num_heads, "num_heads (H) mismatch")
+        _check(q_cache.shape[3] == head_dim, "head_dim (D) mismatch")
+        _check(tuple(attn_cache.shape) == tuple(q_cache.shape), "attn_cache must match q_cache")
+        _check(lse_cache.dim() == 3 and lse_cache.shape[0] == R and lse_cache.shape[1] == capacity
+               and lse_cache.shape[2] == num_heads, "lse_cache shape mismatch")
+        _check(src_q.dim() == 3 and src_q.shape[1] == num_heads and src_q.shape[2] == head_dim,
+               "src_q must be [sumN,H,D]")
+        _check(tuple(src_attn.shape) == tuple(src_q.shape), "src_attn must match src_q")
+        _check(src_lse.dim() == 2 and src_lse.shape[1] == num_heads, "src_lse must be [sumN,H]")
+        _check(src_lse.shape[0] == src_q.shape[0], "src_lse row count must match src_q")
+        B = int(req_ids.shape[0])
+        _check(offsets.shape[0] == B + 1, "offsets must be [B+1]")
+        _check(lens.shape[0] == B, "lens must be [B]")
+        _check(request_length.shape[0] in (R, B), "request_length must be [R] or [B]")
+        qpc = None
+        if q_post_cache is not None and q_post_cache.numel() > 0:
+            _check(q_post_cache.is_cuda, "q_post_cache must be a CUDA tensor")
+            _check(q_post_cache.is_contiguous(), "q_post_cache must be contiguous")
+            _check(q_post_cache.dtype == torch.bfloat16, "q_post_cache has wrong dtype")
+            _check(tuple(q_post_cache.shape) == tuple(q_cache.shape),
+                   "q_post_cache must match q_cache")
+            qpc = q_post_cache
+        with torch.cuda.device(q_cache.device):
+            rc = self._lib.mac_prefill_update_cache(
+                _ptr(q_cache), _ptr(attn_cache), _ptr(lse_cache), _ptr(request_length),
+                int(request_length.shape[0]), _ptr(req_ids), B, _ptr(src_q), _ptr(src_attn),
+                _ptr(src_lse), int(src_q.shape[0]), _ptr(offsets), _ptr(lens), R, capacity,
+                num_heads, head_dim, _ptr(qpc), _stream(q_cache.device))
+        _raise_on(self._lib, rc)
+
+    def _ready_common(self, ready, cache_epoch, request_epoch, req_ids):
+        _check(ready.is_cuda, "ready must be a CUDA tensor")
+        _check(ready.is_contiguous(), "ready must be contiguous")
+        _check(ready.dtype == torch.bool, "ready has wrong dtype")
+        for name, t, dt in (("cache_epoch", cache_epoch, torch.int64),
+                            ("request_epoch", request_epoch, torch.int64),
+                            ("req_ids", req_ids, torch.int32)):
+            _check(t.is_cuda, f"{name} must be a CUDA tensor")
+            _check(t.is_contiguous(), f"{name} must be contiguous")
+            _check(t.dtype == dt, f"{name} has wrong dtype")
+        _check(cache_epoch.shape[0] == ready.shape[0], "cache_epoch must match ready")
+        _check(request_epoch.shape[0] == ready.shape[0], "request_epoch must match ready")
+
+    def mac_mark_persistent_ready(self, ready, cache_epoch, request_epoch, req_ids) -> None:
+        if req_ids.shape[0] == 0:
+            return
+        self._ready_common(ready, cache_epoch, request_epoch, req_ids)
+        with torch.cuda.device(ready.device):
+            rc = self._lib.mac_mark_persistent_ready(
+                _ptr(ready), _ptr(cache_epoch), _ptr(request_epoch), _ptr(req_ids),
+                int(req_ids.shape[0]), int(ready.shape[0]), _stream(ready.device))
+        _raise_on(self._lib, rc)
+
+    def mac_invalidate_persistent_ready(self, ready, cache_epoch, request_epoch, req_ids) -> None:
+        if req_ids.shape[0] == 0:
+            return
+        self._ready_common(ready, cache_epoch, request_epoch, req_ids)
+        with torch.cuda.device(ready.device):
+            rc = self._lib.mac_invalidate_persistent_ready(
+                _ptr(ready), _ptr(cache_epoch), _ptr(request_epoch), _ptr(req_ids),
+                int(req_ids.shape[0]), int(ready.shape[0]), _stream(ready.device))
+        _raise_on(self._lib, rc)
+
+    def mac_update_request_state(self, req_len, match_req_len, cache_lens, req_ids, seq_lens,
+                                 cur_lens) -> None:
+        if req_ids.shape[0] == 0:
+            return
+        for name, t in (("req_len", req_len), ("match_req_len", match_req_len),
+                        ("cache_lens", cache_lens), ("req_ids", req_ids), ("seq_lens", seq_lens),
+                        ("cur_lens", cur_lens)):
+            _check(t.is_cuda, f"{name} must be a CUDA tensor")
+            _check(t.is_contiguous(), f"{name} must be contiguous")
+            _check(t.dtype == torch.int32, f"{name} has wrong dtype")
+        B = int(req_ids.shape[0])
+        _check(match_req_len.shape[0] == req_len.shape[0], "match_req_len must match req_len")
+        _check(seq_lens.shape[0] >= B, "seq_lens is shorter than req_ids")
+        _check(cur_lens.shape[0] >= B, "cur_lens is shorter than req_ids")
+        _check(cache_lens.shape[0] >= B, "cache_lens is shorter than req_ids")
+        with torch.cuda.device(req_len.device):
+            rc = self._lib.mac_update_request_state(
+                _ptr(req_len), _ptr(match_req_len), _ptr(cache_lens), _ptr(req_ids),
+                _ptr(seq_lens), _ptr(cur_lens), B, int(req_len.shape[0]), _stream(req_len.device))
+        _raise_on(self._lib, rc)
+
+
+@lru_cache(maxsize=4)
+def load_mac_persistent_decode_extension(verbose: bool = False, fast_math: bool | None = None) -> Any:
+    """Reference bridge.py:211-269.  The kernels are prebuilt for gfx950, so
+    ``verbose`` and ``fast_math`` have nothing to select; they are accepted for
+    call compatibility."""
+    return PersistentDecodeExtension(load_library())
+
+
+@lru_cache(maxsize=1)
+def load_mac_prefill_update_cache_extension(verbose: bool = False) -> Any:
+    """Reference bridge.py:172-187."""
+    return PrefillUpdateCacheExtension(load_library())

@@ -1,0 +1,182 @@
+"""GPU parity of the fused MAC decode step, through the reference's 68-argument
+binding (which calls the C ABI of libmac_hip.so).
+
+Expected values: the reference's known-answer recipe (kat_cases) and the CPU
+oracle on identical inputs.  Integer decisions must match the oracle exactly;
+values within the reference's tolerances and 1e-2 relative L2.
+"""
+
+import numpy as np
+import pytest
+
+import kat_cases
+from helpers import assert_close, bits, oracle_run, rel_l2, syn
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ext():
+    from mac_attention.integrations.sglang.bridge import load_mac_persistent_decode_extension
+
+    return load_mac_persistent_decode_extension(False)
+
+
+def _np(t):
+    if t.dtype == torch.bfloat16:
+        return t.float().cpu().numpy()
+    return t.cpu().numpy()
+
+
+def _check_against_oracle(case, dev, out, out_lse, ws, res, tol=1e-2, what=""):
+    n_req = case.q_post.shape[0]
+    np.testing.assert_array_equal(_np(ws[3])[:n_req], res.head["hit"], err_msg=f"{what} head_hit")
+    np.testing.assert_array_equal(_np(ws[5])[:n_req], res.head["match_pos"], err_msg=f"{what} match_pos")
+    np.testing.assert_array_equal(_np(ws[4])[:n_req], res.head["match_slot"], err_msg=f"{what} match_slot")
+    np.testing.assert_array_equal(_np(ws[7])[:n_req], res.head["rect_start"], err_msg=f"{what} rect_start")
+    np.testing.assert_array_equal(_np(ws[15])[:n_req], res.group["mode"], err_msg=f"{what} group_mode")
+    np.testing.assert_array_equal(_np(ws[9])[:n_req], res.group["rect_begin"], err_msg=f"{what} rect_begin")
+    got = _np(out)
+    exp = bits(res.out)
+    assert rel_l2(got, exp) < tol, f"{what} out rel_l2 {rel_l2(got, exp)}"
+    assert_close(got, exp, 3e-2, f"{what} out")
+    assert_close(_np(out_lse), res.out_lse, 3e-2, f"{what} out_lse")
+    qc, ac, lc = _np(dev["query_cache"]), _np(dev["attn_cache"]), _np(dev["lse_cache"])
+    np.testing.assert_array_equal(syn.to_bits(qc), res.query_cache, err_msg=f"{what} query_cache")
+    assert rel_l2(ac, bits(res.attn_cache)) < tol, f"{what} attn_cache"
+    assert_close(ac, bits(res.attn_cache), 3e-2, f"{what} attn_cache")
+    assert_close(lc, res.lse_cache, 3e-2, f"{what} lse_cache")
+
+
+@pytest.mark.parametrize("partial", ["f32", "bf16"])
+@pytest.mark.parametrize("builder", kat_cases.ALL, ids=lambda f: f.__name__)
+def test_reference_kat(builder, partial, ext, monkeypatch):
+    kat = builder()
+    for k, v in kat.env.items():
+        monkeypatch.setenv(k, v)
+    print(f"case={kat.name} partial={partial}", flush=True)
+    c = kat.case
+    res = oracle_run(c)
+    dev = syn.to_device(torch, c)
+    pdt = torch.float32 if partial == "f32" else torch.bfloat16
+    out, out_lse, ws = syn.run_decode(torch, ext, dev, c, max_context=kat.max_context,
+                                      tile_tokens=kat.tile_tokens,
+                                      match_tile_slots=kat.match_tile_slots, partial_dtype=pdt)
+    torch.cuda.synchronize()
+    if kat.head_hit is not None:
+        np.testing.assert_array_equal(_np(ws[3]), kat.head_hit)
+    if kat.head_match_pos is not None:
+        np.testing.assert_array_equal(_np(ws[5]), kat.head_match_pos)
+    if kat.group_mode is not None:
+        np.testing.assert_array_equal(_np(ws[15]), kat.group_mode)
+    if kat.min_reduce_groups:
+        assert int(_np(ws[22])[3]) >= kat.min_reduce_groups
+    m = c.query_cache.shape[1]
+    o = _np(out)
+    for n, (eo, el) in kat.exp_out.items():
+        assert_close(o[n], eo, kat.o_tol, f"{kat.name} out[{n}]")
+        assert_close(_np(out_lse)[n], el, kat.lse_tol, f"{kat.name} out_lse[{n}]")
+    ac, lc, qc = _np(dev["attn_cache"]), _np(dev["lse_cache"]), _np(dev["query_cache"])
+    for n, (ro, rl) in kat.exp_ring.items():
+        dest = int(c.past_lens[n]) % m
+        assert_close(ac[n, dest], ro, kat.o_tol, f"{kat.name} ring o[{n}]")
+        assert_close(lc[n, dest], rl, kat.lse_tol, f"{kat.name} ring lse[{n}]")
+    if kat.ring_exact_empty:
+        dest = int(c.past_lens[0]) % m
+        np.testing.assert_array_equal(qc[0, dest], c.q_pre[0])
+        assert np.all(ac[0, dest] == 0)
+        assert np.all(np.isneginf(lc[0, dest]))
+    _check_against_oracle(c, dev, out, out_lse, ws, res, tol=1e-2 if partial == "f32" else 2e-2,
+                          what=kat.name)
+
+
+def test_two_step_recurrence(ext, monkeypatch):
+    monkeypatch.setenv("MAC_PERSISTENT_MIXED_GROUP_FALLBACK", "1")
+    r = kat_cases.recurrence_inputs()
+    c1 = r["step1"]
+    dev = syn.to_device(torch, c1)
+    syn.run_decode(torch, ext, dev, c1, max_context=32)
+    torch.cuda.synchronize()
+    qc, ac, lc = _np(dev["query_cache"]), _np(dev["attn_cache"]), _np(dev["lse_cache"])
+    d1 = r["dest1"]
+    for h in range(r["hq"]):
+        exp = r["e_hit"][0][h] if h in r["hit_heads"] else r["e_miss"][0][h]
+        assert rel_l2(ac[0, d1, h], exp) < 0.08
+    c2 = r["step2"](qc, ac, lc)
+    dev2 = syn.to_device(torch, c2)
+    out2, _, ws2 = syn.run_decode(torch, ext, dev2, c2, max_context=32)
+    torch.cuda.synchronize()
+    assert _np(ws2[3])[0].tolist() == [1] * r["hq"]
+    assert _np(ws2[5])[0].tolist() == [r["p1"]] * r["hq"]
+    hit = np.array([h in r["hit_heads"] for h in range(r["hq"])])
+    base_o = np.where(hit[:, None], r["e_hit"][0], r["e_miss"][0])
+    base_l = np.where(hit, r["e_hit"][1], r["e_miss"][1])
+    ref_o, _ = r["expected_step2"](base_o, base_l)
+    assert rel_l2(_np(out2)[0], ref_o) < 0.08
+
+
+RANDOM_CASES = [
+    # (batch, hq, hkv, kv_lens, M, S, F, hit_rate, seed)
+    (3, 32, 8, [300, 517, 1024], 32, 64, 0, 0.5, 10),
+    (2, 32, 4, [777, 2049], 16, 128, 16, 0.75, 11),
+    (4, 8, 8, [65, 130, 260, 1000], 8, 16, 4, 0.5, 12),
+    (2, 16, 2, [5000, 1234], 32, 256, 64, 0.9, 13),
+    (3, 12, 4, [40, 41, 300], 64, 8, 0, 0.3, 14),
+    (2, 6, 1, [200, 300], 16, 32, 8, 0.6, 15),
+    (1, 32, 8, [4097], 16, 256, 0, 1.0, 16),
+    (2, 32, 8, [3000, 3001], 32, 256, 128, 0.0, 17),
+]
+
+
+@pytest.mark.parametrize("cfg", RANDOM_CASES, ids=lambda c: f"B{c[0]}_Hq{c[1]}_Hkv{c[2]}_seed{c[-1]}")
+def test_random_vs_oracle(cfg, ext):
+    b, hq, hkv, kv_lens, m, s, f, hit_rate, seed = cfg
+    print(f"random case {cfg}", flush=True)
+    c = syn.random_case(batch=b, hq=hq, hkv=hkv, kv_lens=kv_lens, capacity=m, semantic_pos_ahead=s,
+                        front_sink_tokens=f, hit_rate=hit_rate, match_lag=m // 2, seed=seed)
+    res = oracle_run(c)
+    dev = syn.to_device(torch, c, out_cache_loc_dtype=torch.int32 if seed % 2 else torch.int64)
+    out, out_lse, ws = syn.run_decode(torch, ext, dev, c, max_context=max(kv_lens) + 8,
+                                      tile_tokens=16, match_tile_slots=8)
+    torch.cuda.synchronize()
+    _check_against_oracle(c, dev, out, out_lse, ws, res, what=str(cfg))
+
+
+def test_readiness_gate(ext):
+    """Not-ready and epoch-mismatched requests run exact attention and leave
+    their ring rows untouched (DECODE:208-230, :4487-4497)."""
+    c = syn.random_case(batch=4, hq=32, hkv=8, kv_lens=[500, 600, 700, 800], capacity=16,
+                        semantic_pos_ahead=64, front_sink_tokens=8, hit_rate=1.0, match_lag=8,
+                        seed=21)
+    c.cache_ready = np.array([1, 0, 1, 1], np.uint8)
+    c.cache_epoch = np.array([3, 3, 2, 5], np.int64)
+    c.request_epoch = np.array([3, 3, 7, 5], np.int64)
+    res = oracle_run(c)
+    assert res.head["hit"][1].sum() == 0 and res.head["hit"][2].sum() == 0
+    assert res.head["hit"][0].sum() == 32 and res.head["hit"][3].sum() == 32
+    dev = syn.to_device(torch, c)
+    before = _np(dev["attn_cache"]).copy()
+    out, out_lse, ws = syn.run_decode(torch, ext, dev, c, max_context=1024, tile_tokens=32)
+    torch.cuda.synchronize()
+    _check_against_oracle(c, dev, out, out_lse, ws, res, what="ready gate")
+    after = _np(dev["attn_cache"])
+    np.testing.assert_array_equal(after[1], before[1])
+    np.testing.assert_array_equal(after[2], before[2])
+
+
+@pytest.mark.parametrize("bench_mode", [1, 2])
+def test_bench_mode_override(bench_mode, ext):
+    """Synthetic bench override (DECODE:1184-1269) gives the oracle's decisions."""
+    c = syn.random_case(batch=3, hq=32, hkv=8, kv_lens=[1000, 1100, 1200], capacity=32,
+                        semantic_pos_ahead=64, hit_rate=0.0, seed=31, entry_builder="random")
+    c.lse_cache[:] = 0.0  # every slot holds a finite entry, as in the reference's bench case
+    bench = dict(bench_mode=bench_mode, bench_hit_rate=0.7, bench_match_lag_mean=16.0, bench_seed=5)
+    res = oracle_run(c, bench_mode=bench_mode, bench_hit_rate=0.7, bench_match_lag_mean=16.0,
+                     bench_seed=5)
+    dev = syn.to_device(torch, c)
+    out, out_lse, ws = syn.run_decode(torch, ext, dev, c, max_context=1300, tile_tokens=32,
+                                      bench=bench)
+    torch.cuda.synchronize()
+    _check_against_oracle(c, dev, out, out_lse, ws, res, what=f"bench{bench_mode}")
