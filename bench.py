@@ -1,0 +1,325 @@
+#!/usr/bin/env python3
+"""Benchmark of the MAC decode step on one MI355X.
+
+Headline workload: GQA-4 (Hq=32, Hkv=8), D=128,
+batch 64, past_len 130048 (kv_len 130049) per request, ring of 32 cached
+queries, semantic_pos_ahead 256, front sink 0, threshold 0.45, hit decisions
+from the reference's synthetic_head exact-quota override (bench_mode=1,
+mac_decode_persistent.cu:1184-1269) at hit ratio 0.8.  A step is one
+graph-replayed decode step of one layer (match scan, scheduling, span
+attention, merge and ring write).
+
+Prints ONE JSON line (see the repository's bench contract): value = µs per
+decode step (lower is better), plus
+  roofline      -- the dominant kernel (span_attention): algorithmic bytes per
+                   launch / its average duration from HIP events on its stream;
+  step_roofline -- all algorithmic bytes of the step / graph-replayed step time;
+  cpu_baseline  -- the CPU oracle (oracle/mac_oracle.c, one thread) timed on a
+                   bounded sample of the same workload, scaled to µs per step;
+  sweep         -- µs/step and achieved GB/s across hit ratios for GQA-4 and
+                   GQA-8, and the same kernel forced to exact attention through
+                   the readiness gate (the hit-0 path).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(REPO, "mac-attention_amd"), REPO):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "µs per decode step & HBM GB/s vs hit ratio, GQA-4/8, B=64, 127K ctx"
+HBM_PEAK_GBS = 8000.0
+D = 128
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--ctx", type=int, default=130048)
+    ap.add_argument("--hq", type=int, default=32)
+    ap.add_argument("--hkv", type=int, default=8)
+    ap.add_argument("--ring", type=int, default=32)
+    ap.add_argument("--semantic-pos-ahead", type=int, default=256)
+    ap.add_argument("--front-sink", type=int, default=0)
+    ap.add_argument("--hit", type=float, default=0.8)
+    ap.add_argument("--max-context", type=int, default=131072)
+    ap.add_argument("--tile-tokens", type=int, default=32)
+    ap.add_argument("--sweep", choices=["none", "short", "full"], default="short")
+    ap.add_argument("--sweep-replays", type=int, default=30)
+    ap.add_argument("--cpu-requests", type=int, default=48)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--phase-runs", type=int, default=5)
+    ap.add_argument("--json-out", default=None)
+    return ap.parse_args()
+
+
+class Step:
+    """One decode-step configuration bound to device tensors."""
+
+    def __init__(self, torch, ext, dev, *, args, hkv, ring, hit, exact, bench_mode=1):
+        from mac_attention import synthetic as syn
+
+        self.torch, self.ext, self.dev = torch, ext, dev
+        self.batch, self.hq, _ = dev["q_post"].shape
+        self.hkv, self.ring, self.hit, self.exact = hkv, ring, hit, exact
+        self.S, self.F = args.semantic_pos_ahead, args.front_sink
+        self.max_context, self.tile = args.max_context, args.tile_tokens
+        self.bench_mode = bench_mode
+        self.ws = syn.workspace(torch, batch=self.batch, hq=self.hq, hkv=hkv, capacity=ring,
+                                max_context=args.max_context, tile_tokens=args.tile_tokens,
+                                match_tile_slots=32, semantic_pos_ahead=self.S,
+                                front_sink_tokens=self.F, partial_dtype=torch.float32,
+                                device=dev["q_post"].device)
+        self.out = torch.empty_like(dev["q_post"])
+        self.out_lse = torch.empty(self.batch, self.hq, device=dev["q_post"].device)
+        if exact:
+            # every request fails the readiness gate -> exact attention, no ring writes
+            self.ready = torch.zeros(self.batch, dtype=torch.bool, device=dev["q_post"].device)
+        else:
+            self.ready = torch.empty(0, device=dev["q_post"].device)
+
+    def args(self):
+        d = self.dev
+        e = self.torch.empty(0, device=d["q_post"].device)
+        return (
+            d["q_post"], d["q_pre"], d["k"], d["v"], d["req_to_token"], d["req_ids"],
+            d["past_lens"], d["out_cache_loc"], d["query_cache"], d["attn_cache"],
+            d["lse_cache"], self.out, self.out_lse, *self.ws,
+            self.max_context, self.tile, 32, self.S, self.F, 0, 0, 0, 0.45, 1.0 / math.sqrt(D),
+            0, self.bench_mode, self.hit, 0.0, -1.0, 0.0, 64.0, 0.0, 1, -1, 0,
+            d["query_cache"], self.ready, e, e,
+        )
+
+    def launch(self):
+        self.ext.mac_persistent_decode_bf16(*self.args())
+
+    def phase_ms(self, runs):
+        acc = [0.0, 0.0, 0.0]
+        for _ in range(runs):
+            t = self.ext.phase_times_ms(*self.args())
+            acc = [a + b for a, b in zip(acc, t)]
+        return [a / runs for a in acc]
+
+    def bytes(self):
+        """Algorithmic HBM bytes of one step from the decisions it made."""
+        import numpy as np
+
+        ws = self.ws
+        mode = ws[15].cpu().numpy()[: self.batch]
+        rb = ws[9].cpu().numpy()[: self.batch].astype(np.int64)
+        ne = ws[10].cpu().numpy()[: self.batch].astype(np.int64)
+        kvl = ws[13].cpu().numpy()[: self.batch].astype(np.int64)
+        hit = ws[3].cpu().numpy()[: self.batch]
+        past = self.dev["past_lens"].cpu().numpy()[: self.batch].astype(np.int64)
+        sink = np.minimum(self.F, ne)
+        tokens = sink + (ne - rb) + (kvl - ne)  # per group
+        kv = int(tokens.sum()) * 2 * 2 * D
+        r2t = int(tokens.max(axis=1).sum()) * 4
+        ready = not self.exact
+        scan = int(self.hq * np.minimum(self.ring, past).sum()) * 2 * D if ready else 0
+        cached = int(hit.sum()) * (2 * D + 4)
+        heads = self.batch * self.hq
+        small = heads * (2 * D + 2 * D + 2 * D + 4) + (heads * (2 * D + 2 * D + 2 * D + 4) if ready else 0)
+        attn = kv + r2t + heads * 2 * D
+        return dict(total=kv + r2t + scan + cached + small, attention_kernel=attn, kv=kv,
+                    ring_scan=scan, hit_heads=int(hit.sum()), heads=heads,
+                    nonhit_groups=int((mode != 0).sum()), groups=int(mode.size))
+
+
+def time_graph(torch, step: Step, warmup: int, steps: int):
+    """Capture one decode step into a graph, replay `warmup` untimed, then time
+    exactly `steps` replays with events (and the host clock) around them."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            step.launch()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step.launch()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    ms = start.elapsed_time(end) / steps
+    del graph
+    return ms, wall
+
+
+def measure(torch, step: Step, warmup, steps, phase_runs):
+    ms, wall = time_graph(torch, step, warmup, steps)
+    phases = step.phase_ms(phase_runs)
+    b = step.bytes()
+    return dict(
+        hit_ratio=step.hit, gqa=step.hq // step.hkv, ring=step.ring, exact=step.exact,
+        us_per_step=round(ms * 1e3, 2), wall_us_per_step=round(wall * 1e3, 2),
+        phase_us=[round(p * 1e3, 2) for p in phases],
+        algorithmic_bytes=b["total"], attention_kernel_bytes=b["attention_kernel"],
+        achieved_gbs=round(b["total"] / (ms * 1e-3) / 1e9, 1),
+        frac_of_peak=round(b["total"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        attention_kernel_gbs=round(b["attention_kernel"] / (phases[1] * 1e-3) / 1e9, 1),
+        head_hit_ratio=round(b["hit_heads"] / b["heads"], 4),
+        group_all_hit_fraction=round(1 - b["nonhit_groups"] / b["groups"], 4),
+        nonhit_groups=b["nonhit_groups"],
+    )
+
+
+def cpu_baseline(args, hit):
+    """Times the CPU oracle on `cpu_requests` requests of the headline shape."""
+    import numpy as np
+
+    from mac_attention import synthetic as syn
+    from oracle import oracle as orc
+
+    nreq = max(1, args.cpu_requests)
+    # One request's K/V rows are generated and every sampled request reads them
+    # (same req_to_token row), so host memory stays at one request's 0.5 GB
+    # while the oracle does the full per-request work.
+    c = syn.random_case(batch=1, hq=args.hq, hkv=args.hkv, kv_lens=[args.ctx + 1],
+                        capacity=args.ring, semantic_pos_ahead=args.semantic_pos_ahead,
+                        front_sink_tokens=args.front_sink, hit_rate=1.0, seed=7,
+                        entry_builder="random", separate_pre_post=False)
+    rep = lambda a: np.ascontiguousarray(np.repeat(a, nreq, axis=0))  # noqa: E731
+    c.q_post = c.q_pre = rep(c.q_pre)
+    c.req_to_token = rep(c.req_to_token)
+    c.query_cache, c.attn_cache = rep(c.query_cache), rep(c.attn_cache)
+    c.lse_cache = np.zeros((nreq,) + c.lse_cache.shape[1:], np.float32)
+    c.req_ids = np.arange(nreq, dtype=np.int32)
+    c.past_lens = rep(c.past_lens)
+    c.out_cache_loc = rep(c.out_cache_loc)
+    params = orc.DecodeParams(semantic_pos_ahead=c.semantic_pos_ahead,
+                              front_sink_tokens=c.front_sink_tokens, bench_mode=1,
+                              bench_hit_rate=hit, sm_scale=c.sm_scale)
+    inputs = dict(q_post=syn.to_bits(c.q_post), q_pre=syn.to_bits(c.q_pre),
+                  k_buffer=syn.to_bits(c.k), v_buffer=syn.to_bits(c.v),
+                  req_to_token=c.req_to_token, req_ids=c.req_ids, past_lens=c.past_lens,
+                  out_cache_loc=c.out_cache_loc, query_cache=syn.to_bits(c.query_cache),
+                  attn_cache=syn.to_bits(c.attn_cache), lse_cache=c.lse_cache)
+    t0 = time.perf_counter()
+    res = orc.decode(**inputs, params=params)
+    sec = time.perf_counter() - t0
+    us_step = sec * 1e6 * args.batch / nreq
+    return dict(value=round(us_step, 1), unit="us/step", cores=1, kind="port",
+                sample=(f"{nreq} of {args.batch} requests of the headline shape sharing one "
+                        f"request's K/V rows (kv_len "
+                        f"{args.ctx + 1}, Hq {args.hq}, Hkv {args.hkv}, ring {args.ring}, "
+                        f"synthetic_head hit {hit}), {sec:.2f} s single-threaded C oracle, "
+                        f"scaled linearly to {args.batch} requests"),
+                sample_head_hits=int(res.head["hit"].sum()))
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; every GPU box here has one, "
+                                   "so --gpus must be 1 (multi-GPU sharding is design-only)"}))
+        sys.exit(2)
+    import torch
+
+    from mac_attention import synthetic as syn
+    from mac_attention.integrations.sglang.bridge import load_mac_persistent_decode_extension
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    ext = load_mac_persistent_decode_extension(False)
+    log = lambda *a: print(*a, file=sys.stderr, flush=True)  # noqa: E731
+
+    sweep = []
+    headline = None
+    gqa_list = [args.hkv] if args.sweep == "none" else [args.hkv, args.hq // 8]
+    hits = [0.0, 0.25, 0.5, 0.75, 0.8, 0.9, 1.0]
+    for hkv in gqa_list:
+        t0 = time.perf_counter()
+        dev = syn.device_case(torch, batch=args.batch, hq=args.hq, hkv=hkv, ctx=args.ctx,
+                              capacity=args.ring, seed=0)
+        torch.cuda.synchronize()
+        log(f"[bench] GQA-{args.hq // hkv}: inputs ready in {time.perf_counter() - t0:.1f}s")
+        syn.plant_synthetic_hits(torch, dev, hit_rate=args.hit, bench_mode=1,
+                                 semantic_pos_ahead=args.semantic_pos_ahead)
+        if hkv == args.hkv:
+            step = Step(torch, ext, dev, args=args, hkv=hkv, ring=args.ring, hit=args.hit,
+                        exact=False)
+            headline = measure(torch, step, args.warmup, args.steps, args.phase_runs)
+            log(f"[bench] headline {headline}")
+            del step
+        if args.sweep != "none":
+            for exact in (True, False):
+                for h in ([0.0] if exact else hits):
+                    step = Step(torch, ext, dev, args=args, hkv=hkv, ring=args.ring, hit=h,
+                                exact=exact)
+                    r = measure(torch, step, 5, args.sweep_replays, 3)
+                    sweep.append(r)
+                    log(f"[bench] sweep {r}")
+                    del step
+        del dev
+        torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] timing the CPU oracle sample")
+        cpu = cpu_baseline(args, args.hit)
+        log(f"[bench] cpu {cpu}")
+
+    ms = headline["us_per_step"] / 1e3
+    attn_us = headline["phase_us"][1]
+    roof = dict(bound="hbm", achieved=headline["attention_kernel_gbs"], peak=HBM_PEAK_GBS,
+                unit="GB/s", frac=round(headline["attention_kernel_gbs"] / HBM_PEAK_GBS, 4),
+                traffic=None, kernel="span_attention", kernel_us=attn_us,
+                bytes_per_launch=headline["attention_kernel_bytes"])
+    line = {
+        "metric": METRIC,
+        "value": headline["us_per_step"],
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (N(0,1) bf16 K/V/q, randn+10 ring, synthetic_head hit override)",
+        "config": {
+            "workload": (f"MAC decode step, GQA-{args.hq // args.hkv}, B={args.batch}, "
+                         f"ctx={args.ctx}, ring={args.ring}, hit={args.hit}"),
+            "batch": args.batch, "ctx": args.ctx, "hq": args.hq, "hkv": args.hkv, "head_dim": D,
+            "ring": args.ring, "semantic_pos_ahead": args.semantic_pos_ahead,
+            "front_sink": args.front_sink, "hit_ratio": args.hit, "bench_mode": "synthetic_head",
+            "graph": "hipGraph replay",
+        },
+        "step_roofline": dict(achieved=headline["achieved_gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
+                              frac=headline["frac_of_peak"],
+                              bytes_per_step=headline["algorithmic_bytes"]),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "headline": headline,
+        "sweep": sweep,
+    }
+    text = json.dumps(line)
+    if args.json_out:
+        with open(args.json_out, "w") as f:
+            f.write(text + "\n")
+    print(text, flush=True)
+
+
+if __name__ == "__main__":
+    main()

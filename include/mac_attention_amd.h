@@ -194,6 +194,14 @@ MAC_API int mac_update_request_state(int32_t* req_len, int32_t* match_req_len, i
                              const int32_t* req_ids, const int32_t* seq_lens,
                              const int32_t* cur_lens, int32_t B, int32_t R, void* stream);
 
+/* Profiling variant of mac_persistent_decode_bf16: same arguments and effects,
+ * plus HIP events on `stream` around each of the three kernels; synchronises
+ * on the last event and stores the elapsed milliseconds of match_decide,
+ * span_attention and merge_write in ms[0..2].  Not graph-capturable.  No
+ * reference counterpart (the reference stamps clock64() phases into
+ * phase_cycles instead, DECODE:4751-4929). */
+MAC_API int mac_persistent_decode_bf16_timed(const MacDecodeArgs* args, void* stream, float* ms);
+
 /* Message of the last failed call on this thread ("" if none).  No reference
  * counterpart: the reference raises through TORCH_CHECK instead. */
 MAC_API const char* mac_last_error(void);

@@ -976,16 +976,21 @@ int attn_residency(int dev, int G, int* cus, int* per_cu) {
   return MAC_OK;
 }
 
+// ev (optional): four events recorded before, between and after the kernels.
 template <int G>
 int launch_all(const DecideParams& dp, const AttnParams& ap, const MergeParams& mp, int attn_grid,
-               hipStream_t stream) {
+               hipStream_t stream, hipEvent_t* ev) {
   const int NG = dp.s.N * dp.s.Hkv;
+  if (ev) MAC_HIP(hipEventRecord(ev[0], stream));
   hipLaunchKernelGGL(match_decide_kernel<G>, dim3(NG), dim3(kBlock), 0, stream, dp);
   MAC_HIP(hipGetLastError());
+  if (ev) MAC_HIP(hipEventRecord(ev[1], stream));
   hipLaunchKernelGGL(span_attention_kernel<G>, dim3(attn_grid), dim3(kBlock), 0, stream, ap);
   MAC_HIP(hipGetLastError());
+  if (ev) MAC_HIP(hipEventRecord(ev[2], stream));
   hipLaunchKernelGGL(merge_write_kernel<G>, dim3(NG), dim3(kBlock), 0, stream, mp);
   MAC_HIP(hipGetLastError());
+  if (ev) MAC_HIP(hipEventRecord(ev[3], stream));
   return MAC_OK;
 }
 
@@ -996,7 +1001,30 @@ using namespace mac;
 extern "C" const char* mac_last_error(void) { return g_err; }
 extern "C" int mac_abi_version(void) { return MAC_ABI_VERSION; }
 
+namespace mac {
+int decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev);
+}
+
 extern "C" int mac_persistent_decode_bf16(const MacDecodeArgs* a, void* stream_ptr) {
+  return mac::decode_impl(a, stream_ptr, nullptr);
+}
+
+extern "C" int mac_persistent_decode_bf16_timed(const MacDecodeArgs* a, void* stream_ptr, float* ms) {
+  g_err[0] = '\0';
+  MAC_REQUIRE(ms != nullptr, "ms must not be NULL");
+  hipEvent_t ev[4];
+  for (int i = 0; i < 4; ++i) MAC_HIP(hipEventCreate(&ev[i]));
+  int rc = mac::decode_impl(a, stream_ptr, ev);
+  if (rc == MAC_OK) {
+    hipError_t e = hipEventSynchronize(ev[3]);
+    for (int i = 0; i < 3 && e == hipSuccess; ++i) e = hipEventElapsedTime(&ms[i], ev[i], ev[i + 1]);
+    if (e != hipSuccess) rc = fail(MAC_ERR_HIP, "event timing: %s", hipGetErrorString(e));
+  }
+  for (int i = 0; i < 4; ++i) (void)hipEventDestroy(ev[i]);
+  return rc;
+}
+
+int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   g_err[0] = '\0';
   MAC_REQUIRE(a != nullptr, "args must not be NULL");
   MAC_REQUIRE(a->struct_size == sizeof(MacDecodeArgs) && a->abi_version == MAC_ABI_VERSION,
@@ -1171,13 +1199,13 @@ extern "C" int mac_persistent_decode_bf16(const MacDecodeArgs* a, void* stream_p
   if (grid < 1) grid = 1;
 
   switch (G) {
-    case 1: return launch_all<1>(dp, ap, mp, static_cast<int>(grid), stream);
-    case 2: return launch_all<2>(dp, ap, mp, static_cast<int>(grid), stream);
-    case 3: return launch_all<3>(dp, ap, mp, static_cast<int>(grid), stream);
-    case 4: return launch_all<4>(dp, ap, mp, static_cast<int>(grid), stream);
-    case 5: return launch_all<5>(dp, ap, mp, static_cast<int>(grid), stream);
-    case 6: return launch_all<6>(dp, ap, mp, static_cast<int>(grid), stream);
-    case 7: return launch_all<7>(dp, ap, mp, static_cast<int>(grid), stream);
-    default: return launch_all<8>(dp, ap, mp, static_cast<int>(grid), stream);
+    case 1: return launch_all<1>(dp, ap, mp, static_cast<int>(grid), stream, ev);
+    case 2: return launch_all<2>(dp, ap, mp, static_cast<int>(grid), stream, ev);
+    case 3: return launch_all<3>(dp, ap, mp, static_cast<int>(grid), stream, ev);
+    case 4: return launch_all<4>(dp, ap, mp, static_cast<int>(grid), stream, ev);
+    case 5: return launch_all<5>(dp, ap, mp, static_cast<int>(grid), stream, ev);
+    case 6: return launch_all<6>(dp, ap, mp, static_cast<int>(grid), stream, ev);
+    case 7: return launch_all<7>(dp, ap, mp, static_cast<int>(grid), stream, ev);
+    default: return launch_all<8>(dp, ap, mp, static_cast<int>(grid), stream, ev);
   }
 }

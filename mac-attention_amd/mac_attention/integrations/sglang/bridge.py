@@ -72,6 +72,7 @@ class MacDecodeArgs(ctypes.Structure):
 
 EXPORTED_SYMBOLS = (
     "mac_persistent_decode_bf16",
+    "mac_persistent_decode_bf16_timed",
     "mac_prefill_update_cache",
     "mac_mark_persistent_ready",
     "mac_invalidate_persistent_ready",
@@ -95,6 +96,9 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.mac_abi_version.restype = ctypes.c_int
     lib.mac_persistent_decode_bf16.argtypes = [ctypes.POINTER(MacDecodeArgs), _p]
     lib.mac_persistent_decode_bf16.restype = ctypes.c_int
+    lib.mac_persistent_decode_bf16_timed.argtypes = [
+        ctypes.POINTER(MacDecodeArgs), _p, ctypes.POINTER(ctypes.c_float)]
+    lib.mac_persistent_decode_bf16_timed.restype = ctypes.c_int
     lib.mac_prefill_update_cache.argtypes = [
         _p, _p, _p, _p, _i32, _p, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i32, _p, _p,
     ]
@@ -167,7 +171,31 @@ class PersistentDecodeExtension:
     def __init__(self, lib: ctypes.CDLL):
         self._lib = lib
 
-    def mac_persistent_decode_bf16(
+    def mac_persistent_decode_bf16(self, *args) -> None:
+        """One fused MAC decode step (reference: mac_decode_persistent.cu:4962-5524).
+
+        Same 68 positional arguments, same in-place outputs, returns None.
+        ``query_post_cache`` is accepted and ignored, as in the reference
+        (:5045-5049).  ``MAC_PERSISTENT_MIXED_GROUP_FALLBACK`` and
+        ``MAC_BENCH_EXACT_QUOTA`` are read from the environment on every call.
+        """
+        a, device = self._marshal(*args)
+        with torch.cuda.device(device):
+            rc = self._lib.mac_persistent_decode_bf16(ctypes.byref(a), _stream(device))
+        _raise_on(self._lib, rc)
+
+    def phase_times_ms(self, *args) -> tuple[float, float, float]:
+        """Runs the same step eagerly with HIP events around each kernel and
+        returns (match_decide, span_attention, merge_write) milliseconds.
+        Synchronises; profiling only (no reference counterpart)."""
+        a, device = self._marshal(*args)
+        ms = (ctypes.c_float * 3)()
+        with torch.cuda.device(device):
+            rc = self._lib.mac_persistent_decode_bf16_timed(ctypes.byref(a), _stream(device), ms)
+        _raise_on(self._lib, rc)
+        return float(ms[0]), float(ms[1]), float(ms[2])
+
+    def _marshal(
         self,
         q_post, q_pre, k_buffer, v_buffer, req_to_token, req_ids, past_lens, out_cache_loc,
         query_cache, attn_cache, lse_cache, out, optional_lse,
@@ -185,14 +213,9 @@ class PersistentDecodeExtension:
         bench_hit_rate, bench_hit_rate_std, bench_skip_ratio, bench_skip_ratio_std,
         bench_match_lag_mean, bench_match_lag_std, bench_seed, bench_miss_mask, bench_layer_id,
         query_post_cache, mac_cache_ready, mac_cache_epoch, mac_request_epoch,
-    ) -> None:
-        """One fused MAC decode step (reference: mac_decode_persistent.cu:4962-5524).
-
-        Same 68 positional arguments, same in-place outputs, returns None.
-        ``query_post_cache`` is accepted and ignored, as in the reference
-        (:5045-5049).  ``MAC_PERSISTENT_MIXED_GROUP_FALLBACK`` and
-        ``MAC_BENCH_EXACT_QUOTA`` are read from the environment on every call.
-        """
+    ) -> tuple[MacDecodeArgs, torch.device]:
+        """Checks the 68 arguments like the reference launcher
+        (mac_decode_persistent.cu:5031-5175) and fills the C argument block."""
         bf16, f32, i32, i64 = torch.bfloat16, torch.float32, torch.int32, torch.int64
         _check_tensor(q_post, "q_post", bf16, 3)
         _check_tensor(q_pre, "q_pre", bf16, 3)
@@ -385,9 +408,7 @@ class PersistentDecodeExtension:
         a.bench_layer_id = int(bench_layer_id)
         a.mixed_group_fallback = _env_flag("MAC_PERSISTENT_MIXED_GROUP_FALLBACK", 1)
         a.bench_exact_quota = _env_flag("MAC_BENCH_EXACT_QUOTA", 1)
-        with torch.cuda.device(q_post.device):
-            rc = self._lib.mac_persistent_decode_bf16(ctypes.byref(a), _stream(q_post.device))
-        _raise_on(self._lib, rc)
+        return a, q_post.device
 
 
 class PrefillUpdateCacheExtension:

@@ -340,3 +340,75 @@ def run_decode(torch, ext, dev: dict, case: Case, *, max_context, tile_tokens=4,
         dev["query_cache"], dev["cache_ready"], dev["cache_epoch"], dev["request_epoch"],
     )
     return out, out_lse, ws
+
+
+# ------------------------------------------------------ device cases ----
+
+
+def device_case(torch, *, batch: int, hq: int, hkv: int, ctx: int, capacity: int, seed: int = 0,
+                device="cuda", kv=None, chunk_rows: int = 1 << 20):
+    """Benchmark-scale inputs generated on the GPU with the conventions of
+    ``_make_case`` (tools/bench_mac_persistent_decode.py:61-113): every request
+    has past_len = ctx and kv_len = ctx + 1, K/V/q ~ N(0,1) bf16, the ring
+    holds randn + 10 rows with finite lse 0 (hit decisions then come from the
+    synthetic override or from planted copies).  ``kv`` reuses a (k, v) pair
+    of at least batch * (ctx + 1) rows."""
+    kv_len = ctx + 1
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    bf = torch.bfloat16
+    rows = batch * kv_len
+    if kv is None:
+        k = torch.empty(rows, hkv, 128, device=device, dtype=bf)
+        v = torch.empty(rows, hkv, 128, device=device, dtype=bf)
+        for t in (k, v):
+            for i in range(0, rows, chunk_rows):
+                t[i:i + chunk_rows].normal_(generator=g)
+    else:
+        k, v = kv
+        assert k.shape[0] >= rows and k.shape[1] == hkv
+    base = torch.arange(batch, device=device, dtype=torch.int64)[:, None] * kv_len
+    r2t = (base + torch.arange(kv_len, device=device, dtype=torch.int64)[None, :]).to(torch.int32)
+    r2t[:, ctx] = (base[:, 0] + ctx).to(torch.int32)
+    q = torch.randn(batch, hq, 128, device=device, dtype=bf, generator=g)
+    qc = torch.randn(batch, capacity, hq, 128, device=device, dtype=bf, generator=g) + 10
+    return dict(
+        q_post=q, q_pre=q, k=k, v=v, req_to_token=r2t.contiguous(),
+        req_ids=torch.arange(batch, device=device, dtype=torch.int32),
+        past_lens=torch.full((batch,), ctx, device=device, dtype=torch.int32),
+        out_cache_loc=(base[:, 0] + ctx).to(torch.int32),
+        query_cache=qc.contiguous(), attn_cache=torch.zeros_like(qc),
+        lse_cache=torch.zeros(batch, capacity, hq, device=device, dtype=torch.float32),
+        cache_ready=torch.empty(0, device=device), cache_epoch=torch.empty(0, device=device),
+        request_epoch=torch.empty(0, device=device),
+    )
+
+
+def plant_synthetic_hits(torch, dev: dict, *, hit_rate: float, bench_mode: int, semantic_pos_ahead: int,
+                         bench_seed: int = 1, match_lag_mean: float = 64.0):
+    """``apply_synthetic_cache_pattern`` (benchmark/bench_mac_vs_flashinfer_direct.py:214-277):
+    copy each hit head's query into its matched slot.  Returns the number of
+    planted heads."""
+    batch, hq, _ = dev["q_pre"].shape
+    hkv = dev["k"].shape[1]
+    group = hq // hkv
+    cap = dev["query_cache"].shape[1]
+    past = [int(x) for x in dev["past_lens"].cpu().tolist()]
+    ns, hs, ss = [], [], []
+    for n in range(batch):
+        for hq_i in range(hq):
+            hit, slot = synthetic_hit_and_slot(
+                bench_mode=bench_mode, batch=batch, hq=hq, hkv=hkv, past_len=past[n], n=n,
+                hq_i=hq_i, hkv_i=hq_i // group, hit_rate=hit_rate, capacity=cap,
+                semantic_pos_ahead=semantic_pos_ahead, bench_seed=bench_seed,
+                match_lag_mean=match_lag_mean)
+            if hit and slot >= 0:
+                ns.append(n)
+                hs.append(hq_i)
+                ss.append(slot)
+    if ns:
+        ni = torch.tensor(ns, device=dev["q_pre"].device)
+        hi = torch.tensor(hs, device=dev["q_pre"].device)
+        si = torch.tensor(ss, device=dev["q_pre"].device)
+        dev["query_cache"][ni, si, hi] = dev["q_pre"][ni, hi]
+    return len(ns)
