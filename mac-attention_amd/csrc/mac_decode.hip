@@ -44,6 +44,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 
@@ -482,24 +483,18 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* s_tmp, int& tota
   return base + x - v;
 }
 
-template <int G>
-__global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
-  constexpr int U = 2;                 // tokens per row per iteration
-  constexpr int kStep = kWaves * 4 * U;  // tokens per workgroup iteration
-  __shared__ int s_off[kMaxPlanGroups + 1];
-  __shared__ int s_tmp[kWaves];
-  __shared__ float s_o[kWaves][G][kHeadDim];
-  __shared__ float s_ml[kWaves][G][2];
-
+// Every workgroup of span_attention derives the same task list: the chunk C
+// from the total token count of all groups (about four tasks per workgroup,
+// a multiple of 64 tokens, at most 16384), then per-group task counts and
+// their exclusive prefix sums in s_off[0..NG).  Workgroup 0 also publishes the
+// per-group chunk and task counts for merge_write and the task counters.
+__device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& total_tasks_out,
+                           int& chunk_out) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int row = lane >> 4;
-  const int c = lane & 15;
   const int NG = p.s.N * p.s.Hkv;
   const int W = gridDim.x;
-
-  // ---- plan: launch-wide chunk from the total token count ----
   const int per_thread = ceil_div(NG, kBlock);
   const int g_lo = min(tid * per_thread, NG);
   const int g_hi = min(g_lo + per_thread, NG);
@@ -600,43 +595,114 @@ __global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
     }
   }
 
+  total_tasks_out = total_tasks;
+  chunk_out = chunk;
+}
+
+struct TaskInfo {
+  int g, j, n, hkv, a, b;
+  bool band;
+  int P, req;
+  bool req_ok;
+  int64_t cur_loc;
+};
+
+// Group, token range [a, b) and kind of task t (sink, band or tail).
+__device__ __forceinline__ TaskInfo decode_task(const AttnParams& p, const int* s_off, int NG, int chunk,
+                                                int t) {
+  TaskInfo ti;
+  int lo = 0, hi = NG - 1;  // last g with s_off[g] <= t
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_off[mid] <= t) lo = mid; else hi = mid - 1;
+  }
+  ti.g = lo;
+  ti.j = t - s_off[lo];
+  ti.n = lo / p.s.Hkv;
+  ti.hkv = lo - ti.n * p.s.Hkv;
+  const GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, lo, p.F, chunk, p.cap);
+  ti.band = false;
+  if (ti.j < sp.n_sink) {
+    ti.a = ti.j * sp.chunk;
+    ti.b = min(ti.a + sp.chunk, sp.sink_end);
+  } else if (ti.j < sp.n_sink + sp.n_band) {
+    ti.a = sp.band_begin + (ti.j - sp.n_sink) * sp.chunk;
+    ti.b = min(ti.a + sp.chunk, sp.new_end);
+    ti.band = true;
+  } else {
+    ti.a = sp.new_end + (ti.j - sp.n_sink - sp.n_band) * sp.chunk;
+    ti.b = min(ti.a + sp.chunk, sp.kv_len);
+  }
+  ti.P = p.past_lens[ti.n];
+  ti.req = p.req_ids[ti.n];
+  ti.req_ok = ti.req >= 0 && ti.req < p.s.r2t_rows;
+  ti.cur_loc = p.s.out_cache_loc_is_i64 ? static_cast<const int64_t*>(p.out_cache_loc)[ti.n]
+                                        : static_cast<int64_t>(static_cast<const int32_t*>(p.out_cache_loc)[ti.n]);
+  return ti;
+}
+
+// Combines the per-wave softmax states in LDS (unnormalised o, running max m
+// in log2 units, sum l) into one normalised partial (o, natural-log lse) per
+// head and stores it in slot j of group g.
+template <int G>
+__device__ __forceinline__ void write_partial(const AttnParams& p, int g, int j,
+                                              const float (*s_o)[G][kHeadDim],
+                                              const float (*s_ml)[G][2]) {
+  const int tid = threadIdx.x;
+  const int64_t slot = static_cast<int64_t>(g) * p.cap + j;
+  for (int e = tid; e < G * kHeadDim; e += kBlock) {
+    const int h = e / kHeadDim;
+    const int d = e - h * kHeadDim;
+    float mm = kNegBig;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, s_ml[w][h][0]);
+    float ll = 0.0f, oo = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float sc = fast_exp2(s_ml[w][h][0] - mm);
+      ll += s_ml[w][h][1] * sc;
+      oo += s_o[w][h][d] * sc;
+    }
+    const bool nonempty = ll > 0.0f;
+    const float ov = nonempty ? oo / ll : 0.0f;
+    const int64_t oi = static_cast<int64_t>(g) * p.o_group_stride + (static_cast<int64_t>(j) * G + h) * kHeadDim + d;
+    if (p.partial_bf16)
+      static_cast<uint16_t*>(p.partial_o)[oi] = f32_to_bf16(ov);
+    else
+      static_cast<float*>(p.partial_o)[oi] = ov;
+    if (d == 0) p.partial_lse[slot * G + h] = nonempty ? (mm + log2f(ll)) * kLn2 : -INFINITY;
+  }
+}
+
+template <int G>
+__global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
+  constexpr int U = 2;                 // tokens per row per iteration
+  constexpr int kStep = kWaves * 4 * U;  // tokens per workgroup iteration
+  __shared__ int s_off[kMaxPlanGroups + 1];
+  __shared__ int s_tmp[kWaves];
+  __shared__ float s_o[kWaves][G][kHeadDim];
+  __shared__ float s_ml[kWaves][G][2];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int row = lane >> 4;
+  const int c = lane & 15;
+  const int NG = p.s.N * p.s.Hkv;
+  const int W = gridDim.x;
+
+  int total_tasks = 0, chunk = 0;
+  plan_tasks(p, s_off, s_tmp, total_tasks, chunk);
+
   // ---- tasks ----
   const int Hq = p.s.Hq;
   const int Hkv = p.s.Hkv;
   const int my_tok = wave * 4 + row;  // token offset inside each 16-token sub-block
   for (int t = blockIdx.x; t < total_tasks; t += W) {
-    // group of task t: last g with s_off[g] <= t
-    int lo = 0, hi = NG - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_off[mid] <= t) lo = mid; else hi = mid - 1;
-    }
-    const int g = lo;
-    const int j = t - s_off[g];
-    const int n = g / Hkv;
-    const int hkv = g - n * Hkv;
-    const GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, g, p.F, chunk, p.cap);
-    int a, b;
-    bool band = false;
-    if (j < sp.n_sink) {
-      a = j * sp.chunk;
-      b = min(a + sp.chunk, sp.sink_end);
-    } else if (j < sp.n_sink + sp.n_band) {
-      a = sp.band_begin + (j - sp.n_sink) * sp.chunk;
-      b = min(a + sp.chunk, sp.new_end);
-      band = true;
-    } else {
-      a = sp.new_end + (j - sp.n_sink - sp.n_band) * sp.chunk;
-      b = min(a + sp.chunk, sp.kv_len);
-    }
-    const int P = p.past_lens[n];
-    const int req = p.req_ids[n];
-    const bool req_ok = req >= 0 && req < p.s.r2t_rows;
-    int64_t cur_loc;
-    if (p.s.out_cache_loc_is_i64)
-      cur_loc = static_cast<const int64_t*>(p.out_cache_loc)[n];
-    else
-      cur_loc = static_cast<const int32_t*>(p.out_cache_loc)[n];
+    const TaskInfo ti = decode_task(p, s_off, NG, chunk, t);
+    const int g = ti.g, j = ti.j, n = ti.n, hkv = ti.hkv, a = ti.a, b = ti.b, P = ti.P, req = ti.req;
+    const bool band = ti.band, req_ok = ti.req_ok;
+    const int64_t cur_loc = ti.cur_loc;
     const int32_t* r2t = p.req_to_token + static_cast<int64_t>(req_ok ? req : 0) * p.s.r2t_stride;
 
     // per-head band start (positions before it are masked for that head)
@@ -782,29 +848,233 @@ __global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
       }
     }
     __syncthreads();
-    const int64_t slot = static_cast<int64_t>(g) * p.cap + j;
-    for (int e = tid; e < G * kHeadDim; e += kBlock) {
-      const int h = e / kHeadDim;
-      const int d = e - h * kHeadDim;
-      float mm = kNegBig;
+    write_partial<G>(p, g, j, s_o, s_ml);
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------- MFMA span attention ----
+//
+// Same plan and task list as span_attention_kernel; the per-task inner loop
+// runs both contractions on v_mfma_f32_16x16x32_bf16 (gfx950), one 64-lane
+// wave per 32-token block (waves take blocks wave, wave+4, ...):
+//
+//   S^T[t][g] = sum_d K[t][d] Q[g][d]     A = K rows straight from HBM (each
+//       lane loads 16 B of two token rows per k-step, d-chunk 4s + lane/16),
+//       B = Q^T from registers, two 16-token tiles x 4 k-steps;
+//   O^T[d][g] += sum_t V[t][d] P[g][t]    A = V^T gathered from an LDS copy
+//       of the block's V rows, B = P, which is exactly the lane's own S^T
+//       values converted to bf16 (token order of the k axis chosen to match),
+//       8 tiles of 16 dims.
+//
+// Lane l therefore owns query head g = l % 16 for both the softmax state and
+// the O^T accumulators (dims 16*dt + 4*(l/16) + r), so the online-softmax
+// rescale is lane-local.  Heads g >= G are padding (masked to -inf).
+//
+// The V tile is stored row-major per token with 16-byte chunk c of token t at
+// position c ^ 2*((t >> 2) & 3): the four lane groups of one gather then hit
+// disjoint LDS banks.
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& w) { return __builtin_bit_cast(bf16x8_t, w); }
+
+template <int G>
+__global__ void __launch_bounds__(kBlock) span_attention_mfma_kernel(AttnParams p) {
+  constexpr int kBlk = 32;  // tokens per wave block
+  __shared__ int s_off[kMaxPlanGroups + 1];
+  __shared__ int s_tmp[kWaves];
+  __shared__ uint4 s_v[kWaves][kBlk * 16];
+  __shared__ float s_o[kWaves][G][kHeadDim];
+  __shared__ float s_ml[kWaves][G][2];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int quad = lane >> 4;  // lane / 16
+  const int col = lane & 15;   // lane % 16: token row of the K operand, head of the outputs
+  const int NG = p.s.N * p.s.Hkv;
+  const int W = gridDim.x;
+  int total_tasks = 0, chunk = 0;
+  plan_tasks(p, s_off, s_tmp, total_tasks, chunk);
+
+  const int Hq = p.s.Hq;
+  const int Hkv = p.s.Hkv;
+  const int64_t kv_stride = static_cast<int64_t>(Hkv) * kHeadDim;
+  const bool head_ok = col < G;
+  uint16_t* vtile = reinterpret_cast<uint16_t*>(&s_v[wave][0]);
+
+  for (int t = blockIdx.x; t < total_tasks; t += W) {
+    const TaskInfo ti = decode_task(p, s_off, NG, chunk, t);
+    const int n = ti.n, hkv = ti.hkv, a = ti.a, b = ti.b, P = ti.P;
+    const int32_t* r2t = p.req_to_token + static_cast<int64_t>(ti.req_ok ? ti.req : 0) * p.s.r2t_stride;
+    const uint16_t* kbase = p.k_buffer + static_cast<int64_t>(hkv) * kHeadDim;
+    const uint16_t* vbase = p.v_buffer + static_cast<int64_t>(hkv) * kHeadDim;
+
+    // B operand of QK^T: Q^T, lane holds Q[col][8*(4s+quad) .. +8] for k-step s
+    bf16x8_t qb[4];
+    int head_begin = 0;
+    {
+      const int64_t qoff = (static_cast<int64_t>(n) * Hq + hkv * G + (head_ok ? col : 0)) * kHeadDim;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, s_ml[w][h][0]);
-      float ll = 0.0f, oo = 0.0f;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float sc = fast_exp2(s_ml[w][h][0] - mm);
-        ll += s_ml[w][h][1] * sc;
-        oo += s_o[w][h][d] * sc;
+      for (int s = 0; s < 4; ++s) {
+        uint4 w = make_uint4(0, 0, 0, 0);
+        if (head_ok) w = *reinterpret_cast<const uint4*>(p.q_post + qoff + (4 * s + quad) * 8);
+        qb[s] = as_bf16x8(w);
       }
-      const bool nonempty = ll > 0.0f;
-      const float ov = nonempty ? oo / ll : 0.0f;
-      const int64_t oi = static_cast<int64_t>(g) * p.o_group_stride + (static_cast<int64_t>(j) * G + h) * kHeadDim + d;
-      if (p.partial_bf16)
-        static_cast<uint16_t*>(p.partial_o)[oi] = f32_to_bf16(ov);
-      else
-        static_cast<float*>(p.partial_o)[oi] = ov;
-      if (d == 0) p.partial_lse[slot * G + h] = nonempty ? (mm + log2f(ll)) * kLn2 : -INFINITY;
+      if (ti.band && head_ok) head_begin = p.head_rect_start[static_cast<int64_t>(n) * Hq + hkv * G + col];
     }
+    auto phys_of = [&](int pos) -> int64_t {
+      if (pos >= b || !ti.req_ok) return -1;
+      const int64_t ph = pos == P ? ti.cur_loc : static_cast<int64_t>(r2t[pos]);
+      return (ph >= 0 && ph < p.s.pool_tokens) ? ph : -1;
+    };
+
+    float m = kNegBig, l = 0.0f;
+    f32x4_t acc[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int nblk = ceil_div(b - a, kBlk);
+    // Registers kc (K rows of tokens col and 16+col, four 16-byte d-chunks
+    // each) and vc (eight 16-byte chunks of the V row of token lane%32) hold
+    // the current block; each is refilled with the wave's next block right
+    // after its last use, so the loads overlap the rest of the block's work.
+    uint4 kc[2][4], vc[8];
+    auto load_k = [&](int64_t ph0, int64_t ph1) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        kc[0][s] = make_uint4(0, 0, 0, 0);
+        kc[1][s] = make_uint4(0, 0, 0, 0);
+        if (ph0 >= 0) kc[0][s] = *reinterpret_cast<const uint4*>(kbase + ph0 * kv_stride + (4 * s + quad) * 8);
+        if (ph1 >= 0) kc[1][s] = *reinterpret_cast<const uint4*>(kbase + ph1 * kv_stride + (4 * s + quad) * 8);
+      }
+    };
+    auto load_v = [&](int64_t phv) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        vc[i] = make_uint4(0, 0, 0, 0);
+        if (phv >= 0) vc[i] = *reinterpret_cast<const uint4*>(vbase + phv * kv_stride + ((lane >> 5) + 2 * i) * 8);
+      }
+    };
+    int blk = wave;
+    int64_t pk0, pk1, pv, nk0, nk1, nv;
+    {
+      const int base = a + blk * kBlk;
+      pk0 = phys_of(base + col);
+      pk1 = phys_of(base + 16 + col);
+      pv = phys_of(base + (lane & 31));
+      load_k(pk0, pk1);
+      load_v(pv);
+      const int nbase = base + kWaves * kBlk;
+      nk0 = phys_of(nbase + col);
+      nk1 = phys_of(nbase + 16 + col);
+      nv = phys_of(nbase + (lane & 31));
+    }
+    for (; blk < nblk; blk += kWaves) {
+      const int base = a + blk * kBlk;
+      const bool more = blk + kWaves < nblk;
+      // validity of the 32 tokens of this block, as seen by the K loads
+      const uint64_t vm0 = __ballot(pk0 >= 0);
+      const uint64_t vm1 = __ballot(pk1 >= 0);
+      // stage this block's V rows into the wave's LDS tile, then refill vc
+      {
+        const int tv = lane & 31;
+        const int swz = 2 * ((tv >> 2) & 3);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s_v[wave][tv * 16 + (((lane >> 5) + 2 * i) ^ swz)] = vc[i];
+      }
+      if (more) load_v(nv);
+
+      // S^T = K Q^T for tokens [base, base + 32), then refill kc
+      f32x4_t st[2];
+#pragma unroll
+      for (int tile = 0; tile < 2; ++tile) {
+        f32x4_t c4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kc[tile][s]), qb[s], c4, 0, 0, 0);
+        st[tile] = c4;
+      }
+      if (more) load_k(nk0, nk1);
+      pk0 = nk0;
+      pk1 = nk1;
+      pv = nv;
+      {
+        const int fbase = base + 2 * kWaves * kBlk;
+        nk0 = phys_of(fbase + col);
+        nk1 = phys_of(fbase + 16 + col);
+        nv = phys_of(fbase + (lane & 31));
+      }
+
+      // scale, mask, online softmax (lane-local except the block max)
+      float sv[8];
+      float bmax = kNegBig;
+#pragma unroll
+      for (int tile = 0; tile < 2; ++tile) {
+        const uint64_t vm = tile ? vm1 : vm0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tok = 4 * quad + r;  // token within the tile
+          const int pos = base + 16 * tile + tok;
+          const bool ok = head_ok && ((vm >> tok) & 1) && pos >= head_begin;
+          const float x = ok ? st[tile][r] * p.q_scale : -INFINITY;
+          sv[4 * tile + r] = x;
+          bmax = fmaxf(bmax, x);
+        }
+      }
+      bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+      bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+      const float m_new = fmaxf(m, bmax);
+      const float alpha = fast_exp2(m - m_new);
+      m = m_new;
+      bf16x8_t pb;
+      float psum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float pe = fast_exp2(sv[e] - m_new);
+        psum += pe;
+        pb[e] = static_cast<__bf16>(pe);
+      }
+      l = fmaf(l, alpha, psum);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // O^T += V^T P^T: A operand gathered from the LDS tile
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const int chunk_pos = (2 * (dt ^ quad) + (col >> 3));
+        bf16x8_t va;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int tok = e < 4 ? 4 * quad + e : 16 + 4 * quad + (e - 4);
+          const uint16_t bits = vtile[(tok * 16 + chunk_pos) * 8 + (col & 7)];
+          va[e] = __builtin_bit_cast(__bf16, bits);
+        }
+        acc[dt] *= alpha;
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, acc[dt], 0, 0, 0);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+    }
+    (void)pv;
+
+    // ---- wave result -> LDS, then combine the four waves ----
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (head_ok) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s_o[wave][col][16 * dt + 4 * quad + r] = acc[dt][r];
+      if (quad == 0) {
+        s_ml[wave][col][0] = m;
+        s_ml[wave][col][1] = l;
+      }
+    }
+    __syncthreads();
+    write_partial<G>(p, ti.g, ti.j, s_o, s_ml);
     __syncthreads();
   }
 }
@@ -939,53 +1209,69 @@ int fail(int code, const char* fmt, ...) {
 
 struct DeviceInfo {
   int cus = 0;
-  int attn_blocks_per_cu[kMaxGroup + 1] = {};
+  int attn_blocks_per_cu[2][kMaxGroup + 1] = {};
 };
+
+// MAC_AMD_ATTN_IMPL=valu selects the VALU span-attention kernel; the default
+// is the MFMA kernel.  Read once per process.
+int attn_impl() {
+  static const int impl = [] {
+    const char* e = std::getenv("MAC_AMD_ATTN_IMPL");
+    return (e != nullptr && std::strcmp(e, "valu") == 0) ? 0 : 1;
+  }();
+  return impl;
+}
 
 std::mutex g_dev_mu;
 DeviceInfo g_dev[64];
 
 template <int G>
-void* attn_kernel_ptr() { return reinterpret_cast<void*>(&span_attention_kernel<G>); }
+void* attn_kernel_ptr(int impl) {
+  return impl ? reinterpret_cast<void*>(&span_attention_mfma_kernel<G>)
+              : reinterpret_cast<void*>(&span_attention_kernel<G>);
+}
 
-int attn_residency(int dev, int G, int* cus, int* per_cu) {
+int attn_residency(int dev, int G, int impl, int* cus, int* per_cu) {
   std::lock_guard<std::mutex> lk(g_dev_mu);
   if (dev < 0 || dev >= 64) return fail(MAC_ERR_UNSUPPORTED, "device index %d out of range", dev);
   DeviceInfo& di = g_dev[dev];
   if (di.cus == 0) {
     MAC_HIP(hipDeviceGetAttribute(&di.cus, hipDeviceAttributeMultiprocessorCount, dev));
   }
-  if (di.attn_blocks_per_cu[G] == 0) {
+  if (di.attn_blocks_per_cu[impl][G] == 0) {
     void* fn = nullptr;
     switch (G) {
-      case 1: fn = attn_kernel_ptr<1>(); break;
-      case 2: fn = attn_kernel_ptr<2>(); break;
-      case 3: fn = attn_kernel_ptr<3>(); break;
-      case 4: fn = attn_kernel_ptr<4>(); break;
-      case 5: fn = attn_kernel_ptr<5>(); break;
-      case 6: fn = attn_kernel_ptr<6>(); break;
-      case 7: fn = attn_kernel_ptr<7>(); break;
-      default: fn = attn_kernel_ptr<8>(); break;
+      case 1: fn = attn_kernel_ptr<1>(impl); break;
+      case 2: fn = attn_kernel_ptr<2>(impl); break;
+      case 3: fn = attn_kernel_ptr<3>(impl); break;
+      case 4: fn = attn_kernel_ptr<4>(impl); break;
+      case 5: fn = attn_kernel_ptr<5>(impl); break;
+      case 6: fn = attn_kernel_ptr<6>(impl); break;
+      case 7: fn = attn_kernel_ptr<7>(impl); break;
+      default: fn = attn_kernel_ptr<8>(impl); break;
     }
     int blocks = 0;
     MAC_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kBlock, 0));
-    di.attn_blocks_per_cu[G] = blocks > 0 ? blocks : 1;
+    di.attn_blocks_per_cu[impl][G] = blocks > 0 ? blocks : 1;
   }
   *cus = di.cus;
-  *per_cu = di.attn_blocks_per_cu[G];
+  *per_cu = di.attn_blocks_per_cu[impl][G];
   return MAC_OK;
 }
 
 // ev (optional): four events recorded before, between and after the kernels.
 template <int G>
 int launch_all(const DecideParams& dp, const AttnParams& ap, const MergeParams& mp, int attn_grid,
-               hipStream_t stream, hipEvent_t* ev) {
+               int impl, hipStream_t stream, hipEvent_t* ev) {
   const int NG = dp.s.N * dp.s.Hkv;
   if (ev) MAC_HIP(hipEventRecord(ev[0], stream));
   hipLaunchKernelGGL(match_decide_kernel<G>, dim3(NG), dim3(kBlock), 0, stream, dp);
   MAC_HIP(hipGetLastError());
   if (ev) MAC_HIP(hipEventRecord(ev[1], stream));
-  hipLaunchKernelGGL(span_attention_kernel<G>, dim3(attn_grid), dim3(kBlock), 0, stream, ap);
+  if (impl)
+    hipLaunchKernelGGL(span_attention_mfma_kernel<G>, dim3(attn_grid), dim3(kBlock), 0, stream, ap);
+  else
+    hipLaunchKernelGGL(span_attention_kernel<G>, dim3(attn_grid), dim3(kBlock), 0, stream, ap);
   MAC_HIP(hipGetLastError());
   if (ev) MAC_HIP(hipEventRecord(ev[2], stream));
   hipLaunchKernelGGL(merge_write_kernel<G>, dim3(NG), dim3(kBlock), 0, stream, mp);
@@ -1070,7 +1356,8 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   int dev = 0;
   MAC_HIP(hipGetDevice(&dev));
   int cus = 0, per_cu = 0;
-  int rc = attn_residency(dev, G, &cus, &per_cu);
+  const int impl = attn_impl();
+  int rc = attn_residency(dev, G, impl, &cus, &per_cu);
   if (rc != MAC_OK) return rc;
 
   Shape s{};
@@ -1199,13 +1486,13 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   if (grid < 1) grid = 1;
 
   switch (G) {
-    case 1: return launch_all<1>(dp, ap, mp, static_cast<int>(grid), stream, ev);
-    case 2: return launch_all<2>(dp, ap, mp, static_cast<int>(grid), stream, ev);
-    case 3: return launch_all<3>(dp, ap, mp, static_cast<int>(grid), stream, ev);
-    case 4: return launch_all<4>(dp, ap, mp, static_cast<int>(grid), stream, ev);
-    case 5: return launch_all<5>(dp, ap, mp, static_cast<int>(grid), stream, ev);
-    case 6: return launch_all<6>(dp, ap, mp, static_cast<int>(grid), stream, ev);
-    case 7: return launch_all<7>(dp, ap, mp, static_cast<int>(grid), stream, ev);
-    default: return launch_all<8>(dp, ap, mp, static_cast<int>(grid), stream, ev);
+    case 1: return launch_all<1>(dp, ap, mp, static_cast<int>(grid), impl, stream, ev);
+    case 2: return launch_all<2>(dp, ap, mp, static_cast<int>(grid), impl, stream, ev);
+    case 3: return launch_all<3>(dp, ap, mp, static_cast<int>(grid), impl, stream, ev);
+    case 4: return launch_all<4>(dp, ap, mp, static_cast<int>(grid), impl, stream, ev);
+    case 5: return launch_all<5>(dp, ap, mp, static_cast<int>(grid), impl, stream, ev);
+    case 6: return launch_all<6>(dp, ap, mp, static_cast<int>(grid), impl, stream, ev);
+    case 7: return launch_all<7>(dp, ap, mp, static_cast<int>(grid), impl, stream, ev);
+    default: return launch_all<8>(dp, ap, mp, static_cast<int>(grid), impl, stream, ev);
   }
 }
