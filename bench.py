@@ -228,6 +228,24 @@ def cpu_baseline(args, hit):
                 sample_head_hits=int(res.head["hit"].sum()))
 
 
+PMC_SUMMARY = os.path.join(REPO, "profiles", "span_attention_config3_gqa4_hit0.8_pmc.txt")
+
+
+def pmc_traffic(args):
+    """HBM bytes per span_attention launch from the committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE summary (scaled by the copy-kernel calibration it
+    records).  Only valid for the workload that summary profiled."""
+    default = (args.hkv == 8 and args.batch == 64 and args.ctx == 130048 and args.ring == 32
+               and abs(args.hit - 0.8) < 1e-9 and args.front_sink == 0)
+    if not default or not os.path.exists(PMC_SUMMARY):
+        return None, None
+    with open(PMC_SUMMARY) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch="):
+                return int(line.split("=", 1)[1]), os.path.relpath(PMC_SUMMARY, REPO)
+    return None, None
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -281,9 +299,10 @@ def main():
 
     ms = headline["us_per_step"] / 1e3
     attn_us = headline["phase_us"][1]
+    traffic, traffic_src = pmc_traffic(args)
     roof = dict(bound="hbm", achieved=headline["attention_kernel_gbs"], peak=HBM_PEAK_GBS,
                 unit="GB/s", frac=round(headline["attention_kernel_gbs"] / HBM_PEAK_GBS, 4),
-                traffic=None, kernel="span_attention", kernel_us=attn_us,
+                traffic=traffic, traffic_source=traffic_src, kernel="span_attention", kernel_us=attn_us,
                 bytes_per_launch=headline["attention_kernel_bytes"])
     line = {
         "metric": METRIC,
