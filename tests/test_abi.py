@@ -1,0 +1,90 @@
+"""The C-ABI library loads, exports every entry point include/*.h declares,
+matches the binding's struct layout, and rejects bad arguments with a message
+(CPU only: no kernel is launched)."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from helpers import REPO
+
+HEADER = os.path.join(REPO, "include", "mac_attention_amd.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return re.findall(r"MAC_API\s+[\w\s\*]+?\b(mac_\w+)\s*\(", text)
+
+
+@pytest.fixture(scope="module")
+def bridge():
+    from mac_attention.integrations.sglang import bridge as b
+
+    if not os.path.exists(b.LIB_PATH):
+        pytest.fail(f"{b.LIB_PATH} is not built; run __graft_entry__.build()")
+    return b
+
+
+def test_library_exports_every_declared_symbol(bridge):
+    names = _declared()
+    assert len(names) >= 8
+    lib = bridge.load_library()
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(bridge.EXPORTED_SYMBOLS)
+    nm = subprocess.run(["nm", "-D", "--defined-only", bridge.LIB_PATH], capture_output=True,
+                        text=True, check=True).stdout
+    exported = {l.split()[-1] for l in nm.splitlines() if " T " in l}
+    assert exported == set(names)
+    assert lib.mac_abi_version() == bridge.ABI_VERSION
+
+
+def test_struct_layout_matches_header(bridge, tmp_path):
+    fields = [f[0] for f in bridge.MacDecodeArgs._fields_]
+    src = ['#include <stdio.h>', '#include <stddef.h>', '#include "mac_attention_amd.h"',
+           'int main(void) {', 'printf("size %zu\\n", sizeof(MacDecodeArgs));']
+    for f in fields:
+        src.append(f'printf("{f} %zu\\n", offsetof(MacDecodeArgs, {f}));')
+    src.append("return 0; }")
+    c = tmp_path / "layout.c"
+    c.write_text("\n".join(src))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.dirname(HEADER), str(c), "-o", str(exe)], check=True)
+    out = dict(l.split() for l in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                  check=True).stdout.splitlines())
+    assert int(out["size"]) == ctypes.sizeof(bridge.MacDecodeArgs)
+    for f in fields:
+        assert int(out[f]) == getattr(bridge.MacDecodeArgs, f).offset, f
+
+
+def test_bad_arguments_return_error_and_message(bridge):
+    lib = bridge.load_library()
+    a = bridge.MacDecodeArgs()
+    a.struct_size = ctypes.sizeof(a) + 8
+    a.abi_version = bridge.ABI_VERSION
+    assert lib.mac_persistent_decode_bf16(ctypes.byref(a), None) == 1
+    assert b"size/version mismatch" in lib.mac_last_error()
+    a.struct_size = ctypes.sizeof(a)
+    a.N, a.Hq, a.Hkv, a.D, a.M, a.R = 1, 32, 8, 64, 8, 1
+    assert lib.mac_persistent_decode_bf16(ctypes.byref(a), None) == 1
+    assert b"D=128" in lib.mac_last_error()
+    a.D, a.Hkv = 128, 3
+    assert lib.mac_persistent_decode_bf16(ctypes.byref(a), None) == 1
+    assert b"divisible" in lib.mac_last_error()
+    a.Hkv, a.Hq = 2, 32
+    assert lib.mac_persistent_decode_bf16(ctypes.byref(a), None) == 1
+    assert b"group size" in lib.mac_last_error()
+    assert lib.mac_mark_persistent_ready(None, None, None, None, 0, 4, None) == 0
+    assert lib.mac_mark_persistent_ready(None, None, None, None, 2, 4, None) == 1
+    assert b"NULL" in lib.mac_last_error()
+
+
+def test_binding_rejects_host_tensors(bridge):
+    torch = pytest.importorskip("torch")
+    ext = bridge.PersistentDecodeExtension(bridge.load_library())
+    q = torch.zeros(1, 8, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="q_post must be CUDA"):
+        ext.mac_persistent_decode_bf16(q, *([None] * 67))
