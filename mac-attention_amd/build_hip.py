@@ -21,6 +21,9 @@ FLAGS = [
     # keep the compiler from forming packed-fp32 VALU ops (toolchain notes)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-fvisibility=hidden",
+    # MFMA accumulators in VGPRs: the online-softmax rescale then works on
+    # them in place instead of copying them through AGPRs every block
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", os.path.join(REPO, "include"),
     "-I", os.path.join(HERE, "csrc"),
 ]

@@ -890,7 +890,7 @@ __global__ void __launch_bounds__(kBlock) span_attention_mfma_kernel(AttnParams 
   __shared__ float s_ml[kWaves][G][2];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) control flow
   const int lane = tid & 63;
   const int quad = lane >> 4;  // lane / 16
   const int col = lane & 15;   // lane % 16: token row of the K operand, head of the outputs
@@ -925,10 +925,18 @@ __global__ void __launch_bounds__(kBlock) span_attention_mfma_kernel(AttnParams 
       }
       if (ti.band && head_ok) head_begin = p.head_rect_start[static_cast<int64_t>(n) * Hq + hkv * G + col];
     }
-    auto phys_of = [&](int pos) -> int64_t {
-      if (pos >= b || !ti.req_ok) return -1;
-      const int64_t ph = pos == P ? ti.cur_loc : static_cast<int64_t>(r2t[pos]);
-      return (ph >= 0 && ph < p.s.pool_tokens) ? ph : -1;
+    // Physical rows are looked up two blocks ahead: raw_row() only issues the
+    // req_to_token load (unconditionally, index clamped into the row), and
+    // the value is checked one iteration later by phys_ok(), so no wait on
+    // that load ever forces the in-flight K/V loads to drain.  A position
+    // outside the task or a row out of range yields -1 (masked token).
+    const int r2t_last = max(min(P, p.s.r2t_stride) - 1, 0);
+    const int cur_row = (ti.cur_loc >= 0 && ti.cur_loc < p.s.pool_tokens) ? static_cast<int>(ti.cur_loc) : -1;
+    const unsigned pool_rows = static_cast<unsigned>(min(p.s.pool_tokens, static_cast<int64_t>(INT_MAX)));
+    auto raw_row = [&](int pos) -> int { return r2t[min(max(pos, 0), r2t_last)]; };
+    auto phys_ok = [&](int pos, int raw) -> int {
+      const int ph = pos == P ? cur_row : raw;
+      return (pos < b && ti.req_ok && static_cast<unsigned>(ph) < pool_rows) ? ph : -1;
     };
 
     float m = kNegBig, l = 0.0f;
@@ -941,51 +949,85 @@ __global__ void __launch_bounds__(kBlock) span_attention_mfma_kernel(AttnParams 
     // each) and vc (eight 16-byte chunks of the V row of token lane%32) hold
     // the current block; each is refilled with the wave's next block right
     // after its last use, so the loads overlap the rest of the block's work.
+    // Loads are unconditional (a masked token reads row 0) so that no
+    // exec-mask branches split the load stream; masked K scores become -inf
+    // and masked V rows are zeroed before they reach LDS.
     uint4 kc[2][4], vc[8];
-    auto load_k = [&](int64_t ph0, int64_t ph1) {
+    auto load_k = [&](int ph0, int ph1) {
+      const uint16_t* r0 = kbase + static_cast<int64_t>(max(ph0, 0)) * kv_stride + quad * 8;
+      const uint16_t* r1 = kbase + static_cast<int64_t>(max(ph1, 0)) * kv_stride + quad * 8;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        kc[0][s] = make_uint4(0, 0, 0, 0);
-        kc[1][s] = make_uint4(0, 0, 0, 0);
-        if (ph0 >= 0) kc[0][s] = *reinterpret_cast<const uint4*>(kbase + ph0 * kv_stride + (4 * s + quad) * 8);
-        if (ph1 >= 0) kc[1][s] = *reinterpret_cast<const uint4*>(kbase + ph1 * kv_stride + (4 * s + quad) * 8);
+        kc[0][s] = *reinterpret_cast<const uint4*>(r0 + 32 * s);
+        kc[1][s] = *reinterpret_cast<const uint4*>(r1 + 32 * s);
       }
     };
-    auto load_v = [&](int64_t phv) {
+    auto load_v = [&](int phv) {
+      const uint16_t* r = vbase + static_cast<int64_t>(max(phv, 0)) * kv_stride + (lane >> 5) * 8;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        vc[i] = make_uint4(0, 0, 0, 0);
-        if (phv >= 0) vc[i] = *reinterpret_cast<const uint4*>(vbase + phv * kv_stride + ((lane >> 5) + 2 * i) * 8);
-      }
+      for (int i = 0; i < 8; ++i) vc[i] = *reinterpret_cast<const uint4*>(r + 16 * i);
     };
+    const int tk0 = col, tk1 = 16 + col, tv = lane & 31;  // tokens this lane loads
     int blk = wave;
-    int64_t pk0, pk1, pv, nk0, nk1, nv;
+    int pk0, pk1, pv;     // checked rows of the current block
+    int rk0, rk1, rv;     // raw rows of the next block
     {
       const int base = a + blk * kBlk;
-      pk0 = phys_of(base + col);
-      pk1 = phys_of(base + 16 + col);
-      pv = phys_of(base + (lane & 31));
-      load_k(pk0, pk1);
-      load_v(pv);
+      pk0 = phys_ok(base + tk0, raw_row(base + tk0));
+      pk1 = phys_ok(base + tk1, raw_row(base + tk1));
+      pv = phys_ok(base + tv, raw_row(base + tv));
       const int nbase = base + kWaves * kBlk;
-      nk0 = phys_of(nbase + col);
-      nk1 = phys_of(nbase + 16 + col);
-      nv = phys_of(nbase + (lane & 31));
+      rk0 = raw_row(nbase + tk0);
+      rk1 = raw_row(nbase + tk1);
+      rv = raw_row(nbase + tv);
+      __builtin_amdgcn_sched_barrier(0);
+      // same issue order as the loop body (req_to_token, V, K) and always
+      // issued, so the loop entry and the back edge agree on what is in flight
+      load_v(pv);
+      __builtin_amdgcn_sched_barrier(0);
+      load_k(pk0, pk1);
+      __builtin_amdgcn_sched_barrier(0);
     }
     for (; blk < nblk; blk += kWaves) {
       const int base = a + blk * kBlk;
-      const bool more = blk + kWaves < nblk;
+      const int nbase = base + kWaves * kBlk;
+      // rows of the next block (their loads were issued one iteration ago);
+      // past the wave's last block they are -1 and the unconditional refills
+      // below re-read row 0 (a cache hit), which keeps the load count of
+      // every iteration equal so the compiler never has to drain the queue.
+      const int nk0 = phys_ok(nbase + tk0, rk0);
+      const int nk1 = phys_ok(nbase + tk1, rk1);
+      const int nv = phys_ok(nbase + tv, rv);
+      // raw rows two blocks ahead.  The scheduling barriers keep the issue
+      // order req_to_token -> V -> K within an iteration: the loads retire in
+      // order, so consuming the row indices next iteration then never waits
+      // for the K/V loads issued after them.
+      {
+        const int fbase = nbase + kWaves * kBlk;
+        rk0 = raw_row(fbase + tk0);
+        rk1 = raw_row(fbase + tk1);
+        rv = raw_row(fbase + tv);
+      }
+      __builtin_amdgcn_sched_barrier(0);
       // validity of the 32 tokens of this block, as seen by the K loads
       const uint64_t vm0 = __ballot(pk0 >= 0);
       const uint64_t vm1 = __ballot(pk1 >= 0);
       // stage this block's V rows into the wave's LDS tile, then refill vc
       {
-        const int tv = lane & 31;
         const int swz = 2 * ((tv >> 2) & 3);
+        const uint32_t keep = pv >= 0 ? 0xffffffffu : 0u;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s_v[wave][tv * 16 + (((lane >> 5) + 2 * i) ^ swz)] = vc[i];
+        for (int i = 0; i < 8; ++i) {
+          uint4 w = vc[i];
+          w.x &= keep;
+          w.y &= keep;
+          w.z &= keep;
+          w.w &= keep;
+          s_v[wave][tv * 16 + (((lane >> 5) + 2 * i) ^ swz)] = w;
+        }
       }
-      if (more) load_v(nv);
+      load_v(nv);
+      __builtin_amdgcn_sched_barrier(0);
 
       // S^T = K Q^T for tokens [base, base + 32), then refill kc
       f32x4_t st[2];
@@ -997,16 +1039,11 @@ __global__ void __launch_bounds__(kBlock) span_attention_mfma_kernel(AttnParams 
           c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kc[tile][s]), qb[s], c4, 0, 0, 0);
         st[tile] = c4;
       }
-      if (more) load_k(nk0, nk1);
+      load_k(nk0, nk1);
+      __builtin_amdgcn_sched_barrier(0);
       pk0 = nk0;
       pk1 = nk1;
       pv = nv;
-      {
-        const int fbase = base + 2 * kWaves * kBlk;
-        nk0 = phys_of(fbase + col);
-        nk1 = phys_of(fbase + 16 + col);
-        nv = phys_of(fbase + (lane & 31));
-      }
 
       // scale, mask, online softmax (lane-local except the block max)
       float sv[8];
@@ -1026,18 +1063,28 @@ __global__ void __launch_bounds__(kBlock) span_attention_mfma_kernel(AttnParams 
       }
       bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
       bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-      const float m_new = fmaxf(m, bmax);
-      const float alpha = fast_exp2(m - m_new);
-      m = m_new;
+      // Lazy rescale: the reference point m only moves when the block max
+      // exceeds it by more than kRescaleSlack (log2 units), so most blocks
+      // skip the 32-accumulator rescale; p <= 2^kRescaleSlack stays exact in
+      // fp32 and well inside bf16 range.
+      constexpr float kRescaleSlack = 8.0f;
+      if (__any(bmax > m + kRescaleSlack)) {
+        const float m_new = fmaxf(m, bmax);
+        const float alpha = fast_exp2(m - m_new);
+        m = m_new;
+        l *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+      }
       bf16x8_t pb;
       float psum = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float pe = fast_exp2(sv[e] - m_new);
+        const float pe = fast_exp2(sv[e] - m);
         psum += pe;
         pb[e] = static_cast<__bf16>(pe);
       }
-      l = fmaf(l, alpha, psum);
+      l += psum;
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -1052,13 +1099,11 @@ __global__ void __launch_bounds__(kBlock) span_attention_mfma_kernel(AttnParams 
           const uint16_t bits = vtile[(tok * 16 + chunk_pos) * 8 + (col & 7)];
           va[e] = __builtin_bit_cast(__bf16, bits);
         }
-        acc[dt] *= alpha;
         acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, acc[dt], 0, 0, 0);
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
     }
-    (void)pv;
 
     // ---- wave result -> LDS, then combine the four waves ----
     l += __shfl_xor(l, 16);
