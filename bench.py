@@ -57,6 +57,7 @@ def parse_args():
     ap.add_argument("--tile-tokens", type=int, default=32)
     ap.add_argument("--sweep", choices=["none", "short", "full"], default="short")
     ap.add_argument("--sweep-replays", type=int, default=30)
+    ap.add_argument("--sweep-hits", default="0,0.25,0.5,0.75,0.8,0.9,1.0")
     ap.add_argument("--cpu-requests", type=int, default=48)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--phase-runs", type=int, default=5)
@@ -264,7 +265,7 @@ def main():
     sweep = []
     headline = None
     gqa_list = [args.hkv] if args.sweep == "none" else [args.hkv, args.hq // 8]
-    hits = [0.0, 0.25, 0.5, 0.75, 0.8, 0.9, 1.0]
+    hits = [float(x) for x in args.sweep_hits.split(",") if x.strip()]
     for hkv in gqa_list:
         t0 = time.perf_counter()
         dev = syn.device_case(torch, batch=args.batch, hq=args.hq, hkv=hkv, ctx=args.ctx,

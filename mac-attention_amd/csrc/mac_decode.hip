@@ -880,12 +880,19 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& w) { return __builtin_bit_cast(bf16x8_t, w); }
 
-template <int G>
-__global__ void __launch_bounds__(kBlock) span_attention_mfma_kernel(AttnParams p) {
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+// 16-byte non-temporal (streaming) global load.
+__device__ __forceinline__ uint4 load_stream16(const uint16_t* ptr) {
+  return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(ptr)));
+}
+
+template <int G, int kDepth>
+__global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnParams p) {
   constexpr int kBlk = 32;  // tokens per wave block
   __shared__ int s_off[kMaxPlanGroups + 1];
   __shared__ int s_tmp[kWaves];
   __shared__ uint4 s_v[kWaves][kBlk * 16];
+  __shared__ uint4 s_q[16 * 16];
   __shared__ float s_o[kWaves][G][kHeadDim];
   __shared__ float s_ml[kWaves][G][2];
 
@@ -912,18 +919,21 @@ __global__ void __launch_bounds__(kBlock) span_attention_mfma_kernel(AttnParams 
     const uint16_t* kbase = p.k_buffer + static_cast<int64_t>(hkv) * kHeadDim;
     const uint16_t* vbase = p.v_buffer + static_cast<int64_t>(hkv) * kHeadDim;
 
-    // B operand of QK^T: Q^T, lane holds Q[col][8*(4s+quad) .. +8] for k-step s
-    bf16x8_t qb[4];
+    // B operand of QK^T is Q^T: lane (quad, col) needs Q[col][8*(4s+quad) .. +8]
+    // for k-step s.  The group's queries are staged once per task in LDS
+    // (rows g >= G zero) and re-read per block, which keeps 16 VGPRs free for
+    // the second K/V buffer.
     int head_begin = 0;
     {
-      const int64_t qoff = (static_cast<int64_t>(n) * Hq + hkv * G + (head_ok ? col : 0)) * kHeadDim;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
+      const int64_t qoff = static_cast<int64_t>(n) * Hq * kHeadDim + static_cast<int64_t>(hkv) * G * kHeadDim;
+      for (int e = tid; e < 16 * 16; e += kBlock) {  // 16 rows x 16 chunks of 16 bytes
+        const int g = e >> 4, c = e & 15;
         uint4 w = make_uint4(0, 0, 0, 0);
-        if (head_ok) w = *reinterpret_cast<const uint4*>(p.q_post + qoff + (4 * s + quad) * 8);
-        qb[s] = as_bf16x8(w);
+        if (g < G) w = *reinterpret_cast<const uint4*>(p.q_post + qoff + g * kHeadDim + c * 8);
+        s_q[e] = w;
       }
       if (ti.band && head_ok) head_begin = p.head_rect_start[static_cast<int64_t>(n) * Hq + hkv * G + col];
+      __syncthreads();
     }
     // Physical rows are looked up two blocks ahead: raw_row() only issues the
     // req_to_token load (unconditionally, index clamped into the row), and
@@ -945,80 +955,80 @@ __global__ void __launch_bounds__(kBlock) span_attention_mfma_kernel(AttnParams 
     for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     const int nblk = ceil_div(b - a, kBlk);
-    // Registers kc (K rows of tokens col and 16+col, four 16-byte d-chunks
-    // each) and vc (eight 16-byte chunks of the V row of token lane%32) hold
-    // the current block; each is refilled with the wave's next block right
-    // after its last use, so the loads overlap the rest of the block's work.
-    // Loads are unconditional (a masked token reads row 0) so that no
-    // exec-mask branches split the load stream; masked K scores become -inf
-    // and masked V rows are zeroed before they reach LDS.
-    uint4 kc[2][4], vc[8];
-    auto load_k = [&](int ph0, int ph1) {
-      const uint16_t* r0 = kbase + static_cast<int64_t>(max(ph0, 0)) * kv_stride + quad * 8;
-      const uint16_t* r1 = kbase + static_cast<int64_t>(max(ph1, 0)) * kv_stride + quad * 8;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        kc[0][s] = *reinterpret_cast<const uint4*>(r0 + 32 * s);
-        kc[1][s] = *reinterpret_cast<const uint4*>(r1 + 32 * s);
-      }
-    };
-    auto load_v = [&](int phv) {
-      const uint16_t* r = vbase + static_cast<int64_t>(max(phv, 0)) * kv_stride + (lane >> 5) * 8;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) vc[i] = *reinterpret_cast<const uint4*>(r + 16 * i);
+    // Two register buffers hold the K/V rows of two of the wave's blocks, so
+    // while block i is computed the loads of blocks i+1 and i+2 are in flight
+    // (the refill of a buffer is issued right after its last use).  Loads are
+    // unconditional -- a masked token reads row 0 -- so every block issues
+    // the same loads in the same order (req_to_token, V, K; pinned by
+    // scheduling barriers) and no wait ever drains the queue.  Masked K
+    // scores become -inf and masked V rows are zeroed before they reach LDS.
+    struct Buf {
+      uint4 k[2][4];  // K rows of tokens col and 16+col, 16-byte d-chunks 4s+quad
+      uint4 v[8];     // V row of token lane%32, 16-byte chunks lane/32 + 2i
+      int pk0, pk1, pv;
     };
     const int tk0 = col, tk1 = 16 + col, tv = lane & 31;  // tokens this lane loads
-    int blk = wave;
-    int pk0, pk1, pv;     // checked rows of the current block
-    int rk0, rk1, rv;     // raw rows of the next block
-    {
-      const int base = a + blk * kBlk;
-      pk0 = phys_ok(base + tk0, raw_row(base + tk0));
-      pk1 = phys_ok(base + tk1, raw_row(base + tk1));
-      pv = phys_ok(base + tv, raw_row(base + tv));
-      const int nbase = base + kWaves * kBlk;
-      rk0 = raw_row(nbase + tk0);
-      rk1 = raw_row(nbase + tk1);
-      rv = raw_row(nbase + tv);
-      __builtin_amdgcn_sched_barrier(0);
-      // same issue order as the loop body (req_to_token, V, K) and always
-      // issued, so the loop entry and the back edge agree on what is in flight
-      load_v(pv);
-      __builtin_amdgcn_sched_barrier(0);
-      load_k(pk0, pk1);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    for (; blk < nblk; blk += kWaves) {
-      const int base = a + blk * kBlk;
-      const int nbase = base + kWaves * kBlk;
-      // rows of the next block (their loads were issued one iteration ago);
-      // past the wave's last block they are -1 and the unconditional refills
-      // below re-read row 0 (a cache hit), which keeps the load count of
-      // every iteration equal so the compiler never has to drain the queue.
-      const int nk0 = phys_ok(nbase + tk0, rk0);
-      const int nk1 = phys_ok(nbase + tk1, rk1);
-      const int nv = phys_ok(nbase + tv, rv);
-      // raw rows two blocks ahead.  The scheduling barriers keep the issue
-      // order req_to_token -> V -> K within an iteration: the loads retire in
-      // order, so consuming the row indices next iteration then never waits
-      // for the K/V loads issued after them.
-      {
-        const int fbase = nbase + kWaves * kBlk;
-        rk0 = raw_row(fbase + tk0);
-        rk1 = raw_row(fbase + tk1);
-        rv = raw_row(fbase + tv);
+    // Plain (temporal) loads: the two 64-byte halves of each 128-byte line of
+    // a K row arrive through different instructions, and the non-temporal
+    // policy measured 1.4x slower here because it refetches the line.
+    auto load_k = [&](Buf& B) {
+      const uint16_t* r0 = kbase + static_cast<int64_t>(max(B.pk0, 0)) * kv_stride + quad * 8;
+      const uint16_t* r1 = kbase + static_cast<int64_t>(max(B.pk1, 0)) * kv_stride + quad * 8;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        B.k[0][s] = *reinterpret_cast<const uint4*>(r0 + 32 * s);
+        B.k[1][s] = *reinterpret_cast<const uint4*>(r1 + 32 * s);
       }
+    };
+    auto load_v = [&](Buf& B) {
+      const uint16_t* r = vbase + static_cast<int64_t>(max(B.pv, 0)) * kv_stride + (lane >> 5) * 8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) B.v[i] = *reinterpret_cast<const uint4*>(r + 16 * i);
+    };
+    auto block_base = [&](int k) { return a + (wave + kWaves * k) * kBlk; };  // k-th block of this wave
+    Buf A[kDepth];
+    int rk0, rk1, rv;  // raw rows of the block kDepth ahead of the one being computed
+    {
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) {
+        const int bd = block_base(d);
+        A[d].pk0 = phys_ok(bd + tk0, raw_row(bd + tk0));
+        A[d].pk1 = phys_ok(bd + tk1, raw_row(bd + tk1));
+        A[d].pv = phys_ok(bd + tv, raw_row(bd + tv));
+      }
+      const int bn = block_base(kDepth);
+      rk0 = raw_row(bn + tk0);
+      rk1 = raw_row(bn + tk1);
+      rv = raw_row(bn + tv);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) {
+        load_v(A[d]);
+        __builtin_amdgcn_sched_barrier(0);
+        load_k(A[d]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+
+    // Computes the wave's k-th block from buffer B, refilling B with block k+kDepth.
+    auto process = [&](Buf& B, int k) {
+      const int base = block_base(k);
+      const int b2 = block_base(k + kDepth), b3 = block_base(k + kDepth + 1);
+      const int n0 = phys_ok(b2 + tk0, rk0), n1 = phys_ok(b2 + tk1, rk1), nv = phys_ok(b2 + tv, rv);
+      rk0 = raw_row(b3 + tk0);
+      rk1 = raw_row(b3 + tk1);
+      rv = raw_row(b3 + tv);
       __builtin_amdgcn_sched_barrier(0);
       // validity of the 32 tokens of this block, as seen by the K loads
-      const uint64_t vm0 = __ballot(pk0 >= 0);
-      const uint64_t vm1 = __ballot(pk1 >= 0);
-      // stage this block's V rows into the wave's LDS tile, then refill vc
+      const uint64_t vm0 = __ballot(B.pk0 >= 0);
+      const uint64_t vm1 = __ballot(B.pk1 >= 0);
+      // stage the block's V rows into the wave's LDS tile, then refill
       {
         const int swz = 2 * ((tv >> 2) & 3);
-        const uint32_t keep = pv >= 0 ? 0xffffffffu : 0u;
+        const uint32_t keep = B.pv >= 0 ? 0xffffffffu : 0u;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          uint4 w = vc[i];
+          uint4 w = B.v[i];
           w.x &= keep;
           w.y &= keep;
           w.z &= keep;
@@ -1026,24 +1036,25 @@ __global__ void __launch_bounds__(kBlock) span_attention_mfma_kernel(AttnParams 
           s_v[wave][tv * 16 + (((lane >> 5) + 2 * i) ^ swz)] = w;
         }
       }
-      load_v(nv);
       __builtin_amdgcn_sched_barrier(0);
-
-      // S^T = K Q^T for tokens [base, base + 32), then refill kc
+      B.pv = nv;
+      load_v(B);
+      __builtin_amdgcn_sched_barrier(0);
+      // S^T = K Q^T for the block's 32 tokens, then refill
       f32x4_t st[2];
 #pragma unroll
       for (int tile = 0; tile < 2; ++tile) {
         f32x4_t c4 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-          c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kc[tile][s]), qb[s], c4, 0, 0, 0);
+          c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(B.k[tile][s]),
+                                                      as_bf16x8(s_q[col * 16 + 4 * s + quad]), c4, 0, 0, 0);
         st[tile] = c4;
       }
-      load_k(nk0, nk1);
+      B.pk0 = n0;
+      B.pk1 = n1;
+      load_k(B);
       __builtin_amdgcn_sched_barrier(0);
-      pk0 = nk0;
-      pk1 = nk1;
-      pv = nv;
 
       // scale, mask, online softmax (lane-local except the block max)
       float sv[8];
@@ -1103,6 +1114,15 @@ __global__ void __launch_bounds__(kBlock) span_attention_mfma_kernel(AttnParams 
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
+    };
+
+    // the wave's blocks, kDepth at a time; a trailing partial group is padded
+    // with fully masked blocks (all positions >= b) so every buffer follows
+    // the same pattern
+    const int my_blocks = wave < nblk ? ceil_div(nblk - wave, kWaves) : 0;
+    for (int k = 0; k < my_blocks; k += kDepth) {
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) process(A[d], k + d);
     }
 
     // ---- wave result -> LDS, then combine the four waves ----
@@ -1175,31 +1195,51 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
     }
   }
 
-  auto merge_task = [&](int j) {
-    const int64_t slot = static_cast<int64_t>(g) * p.cap + j;
+  // Folds partials j0..j1-1 into the per-element states.  Partials are read
+  // kBatch at a time (all loads issued before any use) and folded with one
+  // max/exp per partial; an empty partial (lse = -inf) has weight 0, which is
+  // the reference's skip rule (DECODE:866-890).
+  constexpr int kBatch = 8;
+  auto merge_range = [&](int j0, int j1) {
+    for (int jb = j0; jb < j1; jb += kBatch) {
+      float pl[kBatch][kElems], po[kBatch][kElems];
 #pragma unroll
-    for (int k = 0; k < kElems; ++k) {
-      if (!own[k]) continue;
-      const float ol = p.partial_lse[slot * G + hh[k]];
-      if (!isfinite(ol)) continue;  // DECODE:866-890: an empty partial is skipped
-      const int64_t oi = static_cast<int64_t>(g) * p.o_group_stride + (static_cast<int64_t>(j) * G + hh[k]) * kHeadDim + dd[k];
-      const float ov = p.partial_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p.partial_o)[oi])
-                                      : static_cast<const float*>(p.partial_o)[oi];
-      if (!isfinite(lse[k])) {
-        lse[k] = ol;
-        acc[k] = ov;
-        continue;
+      for (int u = 0; u < kBatch; ++u) {
+        const int j = jb + u;
+        const bool jv = j < j1;
+        const int64_t slot = static_cast<int64_t>(g) * p.cap + (jv ? j : j0);
+#pragma unroll
+        for (int k = 0; k < kElems; ++k) {
+          const int64_t oi = static_cast<int64_t>(g) * p.o_group_stride +
+                             (static_cast<int64_t>(jv ? j : j0) * G + hh[k]) * kHeadDim + dd[k];
+          const float l_raw = p.partial_lse[slot * G + hh[k]];
+          const float o_raw = p.partial_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p.partial_o)[oi])
+                                             : static_cast<const float*>(p.partial_o)[oi];
+          pl[u][k] = (jv && own[k]) ? l_raw : -INFINITY;
+          po[u][k] = o_raw;
+        }
       }
-      const float mx = fmaxf(lse[k], ol);
-      const float w1 = __expf(lse[k] - mx);
-      const float w2 = __expf(ol - mx);
-      const float den = w1 + w2;
-      acc[k] = (w1 * acc[k] + w2 * ov) / den;
-      lse[k] = mx + __logf(den);
+#pragma unroll
+      for (int k = 0; k < kElems; ++k) {
+        float mx = lse[k];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) mx = fmaxf(mx, pl[u][k]);
+        if (!isfinite(mx)) continue;  // state and every partial empty
+        float wsum = isfinite(lse[k]) ? __expf(lse[k] - mx) : 0.0f;
+        float o = isfinite(lse[k]) ? wsum * acc[k] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          const float w = isfinite(pl[u][k]) ? __expf(pl[u][k] - mx) : 0.0f;
+          wsum += w;
+          o = fmaf(w, po[u][k], o);
+        }
+        acc[k] = o / wsum;
+        lse[k] = mx + __logf(wsum);
+      }
     }
   };
 
-  for (int j = n_sink; j < n_sink + n_band; ++j) merge_task(j);
+  merge_range(n_sink, n_sink + n_band);
   __syncthreads();  // every entry read above precedes the ring write below
 
   if (ready) {
@@ -1215,8 +1255,8 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
     }
   }
 
-  for (int j = 0; j < n_sink; ++j) merge_task(j);
-  for (int j = n_sink + n_band; j < n_sink + n_band + n_tail; ++j) merge_task(j);
+  merge_range(0, n_sink);
+  merge_range(n_sink + n_band, n_sink + n_band + n_tail);
 
 #pragma unroll
   for (int k = 0; k < kElems; ++k) {
@@ -1254,7 +1294,7 @@ int fail(int code, const char* fmt, ...) {
 
 struct DeviceInfo {
   int cus = 0;
-  int attn_blocks_per_cu[2][kMaxGroup + 1] = {};
+  int attn_blocks_per_cu[3][kMaxGroup + 1] = {};
 };
 
 // MAC_AMD_ATTN_IMPL=valu selects the VALU span-attention kernel; the default
@@ -1262,7 +1302,9 @@ struct DeviceInfo {
 int attn_impl() {
   static const int impl = [] {
     const char* e = std::getenv("MAC_AMD_ATTN_IMPL");
-    return (e != nullptr && std::strcmp(e, "valu") == 0) ? 0 : 1;
+    if (e != nullptr && std::strcmp(e, "valu") == 0) return 0;
+    if (e != nullptr && std::strcmp(e, "mfma2") == 0) return 2;
+    return 1;
   }();
   return impl;
 }
@@ -1272,8 +1314,9 @@ DeviceInfo g_dev[64];
 
 template <int G>
 void* attn_kernel_ptr(int impl) {
-  return impl ? reinterpret_cast<void*>(&span_attention_mfma_kernel<G>)
-              : reinterpret_cast<void*>(&span_attention_kernel<G>);
+  if (impl == 2) return reinterpret_cast<void*>(&span_attention_mfma_kernel<G, 2>);
+  if (impl == 1) return reinterpret_cast<void*>(&span_attention_mfma_kernel<G, 1>);
+  return reinterpret_cast<void*>(&span_attention_kernel<G>);
 }
 
 int attn_residency(int dev, int G, int impl, int* cus, int* per_cu) {
@@ -1313,8 +1356,10 @@ int launch_all(const DecideParams& dp, const AttnParams& ap, const MergeParams& 
   hipLaunchKernelGGL(match_decide_kernel<G>, dim3(NG), dim3(kBlock), 0, stream, dp);
   MAC_HIP(hipGetLastError());
   if (ev) MAC_HIP(hipEventRecord(ev[1], stream));
-  if (impl)
-    hipLaunchKernelGGL(span_attention_mfma_kernel<G>, dim3(attn_grid), dim3(kBlock), 0, stream, ap);
+  if (impl == 2)
+    hipLaunchKernelGGL((span_attention_mfma_kernel<G, 2>), dim3(attn_grid), dim3(kBlock), 0, stream, ap);
+  else if (impl == 1)
+    hipLaunchKernelGGL((span_attention_mfma_kernel<G, 1>), dim3(attn_grid), dim3(kBlock), 0, stream, ap);
   else
     hipLaunchKernelGGL(span_attention_kernel<G>, dim3(attn_grid), dim3(kBlock), 0, stream, ap);
   MAC_HIP(hipGetLastError());
