@@ -46,7 +46,9 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
+#include <tuple>
 
 #include "mac_attention_amd.h"
 #include "mac_common.h"
@@ -678,7 +680,7 @@ template <int G>
 __global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
   constexpr int U = 2;                 // tokens per row per iteration
   constexpr int kStep = kWaves * 4 * U;  // tokens per workgroup iteration
-  __shared__ int s_off[kMaxPlanGroups + 1];
+  extern __shared__ int s_off[];  // NG + 1 task offsets (dynamic)
   __shared__ int s_tmp[kWaves];
   __shared__ float s_o[kWaves][G][kHeadDim];
   __shared__ float s_ml[kWaves][G][2];
@@ -855,52 +857,57 @@ __global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
 
 // ------------------------------------------------- MFMA span attention ----
 //
-// Same plan and task list as span_attention_kernel; the per-task inner loop
-// runs both contractions on v_mfma_f32_16x16x32_bf16 (gfx950), one 64-lane
-// wave per 32-token block (waves take blocks wave, wave+4, ...):
+// Same plan and task list as span_attention_kernel.  One 64-lane wave owns a
+// 32-token block at a time (waves take blocks wave, wave+4, ...):
 //
-//   S^T[t][g] = sum_d K[t][d] Q[g][d]     A = K rows straight from HBM (each
-//       lane loads 16 B of two token rows per k-step, d-chunk 4s + lane/16),
-//       B = Q^T from registers, two 16-token tiles x 4 k-steps;
-//   O^T[d][g] += sum_t V[t][d] P[g][t]    A = V^T gathered from an LDS copy
-//       of the block's V rows, B = P, which is exactly the lane's own S^T
-//       values converted to bf16 (token order of the k axis chosen to match),
-//       8 tiles of 16 dims.
-//
-// Lane l therefore owns query head g = l % 16 for both the softmax state and
-// the O^T accumulators (dims 16*dt + 4*(l/16) + r), so the online-softmax
-// rescale is lane-local.  Heads g >= G are padding (masked to -inf).
-//
-// The V tile is stored row-major per token with 16-byte chunk c of token t at
-// position c ^ 2*((t >> 2) & 3): the four lane groups of one gather then hit
-// disjoint LDS banks.
+//  * Loads: each 256-byte K or V row is read by 16 consecutive lanes (lane
+//    l reads 16-byte chunk l%16 of the row of token 8*(l/16) + i in load i),
+//    so every load instruction covers whole 128-byte lines, with the
+//    non-temporal policy (the rows are read once per step).  Measured on
+//    MI355X this streams ~12% faster than loading the MFMA operands straight
+//    from HBM, whose layout splits lines across instructions.  The block
+//    after the current one is always in flight in registers; its
+//    req_to_token entries are loaded one block earlier still.
+//  * The rows are staged in two 8 KiB per-wave LDS tiles.  In the K tile,
+//    16-byte chunk c of token t sits at position c ^ (t & 15), so the MFMA
+//    A-operand reads of 16 tokens hit 16 different bank groups; in the V tile
+//    at c ^ 2*((t >> 2) & 3), so the column gathers of 4 token groups do.
+//  * S^T[t][g] = sum_d K[t][d] Q[g][d] and O^T[d][g] += sum_t V[t][d] P[g][t]
+//    both run on v_mfma_f32_16x16x32_bf16.  The lane holding head g = l%16
+//    keeps that head's softmax state, its scores (already the B operand of
+//    the PV product after conversion to bf16, by the choice of token order on
+//    the k axis) and its 32 O^T accumulators, so the online-softmax rescale is
+//    lane-local.  Heads g >= G are zero padding rows of the 16-wide MFMA.
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& w) { return __builtin_bit_cast(bf16x8_t, w); }
 
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 // 16-byte non-temporal (streaming) global load.
 __device__ __forceinline__ uint4 load_stream16(const uint16_t* ptr) {
   return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(ptr)));
 }
 
-template <int G, int kDepth>
+template <int G>
 __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnParams p) {
   constexpr int kBlk = 32;  // tokens per wave block
-  __shared__ int s_off[kMaxPlanGroups + 1];
+  extern __shared__ int s_off[];  // NG + 1 task offsets (dynamic)
   __shared__ int s_tmp[kWaves];
+  __shared__ uint4 s_k[kWaves][kBlk * 16];
   __shared__ uint4 s_v[kWaves][kBlk * 16];
   __shared__ uint4 s_q[16 * 16];
-  __shared__ float s_o[kWaves][G][kHeadDim];
   __shared__ float s_ml[kWaves][G][2];
+  // the per-wave o of the task epilogue reuses the K tiles
+  static_assert(sizeof(float) * kWaves * G * kHeadDim <= sizeof(uint4) * kWaves * kBlk * 16, "s_o alias");
+  auto s_o = reinterpret_cast<float (*)[G][kHeadDim]>(&s_k[0][0]);
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) control flow
   const int lane = tid & 63;
   const int quad = lane >> 4;  // lane / 16
-  const int col = lane & 15;   // lane % 16: token row of the K operand, head of the outputs
+  const int col = lane & 15;   // lane % 16
   const int NG = p.s.N * p.s.Hkv;
   const int W = gridDim.x;
   int total_tasks = 0, chunk = 0;
@@ -910,23 +917,22 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
   const int Hkv = p.s.Hkv;
   const int64_t kv_stride = static_cast<int64_t>(Hkv) * kHeadDim;
   const bool head_ok = col < G;
-  uint16_t* vtile = reinterpret_cast<uint16_t*>(&s_v[wave][0]);
+  const uint16_t* vtile = reinterpret_cast<const uint16_t*>(&s_v[wave][0]);
+  // load-side token of load i for this lane: 8*quad + i; chunk: col
 
   for (int t = blockIdx.x; t < total_tasks; t += W) {
     const TaskInfo ti = decode_task(p, s_off, NG, chunk, t);
     const int n = ti.n, hkv = ti.hkv, a = ti.a, b = ti.b, P = ti.P;
     const int32_t* r2t = p.req_to_token + static_cast<int64_t>(ti.req_ok ? ti.req : 0) * p.s.r2t_stride;
-    const uint16_t* kbase = p.k_buffer + static_cast<int64_t>(hkv) * kHeadDim;
-    const uint16_t* vbase = p.v_buffer + static_cast<int64_t>(hkv) * kHeadDim;
+    const uint16_t* kbase = p.k_buffer + static_cast<int64_t>(hkv) * kHeadDim + col * 8;
+    const uint16_t* vbase = p.v_buffer + static_cast<int64_t>(hkv) * kHeadDim + col * 8;
 
-    // B operand of QK^T is Q^T: lane (quad, col) needs Q[col][8*(4s+quad) .. +8]
-    // for k-step s.  The group's queries are staged once per task in LDS
-    // (rows g >= G zero) and re-read per block, which keeps 16 VGPRs free for
-    // the second K/V buffer.
+    // Q of the group's heads (rows g >= G zero), staged once per task; lane
+    // (quad, col) reads Q[col][8*(4s+quad) .. +8] as the B operand of k-step s.
     int head_begin = 0;
     {
       const int64_t qoff = static_cast<int64_t>(n) * Hq * kHeadDim + static_cast<int64_t>(hkv) * G * kHeadDim;
-      for (int e = tid; e < 16 * 16; e += kBlock) {  // 16 rows x 16 chunks of 16 bytes
+      for (int e = tid; e < 16 * 16; e += kBlock) {
         const int g = e >> 4, c = e & 15;
         uint4 w = make_uint4(0, 0, 0, 0);
         if (g < G) w = *reinterpret_cast<const uint4*>(p.q_post + qoff + g * kHeadDim + c * 8);
@@ -935,11 +941,9 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
       if (ti.band && head_ok) head_begin = p.head_rect_start[static_cast<int64_t>(n) * Hq + hkv * G + col];
       __syncthreads();
     }
-    // Physical rows are looked up two blocks ahead: raw_row() only issues the
-    // req_to_token load (unconditionally, index clamped into the row), and
-    // the value is checked one iteration later by phys_ok(), so no wait on
-    // that load ever forces the in-flight K/V loads to drain.  A position
-    // outside the task or a row out of range yields -1 (masked token).
+    // Physical rows: raw_row() only issues the req_to_token load (index
+    // clamped into the row); phys_ok() checks it one block later, so waiting
+    // for it never drains the K/V loads issued after it.  -1 = masked token.
     const int r2t_last = max(min(P, p.s.r2t_stride) - 1, 0);
     const int cur_row = (ti.cur_loc >= 0 && ti.cur_loc < p.s.pool_tokens) ? static_cast<int>(ti.cur_loc) : -1;
     const unsigned pool_rows = static_cast<unsigned>(min(p.s.pool_tokens, static_cast<int64_t>(INT_MAX)));
@@ -948,125 +952,97 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
       const int ph = pos == P ? cur_row : raw;
       return (pos < b && ti.req_ok && static_cast<unsigned>(ph) < pool_rows) ? ph : -1;
     };
+    auto block_base = [&](int k) { return a + (wave + kWaves * k) * kBlk; };  // k-th block of this wave
 
     float m = kNegBig, l = 0.0f;
     f32x4_t acc[8];
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int nblk = ceil_div(b - a, kBlk);
-    // Two register buffers hold the K/V rows of two of the wave's blocks, so
-    // while block i is computed the loads of blocks i+1 and i+2 are in flight
-    // (the refill of a buffer is issued right after its last use).  Loads are
-    // unconditional -- a masked token reads row 0 -- so every block issues
-    // the same loads in the same order (req_to_token, V, K; pinned by
-    // scheduling barriers) and no wait ever drains the queue.  Masked K
-    // scores become -inf and masked V rows are zeroed before they reach LDS.
-    struct Buf {
-      uint4 k[2][4];  // K rows of tokens col and 16+col, 16-byte d-chunks 4s+quad
-      uint4 v[8];     // V row of token lane%32, 16-byte chunks lane/32 + 2i
-      int pk0, pk1, pv;
-    };
-    const int tk0 = col, tk1 = 16 + col, tv = lane & 31;  // tokens this lane loads
-    // Plain (temporal) loads: the two 64-byte halves of each 128-byte line of
-    // a K row arrive through different instructions, and the non-temporal
-    // policy measured 1.4x slower here because it refetches the line.
-    auto load_k = [&](Buf& B) {
-      const uint16_t* r0 = kbase + static_cast<int64_t>(max(B.pk0, 0)) * kv_stride + quad * 8;
-      const uint16_t* r1 = kbase + static_cast<int64_t>(max(B.pk1, 0)) * kv_stride + quad * 8;
+    uint4 kr[8], vr[8];  // rows of tokens 8*quad + i, chunk col (current block)
+    int ph[8];           // checked rows of the current block
+    int raw[8];          // raw rows of the next block
+    auto issue = [&](const int (&rows)[8]) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        B.k[0][s] = *reinterpret_cast<const uint4*>(r0 + 32 * s);
-        B.k[1][s] = *reinterpret_cast<const uint4*>(r1 + 32 * s);
-      }
-    };
-    auto load_v = [&](Buf& B) {
-      const uint16_t* r = vbase + static_cast<int64_t>(max(B.pv, 0)) * kv_stride + (lane >> 5) * 8;
+      for (int i = 0; i < 8; ++i) vr[i] = load_stream16(vbase + static_cast<int64_t>(max(rows[i], 0)) * kv_stride);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) B.v[i] = *reinterpret_cast<const uint4*>(r + 16 * i);
+      for (int i = 0; i < 8; ++i) kr[i] = load_stream16(kbase + static_cast<int64_t>(max(rows[i], 0)) * kv_stride);
     };
-    auto block_base = [&](int k) { return a + (wave + kWaves * k) * kBlk; };  // k-th block of this wave
-    Buf A[kDepth];
-    int rk0, rk1, rv;  // raw rows of the block kDepth ahead of the one being computed
     {
+      const int b0 = block_base(0), b1 = block_base(1);
 #pragma unroll
-      for (int d = 0; d < kDepth; ++d) {
-        const int bd = block_base(d);
-        A[d].pk0 = phys_ok(bd + tk0, raw_row(bd + tk0));
-        A[d].pk1 = phys_ok(bd + tk1, raw_row(bd + tk1));
-        A[d].pv = phys_ok(bd + tv, raw_row(bd + tv));
-      }
-      const int bn = block_base(kDepth);
-      rk0 = raw_row(bn + tk0);
-      rk1 = raw_row(bn + tk1);
-      rv = raw_row(bn + tv);
+      for (int i = 0; i < 8; ++i) ph[i] = phys_ok(b0 + 8 * quad + i, raw_row(b0 + 8 * quad + i));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) raw[i] = raw_row(b1 + 8 * quad + i);
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int d = 0; d < kDepth; ++d) {
-        load_v(A[d]);
-        __builtin_amdgcn_sched_barrier(0);
-        load_k(A[d]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      issue(ph);
+      __builtin_amdgcn_sched_barrier(0);
     }
 
-    // Computes the wave's k-th block from buffer B, refilling B with block k+kDepth.
-    auto process = [&](Buf& B, int k) {
+    const int nblk = ceil_div(b - a, kBlk);
+    const int my_blocks = wave < nblk ? ceil_div(nblk - wave, kWaves) : 0;
+    for (int k = 0; k < my_blocks; ++k) {
       const int base = block_base(k);
-      const int b2 = block_base(k + kDepth), b3 = block_base(k + kDepth + 1);
-      const int n0 = phys_ok(b2 + tk0, rk0), n1 = phys_ok(b2 + tk1, rk1), nv = phys_ok(b2 + tv, rv);
-      rk0 = raw_row(b3 + tk0);
-      rk1 = raw_row(b3 + tk1);
-      rv = raw_row(b3 + tv);
-      __builtin_amdgcn_sched_barrier(0);
-      // validity of the 32 tokens of this block, as seen by the K loads
-      const uint64_t vm0 = __ballot(B.pk0 >= 0);
-      const uint64_t vm1 = __ballot(B.pk1 >= 0);
-      // stage the block's V rows into the wave's LDS tile, then refill
-      {
-        const int swz = 2 * ((tv >> 2) & 3);
-        const uint32_t keep = B.pv >= 0 ? 0xffffffffu : 0u;
+      const int b1 = block_base(k + 1), b2 = block_base(k + 2);
+      int nph[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          uint4 w = B.v[i];
-          w.x &= keep;
-          w.y &= keep;
-          w.z &= keep;
-          w.w &= keep;
-          s_v[wave][tv * 16 + (((lane >> 5) + 2 * i) ^ swz)] = w;
-        }
+      for (int i = 0; i < 8; ++i) nph[i] = phys_ok(b1 + 8 * quad + i, raw[i]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) raw[i] = raw_row(b2 + 8 * quad + i);
+      __builtin_amdgcn_sched_barrier(0);
+      // token validity of this block: bit t set if token t has a row
+      uint32_t vmask = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint64_t bal = __ballot(ph[i] >= 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) vmask |= static_cast<uint32_t>((bal >> (16 * r)) & 1) << (8 * r + i);
+      }
+      // stage K and V rows (V of masked tokens zeroed) into the wave's tiles
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int tok = 8 * quad + i;
+        const uint32_t keep = ph[i] >= 0 ? 0xffffffffu : 0u;
+        uint4 w = vr[i];
+        w.x &= keep;
+        w.y &= keep;
+        w.z &= keep;
+        w.w &= keep;
+        s_k[wave][tok * 16 + (col ^ (tok & 15))] = kr[i];
+        s_v[wave][tok * 16 + (col ^ (2 * ((tok >> 2) & 3)))] = w;
       }
       __builtin_amdgcn_sched_barrier(0);
-      B.pv = nv;
-      load_v(B);
+      // the next block's rows go in flight while this block is computed
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ph[i] = nph[i];
+      issue(ph);
       __builtin_amdgcn_sched_barrier(0);
-      // S^T = K Q^T for the block's 32 tokens, then refill
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+      // S^T = K Q^T for the block's 32 tokens
       f32x4_t st[2];
 #pragma unroll
       for (int tile = 0; tile < 2; ++tile) {
         f32x4_t c4 = {0.0f, 0.0f, 0.0f, 0.0f};
+        const int tok = 16 * tile + col;
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-          c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(B.k[tile][s]),
+          c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(s_k[wave][tok * 16 + ((4 * s + quad) ^ col)]),
                                                       as_bf16x8(s_q[col * 16 + 4 * s + quad]), c4, 0, 0, 0);
         st[tile] = c4;
       }
-      B.pk0 = n0;
-      B.pk1 = n1;
-      load_k(B);
-      __builtin_amdgcn_sched_barrier(0);
 
       // scale, mask, online softmax (lane-local except the block max)
       float sv[8];
       float bmax = kNegBig;
 #pragma unroll
       for (int tile = 0; tile < 2; ++tile) {
-        const uint64_t vm = tile ? vm1 : vm0;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int tok = 4 * quad + r;  // token within the tile
-          const int pos = base + 16 * tile + tok;
-          const bool ok = head_ok && ((vm >> tok) & 1) && pos >= head_begin;
+          const int tok = 16 * tile + 4 * quad + r;
+          const bool ok = head_ok && ((vmask >> tok) & 1) && base + tok >= head_begin;
           const float x = ok ? st[tile][r] * p.q_scale : -INFINITY;
           sv[4 * tile + r] = x;
           bmax = fmaxf(bmax, x);
@@ -1096,10 +1072,7 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
         pb[e] = static_cast<__bf16>(pe);
       }
       l += psum;
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      // O^T += V^T P^T: A operand gathered from the LDS tile
+      // O^T += V^T P^T: A operand gathered from the V tile
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         const int chunk_pos = (2 * (dt ^ quad) + (col >> 3));
@@ -1114,20 +1087,12 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
-    };
-
-    // the wave's blocks, kDepth at a time; a trailing partial group is padded
-    // with fully masked blocks (all positions >= b) so every buffer follows
-    // the same pattern
-    const int my_blocks = wave < nblk ? ceil_div(nblk - wave, kWaves) : 0;
-    for (int k = 0; k < my_blocks; k += kDepth) {
-#pragma unroll
-      for (int d = 0; d < kDepth; ++d) process(A[d], k + d);
     }
 
-    // ---- wave result -> LDS, then combine the four waves ----
+    // ---- wave result -> LDS (over the K tiles), then combine the four waves ----
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
+    __syncthreads();  // every wave is done with its K tile
     if (head_ok) {
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt)
@@ -1292,41 +1257,39 @@ int fail(int code, const char* fmt, ...) {
     if (e_ != hipSuccess) return fail(MAC_ERR_HIP, "%s: %s", #call, hipGetErrorString(e_)); \
   } while (0)
 
-struct DeviceInfo {
-  int cus = 0;
-  int attn_blocks_per_cu[3][kMaxGroup + 1] = {};
-};
-
 // MAC_AMD_ATTN_IMPL=valu selects the VALU span-attention kernel; the default
 // is the MFMA kernel.  Read once per process.
 int attn_impl() {
   static const int impl = [] {
     const char* e = std::getenv("MAC_AMD_ATTN_IMPL");
-    if (e != nullptr && std::strcmp(e, "valu") == 0) return 0;
-    if (e != nullptr && std::strcmp(e, "mfma2") == 0) return 2;
-    return 1;
+    return (e != nullptr && std::strcmp(e, "valu") == 0) ? 0 : 1;
   }();
   return impl;
 }
 
-std::mutex g_dev_mu;
-DeviceInfo g_dev[64];
-
 template <int G>
 void* attn_kernel_ptr(int impl) {
-  if (impl == 2) return reinterpret_cast<void*>(&span_attention_mfma_kernel<G, 2>);
-  if (impl == 1) return reinterpret_cast<void*>(&span_attention_mfma_kernel<G, 1>);
-  return reinterpret_cast<void*>(&span_attention_kernel<G>);
+  return impl ? reinterpret_cast<void*>(&span_attention_mfma_kernel<G>)
+              : reinterpret_cast<void*>(&span_attention_kernel<G>);
 }
 
-int attn_residency(int dev, int G, int impl, int* cus, int* per_cu) {
+// Compute units of the device and resident span-attention workgroups per CU
+// for a given kernel and dynamic LDS size, cached per process.
+std::mutex g_dev_mu;
+std::map<std::tuple<int, int, int, size_t>, int> g_blocks_per_cu;
+std::map<int, int> g_cus;
+
+int attn_residency(int dev, int G, int impl, size_t dyn_lds, int* cus, int* per_cu) {
   std::lock_guard<std::mutex> lk(g_dev_mu);
-  if (dev < 0 || dev >= 64) return fail(MAC_ERR_UNSUPPORTED, "device index %d out of range", dev);
-  DeviceInfo& di = g_dev[dev];
-  if (di.cus == 0) {
-    MAC_HIP(hipDeviceGetAttribute(&di.cus, hipDeviceAttributeMultiprocessorCount, dev));
+  auto ci = g_cus.find(dev);
+  if (ci == g_cus.end()) {
+    int n = 0;
+    MAC_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+    ci = g_cus.emplace(dev, n).first;
   }
-  if (di.attn_blocks_per_cu[impl][G] == 0) {
+  const auto key = std::make_tuple(dev, G, impl, dyn_lds);
+  auto bi = g_blocks_per_cu.find(key);
+  if (bi == g_blocks_per_cu.end()) {
     void* fn = nullptr;
     switch (G) {
       case 1: fn = attn_kernel_ptr<1>(impl); break;
@@ -1339,15 +1302,14 @@ int attn_residency(int dev, int G, int impl, int* cus, int* per_cu) {
       default: fn = attn_kernel_ptr<8>(impl); break;
     }
     int blocks = 0;
-    MAC_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kBlock, 0));
-    di.attn_blocks_per_cu[impl][G] = blocks > 0 ? blocks : 1;
+    MAC_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kBlock, dyn_lds));
+    bi = g_blocks_per_cu.emplace(key, blocks > 0 ? blocks : 1).first;
   }
-  *cus = di.cus;
-  *per_cu = di.attn_blocks_per_cu[impl][G];
+  *cus = ci->second;
+  *per_cu = bi->second;
   return MAC_OK;
 }
 
-// ev (optional): four events recorded before, between and after the kernels.
 template <int G>
 int launch_all(const DecideParams& dp, const AttnParams& ap, const MergeParams& mp, int attn_grid,
                int impl, hipStream_t stream, hipEvent_t* ev) {
@@ -1356,12 +1318,11 @@ int launch_all(const DecideParams& dp, const AttnParams& ap, const MergeParams& 
   hipLaunchKernelGGL(match_decide_kernel<G>, dim3(NG), dim3(kBlock), 0, stream, dp);
   MAC_HIP(hipGetLastError());
   if (ev) MAC_HIP(hipEventRecord(ev[1], stream));
-  if (impl == 2)
-    hipLaunchKernelGGL((span_attention_mfma_kernel<G, 2>), dim3(attn_grid), dim3(kBlock), 0, stream, ap);
-  else if (impl == 1)
-    hipLaunchKernelGGL((span_attention_mfma_kernel<G, 1>), dim3(attn_grid), dim3(kBlock), 0, stream, ap);
+  const size_t plan_lds = sizeof(int) * (static_cast<size_t>(NG) + 1);
+  if (impl)
+    hipLaunchKernelGGL(span_attention_mfma_kernel<G>, dim3(attn_grid), dim3(kBlock), plan_lds, stream, ap);
   else
-    hipLaunchKernelGGL(span_attention_kernel<G>, dim3(attn_grid), dim3(kBlock), 0, stream, ap);
+    hipLaunchKernelGGL(span_attention_kernel<G>, dim3(attn_grid), dim3(kBlock), plan_lds, stream, ap);
   MAC_HIP(hipGetLastError());
   if (ev) MAC_HIP(hipEventRecord(ev[2], stream));
   hipLaunchKernelGGL(merge_write_kernel<G>, dim3(NG), dim3(kBlock), 0, stream, mp);
@@ -1447,7 +1408,8 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   MAC_HIP(hipGetDevice(&dev));
   int cus = 0, per_cu = 0;
   const int impl = attn_impl();
-  int rc = attn_residency(dev, G, impl, &cus, &per_cu);
+  const size_t plan_lds = sizeof(int) * (static_cast<size_t>(N) * Hkv + 1);
+  int rc = attn_residency(dev, G, impl, plan_lds, &cus, &per_cu);
   if (rc != MAC_OK) return rc;
 
   Shape s{};
