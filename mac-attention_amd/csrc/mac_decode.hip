@@ -14,8 +14,8 @@
 //  2. span_attention  (persistent grid sized to the device's residency)
 //     Every workgroup plans the same task list from the group spans: the
 //     spans are cut into chunks of C tokens (C picked from the total token
-//     count so that the grid gets ~4 tasks per workgroup), and workgroup w
-//     takes tasks w, w+W, ...  A task streams the K/V rows of its chunk once
+//     count so that the grid gets ~12 tasks per workgroup), and workgroups
+//     fetch tasks through an atomic counter.  A task streams the K/V rows of its chunk once
 //     for all G query heads of the group (16 lanes per token row, 16-byte
 //     loads, two tokens per row in flight plus a one-iteration prefetch),
 //     masks band positions that precede a head's own band start, and keeps an
@@ -35,9 +35,10 @@
 //     number of tasks of group g (written by workgroup 0 of span_attention);
 //   match_dist/pos/slot[..., 0]: best (distance, position, slot) of the scan;
 //   partial_o / partial_lse: one (o, lse) partial per task and head;
-//   task_counts: [0] tasks, [1] tail tasks, [3] non-hit groups whose band needs
-//     more than one task, [4] chunk C, [5] non-hit groups, [6] full-fallback
-//     groups, [7]/[8] max band tasks of full-fallback / mixed groups.
+//   task_counts: [0] tasks, [1] tail tasks, [3] non-hit groups whose band spans
+//     more than one tile_tokens tile, [4] chunk C, [5] non-hit groups, [6]
+//     full-fallback groups, [7]/[8] max band tasks of full-fallback / mixed
+//     groups.
 
 #include <hip/hip_runtime.h>
 
@@ -88,6 +89,7 @@ struct DecideParams {
   int32_t* group_tail_begin;
   int32_t* group_tail_end;
   int32_t* group_mode;
+  int32_t* task_counter;  // zeroed here for span_attention's dynamic fetch
   int S, F, gen_min_limit, lookback_right, candidate_mode;
   float thr_dist;
   int mixed_group_fallback;
@@ -115,12 +117,14 @@ struct AttnParams {
   int32_t* group_chunk;   // complete_task_go
   int32_t* group_ntasks;  // complete_task_tile
   int32_t* task_counts;
+  int32_t* task_counter;   // complete_task_tile[N * Hkv]; zeroed by match_decide
   void* partial_o;
   float* partial_lse;
   int partial_bf16;
   int64_t o_group_stride;  // elements of partial_o per group
   int cap;                 // task slots per group
   int F;
+  int tile_tokens;  // the caller's tile size (task_counts[3] only)
   float q_scale;  // sm_scale * log2(e)
 };
 
@@ -418,6 +422,7 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
     p.head_rect_start[ho] = rect_start;
     p.head_new_end[ho] = new_end;
   }
+  if (lane == 0 && g == 0) *p.task_counter = 0;
   if (lane == 0) {
     const int64_t go = static_cast<int64_t>(n) * p.s.Hkv + hkv;
     p.group_mode[go] = mode;
@@ -485,11 +490,20 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* s_tmp, int& tota
   return base + x - v;
 }
 
+// Task granularity.  Workgroups fetch tasks dynamically, so about a dozen
+// tasks per workgroup bounds the end-of-kernel imbalance to a few percent,
+// while a task of at least kMinChunk tokens amortises its fixed cost (plan
+// lookup, Q staging, pipeline fill, partial write).
+constexpr int kTasksPerWorkgroup = 12;
+constexpr int kMinChunk = 256;
+constexpr int kMaxChunk = 16384;
+
 // Every workgroup of span_attention derives the same task list: the chunk C
-// from the total token count of all groups (about four tasks per workgroup,
-// a multiple of 64 tokens, at most 16384), then per-group task counts and
-// their exclusive prefix sums in s_off[0..NG).  Workgroup 0 also publishes the
-// per-group chunk and task counts for merge_write and the task counters.
+// from the total token count of all groups (kTasksPerWorkgroup tasks per
+// workgroup, a multiple of 64 tokens in [kMinChunk, kMaxChunk]), then
+// per-group task counts and their exclusive prefix sums in s_off[0..NG).
+// Workgroup 0 also publishes the per-group chunk and task counts for
+// merge_write and the task counters.
 __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& total_tasks_out,
                            int& chunk_out) {
   const int tid = threadIdx.x;
@@ -518,10 +532,10 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
     for (int w = 0; w < kWaves; ++w) tok += s_tok[w];
     __syncthreads();
   }
-  const long long target_tasks = 4LL * W;
+  const long long target_tasks = static_cast<long long>(kTasksPerWorkgroup) * W;
   int chunk = static_cast<int>((tok + target_tasks - 1) / target_tasks);
-  chunk = ceil_div(max(chunk, 64), 64) * 64;
-  chunk = min(chunk, 16384);
+  chunk = ceil_div(max(chunk, kMinChunk), 64) * 64;
+  chunk = min(chunk, kMaxChunk);
   int my_tasks = 0;
   for (int g = g_lo; g < g_hi; ++g) {
     GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, g, p.F, chunk, p.cap);
@@ -551,7 +565,9 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
       tails += sp.n_tail;
       if (mode != MAC_GROUP_MAC_HIT) {
         ++nonhit;
-        if (sp.n_band > 1) ++red;
+        // the reference's reduce condition with its default threshold: the
+        // band spans more than one tile of tile_tokens
+        if (sp.new_end - sp.band_begin > p.tile_tokens) ++red;
       }
       if (mode == MAC_GROUP_FULL_FALLBACK) {
         ++ff;
@@ -599,6 +615,17 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
 
   total_tasks_out = total_tasks;
   chunk_out = chunk;
+}
+
+// Dynamic task fetch: the counter is zeroed by match_decide, which runs
+// before this kernel on the same stream, so every step (and every graph
+// replay) starts from task 0.  Ends with a barrier, so the previous task's
+// LDS use is complete before the caller starts the next one.
+__device__ __forceinline__ int next_task(const AttnParams& p, int& s_task) {
+  __syncthreads();
+  if (threadIdx.x == 0) s_task = atomicAdd(p.task_counter, 1);
+  __syncthreads();
+  return s_task;
 }
 
 struct TaskInfo {
@@ -691,7 +718,6 @@ __global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
   const int row = lane >> 4;
   const int c = lane & 15;
   const int NG = p.s.N * p.s.Hkv;
-  const int W = gridDim.x;
 
   int total_tasks = 0, chunk = 0;
   plan_tasks(p, s_off, s_tmp, total_tasks, chunk);
@@ -700,7 +726,8 @@ __global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
   const int Hq = p.s.Hq;
   const int Hkv = p.s.Hkv;
   const int my_tok = wave * 4 + row;  // token offset inside each 16-token sub-block
-  for (int t = blockIdx.x; t < total_tasks; t += W) {
+  __shared__ int s_task;
+  for (int t = next_task(p, s_task); t < total_tasks; t = next_task(p, s_task)) {
     const TaskInfo ti = decode_task(p, s_off, NG, chunk, t);
     const int g = ti.g, j = ti.j, n = ti.n, hkv = ti.hkv, a = ti.a, b = ti.b, P = ti.P, req = ti.req;
     const bool band = ti.band, req_ok = ti.req_ok;
@@ -909,7 +936,6 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
   const int quad = lane >> 4;  // lane / 16
   const int col = lane & 15;   // lane % 16
   const int NG = p.s.N * p.s.Hkv;
-  const int W = gridDim.x;
   int total_tasks = 0, chunk = 0;
   plan_tasks(p, s_off, s_tmp, total_tasks, chunk);
 
@@ -920,7 +946,8 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
   const uint16_t* vtile = reinterpret_cast<const uint16_t*>(&s_v[wave][0]);
   // load-side token of load i for this lane: 8*quad + i; chunk: col
 
-  for (int t = blockIdx.x; t < total_tasks; t += W) {
+  __shared__ int s_task;
+  for (int t = next_task(p, s_task); t < total_tasks; t = next_task(p, s_task)) {
     const TaskInfo ti = decode_task(p, s_off, NG, chunk, t);
     const int n = ti.n, hkv = ti.hkv, a = ti.a, b = ti.b, P = ti.P;
     const int32_t* r2t = p.req_to_token + static_cast<int64_t>(ti.req_ok ? ti.req : 0) * p.s.r2t_stride;
@@ -1111,15 +1138,51 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
 
 // ============================================================ 3. merge ====
 
+// One workgroup per (group, query head); lane l of every wave owns dims
+// 2l, 2l+1.  The partials of a range are split over the four waves (wave w
+// takes j = j0 + w, j0 + w + 4, ..., eight loads in flight at a time), and the
+// four wave states are combined through LDS, so a full-fallback group with
+// hundreds of partials is merged in a fraction of the serial latency.
+// Order per head (DECODE:4280-4685): state <- cached entry (hit heads) (+)
+// band partials -> ring row (ready requests only) -> (+) sink and tail
+// partials -> out / out_lse.  An empty partial (lse = -inf) has weight 0,
+// the reference's skip rule (DECODE:866-890).
+struct MergeState {
+  float lse;   // natural log; -inf = empty
+  float o[2];  // normalised output of the owned dims
+};
+
+__device__ __forceinline__ void merge_into(MergeState& st, float lse2, float o0, float o1) {
+  if (!isfinite(lse2)) return;
+  if (!isfinite(st.lse)) {
+    st.lse = lse2;
+    st.o[0] = o0;
+    st.o[1] = o1;
+    return;
+  }
+  const float mx = fmaxf(st.lse, lse2);
+  const float w1 = __expf(st.lse - mx), w2 = __expf(lse2 - mx);
+  const float inv = 1.0f / (w1 + w2);
+  st.o[0] = (w1 * st.o[0] + w2 * o0) * inv;
+  st.o[1] = (w1 * st.o[1] + w2 * o1) * inv;
+  st.lse = mx + __logf(w1 + w2);
+}
+
 template <int G>
 __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
-  constexpr int kElems = (G * kHeadDim + kBlock - 1) / kBlock;
+  constexpr int kBatch = 8;
   const int g = blockIdx.x;
+  const int h = blockIdx.y;
   const int n = g / p.s.Hkv;
   const int hkv = g - n * p.s.Hkv;
   const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int d0 = 2 * lane;
   const int M = p.s.M;
   const int Hq = p.s.Hq;
+  const int hq = hkv * G + h;
+  const int64_t ho = static_cast<int64_t>(n) * Hq + hq;
   const int P = p.past_lens[n];
   const int req = p.req_ids[n];
   const bool ready = request_ready(p.cache_ready, p.cache_epoch, p.request_epoch, req, p.s.R);
@@ -1134,103 +1197,88 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
   const int n_band = ceil_div(new_end - band_begin, chunk);
   const int n_tail = ceil_div(kv_len - new_end, chunk);
 
-  float acc[kElems], lse[kElems];
-  int hh[kElems], dd[kElems];
-  bool own[kElems];
-#pragma unroll
-  for (int k = 0; k < kElems; ++k) {
-    const int e = tid + k * kBlock;
-    own[k] = e < G * kHeadDim;
-    hh[k] = own[k] ? e / kHeadDim : 0;
-    dd[k] = e - hh[k] * kHeadDim;
-    acc[k] = 0.0f;
-    lse[k] = -INFINITY;
-    if (own[k]) {
-      const int hq = hkv * G + hh[k];
-      const int64_t ho = static_cast<int64_t>(n) * Hq + hq;
-      const int mslot = p.head_match_slot[ho];
-      if (p.head_hit[ho] != 0 && mslot >= 0 && req >= 0 && req < p.s.R) {
-        const int64_t rowi = (static_cast<int64_t>(req) * M + mslot) * Hq + hq;
-        const float pl = p.lse_cache[rowi];
-        if (isfinite(pl)) {
-          lse[k] = pl;
-          acc[k] = bf16_to_f32(p.attn_cache[rowi * kHeadDim + dd[k]]);
-        }
-      }
-    }
-  }
+  __shared__ float s_o[kWaves][kHeadDim];
+  __shared__ float s_l[kWaves];
 
-  // Folds partials j0..j1-1 into the per-element states.  Partials are read
-  // kBatch at a time (all loads issued before any use) and folded with one
-  // max/exp per partial; an empty partial (lse = -inf) has weight 0, which is
-  // the reference's skip rule (DECODE:866-890).
-  constexpr int kBatch = 8;
-  auto merge_range = [&](int j0, int j1) {
-    for (int jb = j0; jb < j1; jb += kBatch) {
-      float pl[kBatch][kElems], po[kBatch][kElems];
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int j = jb + u;
-        const bool jv = j < j1;
-        const int64_t slot = static_cast<int64_t>(g) * p.cap + (jv ? j : j0);
-#pragma unroll
-        for (int k = 0; k < kElems; ++k) {
-          const int64_t oi = static_cast<int64_t>(g) * p.o_group_stride +
-                             (static_cast<int64_t>(jv ? j : j0) * G + hh[k]) * kHeadDim + dd[k];
-          const float l_raw = p.partial_lse[slot * G + hh[k]];
-          const float o_raw = p.partial_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p.partial_o)[oi])
-                                             : static_cast<const float*>(p.partial_o)[oi];
-          pl[u][k] = (jv && own[k]) ? l_raw : -INFINITY;
-          po[u][k] = o_raw;
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < kElems; ++k) {
-        float mx = lse[k];
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) mx = fmaxf(mx, pl[u][k]);
-        if (!isfinite(mx)) continue;  // state and every partial empty
-        float wsum = isfinite(lse[k]) ? __expf(lse[k] - mx) : 0.0f;
-        float o = isfinite(lse[k]) ? wsum * acc[k] : 0.0f;
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-          const float w = isfinite(pl[u][k]) ? __expf(pl[u][k] - mx) : 0.0f;
-          wsum += w;
-          o = fmaf(w, po[u][k], o);
-        }
-        acc[k] = o / wsum;
-        lse[k] = mx + __logf(wsum);
-      }
+  auto load_partial = [&](int j, float& lse2, float& o0, float& o1) {
+    const int64_t slot = static_cast<int64_t>(g) * p.cap + j;
+    lse2 = p.partial_lse[slot * G + h];
+    const int64_t oi = static_cast<int64_t>(g) * p.o_group_stride + (static_cast<int64_t>(j) * G + h) * kHeadDim + d0;
+    if (p.partial_bf16) {
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(p.partial_o) + oi);
+      o0 = bf16_lo(w);
+      o1 = bf16_hi(w);
+    } else {
+      const float2 v = *reinterpret_cast<const float2*>(static_cast<const float*>(p.partial_o) + oi);
+      o0 = v.x;
+      o1 = v.y;
     }
   };
-
-  merge_range(n_sink, n_sink + n_band);
-  __syncthreads();  // every entry read above precedes the ring write below
-
-  if (ready) {
+  // this wave's share of partials [j0, j1), batched
+  auto merge_range = [&](MergeState& st, int j0, int j1) {
+    for (int jb = j0 + wave; jb < j1; jb += kWaves * kBatch) {
+      float pl[kBatch], p0[kBatch], p1[kBatch];
 #pragma unroll
-    for (int k = 0; k < kElems; ++k) {
-      if (!own[k]) continue;
-      const int hq = hkv * G + hh[k];
-      const int64_t rowi = (static_cast<int64_t>(req) * M + dest) * Hq + hq;
-      const bool valid = isfinite(lse[k]);
-      p.query_cache[rowi * kHeadDim + dd[k]] = p.q_pre[(static_cast<int64_t>(n) * Hq + hq) * kHeadDim + dd[k]];
-      p.attn_cache[rowi * kHeadDim + dd[k]] = valid ? f32_to_bf16(acc[k]) : static_cast<uint16_t>(0);
-      if (dd[k] == 0) p.lse_cache[rowi] = valid ? lse[k] : -INFINITY;
+      for (int u = 0; u < kBatch; ++u) {
+        const int j = jb + kWaves * u;
+        load_partial(j < j1 ? j : j0, pl[u], p0[u], p1[u]);
+        if (j >= j1) pl[u] = -INFINITY;
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) merge_into(st, pl[u], p0[u], p1[u]);
+    }
+  };
+  // combines the four wave states; the result is returned to every wave
+  auto combine = [&](MergeState& st) {
+    __syncthreads();
+    s_o[wave][d0] = st.o[0];
+    s_o[wave][d0 + 1] = st.o[1];
+    if (lane == 0) s_l[wave] = st.lse;
+    __syncthreads();
+    MergeState r{-INFINITY, {0.0f, 0.0f}};
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) merge_into(r, s_l[w], s_o[w][d0], s_o[w][d0 + 1]);
+    st = r;
+  };
+
+  MergeState st{-INFINITY, {0.0f, 0.0f}};
+  const int mslot = p.head_match_slot[ho];
+  if (wave == 0 && p.head_hit[ho] != 0 && mslot >= 0 && req >= 0 && req < p.s.R) {
+    const int64_t rowi = (static_cast<int64_t>(req) * M + mslot) * Hq + hq;
+    const float pl = p.lse_cache[rowi];
+    if (isfinite(pl)) {
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(p.attn_cache + rowi * kHeadDim + d0);
+      st.lse = pl;
+      st.o[0] = bf16_lo(w);
+      st.o[1] = bf16_hi(w);
     }
   }
+  merge_range(st, n_sink, n_sink + n_band);
+  combine(st);  // also orders every entry read before the ring write below
 
-  merge_range(0, n_sink);
-  merge_range(n_sink + n_band, n_sink + n_band + n_tail);
+  if (ready && wave == 0) {
+    const int64_t rowi = (static_cast<int64_t>(req) * M + dest) * Hq + hq;
+    const bool valid = isfinite(st.lse);
+    *reinterpret_cast<uint32_t*>(p.query_cache + rowi * kHeadDim + d0) =
+        *reinterpret_cast<const uint32_t*>(p.q_pre + ho * kHeadDim + d0);
+    const uint32_t packed = valid ? (static_cast<uint32_t>(f32_to_bf16(st.o[0])) |
+                                     (static_cast<uint32_t>(f32_to_bf16(st.o[1])) << 16))
+                                  : 0u;
+    *reinterpret_cast<uint32_t*>(p.attn_cache + rowi * kHeadDim + d0) = packed;
+    if (lane == 0) p.lse_cache[rowi] = valid ? st.lse : -INFINITY;
+  }
 
-#pragma unroll
-  for (int k = 0; k < kElems; ++k) {
-    if (!own[k]) continue;
-    const int hq = hkv * G + hh[k];
-    const int64_t ho = static_cast<int64_t>(n) * Hq + hq;
-    const bool valid = isfinite(lse[k]);
-    p.out[ho * kHeadDim + dd[k]] = valid ? f32_to_bf16(acc[k]) : static_cast<uint16_t>(0);
-    if (p.out_lse != nullptr && dd[k] == 0) p.out_lse[ho] = valid ? lse[k] : -INFINITY;
+  if (wave != 0) st = MergeState{-INFINITY, {0.0f, 0.0f}};
+  merge_range(st, 0, n_sink);
+  merge_range(st, n_sink + n_band, n_sink + n_band + n_tail);
+  combine(st);
+  if (wave == 0) {
+    const bool valid = isfinite(st.lse);
+    const uint32_t packed = valid ? (static_cast<uint32_t>(f32_to_bf16(st.o[0])) |
+                                     (static_cast<uint32_t>(f32_to_bf16(st.o[1])) << 16))
+                                  : 0u;
+    *reinterpret_cast<uint32_t*>(p.out + ho * kHeadDim + d0) = packed;
+    if (p.out_lse != nullptr && lane == 0) p.out_lse[ho] = valid ? st.lse : -INFINITY;
   }
 }
 
@@ -1325,7 +1373,7 @@ int launch_all(const DecideParams& dp, const AttnParams& ap, const MergeParams& 
     hipLaunchKernelGGL(span_attention_kernel<G>, dim3(attn_grid), dim3(kBlock), plan_lds, stream, ap);
   MAC_HIP(hipGetLastError());
   if (ev) MAC_HIP(hipEventRecord(ev[2], stream));
-  hipLaunchKernelGGL(merge_write_kernel<G>, dim3(NG), dim3(kBlock), 0, stream, mp);
+  hipLaunchKernelGGL(merge_write_kernel<G>, dim3(NG, G), dim3(kBlock), 0, stream, mp);
   MAC_HIP(hipGetLastError());
   if (ev) MAC_HIP(hipEventRecord(ev[3], stream));
   return MAC_OK;
@@ -1390,7 +1438,7 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   MAC_REQUIRE(static_cast<int64_t>(N) * Hkv <= kMaxPlanGroups,
               "N * Hkv = %lld exceeds the %d groups one launch can plan", static_cast<long long>(N) * Hkv,
               kMaxPlanGroups);
-  MAC_REQUIRE(a->complete_task_len >= static_cast<int64_t>(N) * Hkv, "complete task workspace too small");
+  MAC_REQUIRE(a->complete_task_len >= static_cast<int64_t>(N) * Hkv + 1, "complete task workspace too small");
   MAC_REQUIRE(a->req_to_token_rows > 0 && a->req_to_token_stride >= 0, "req_to_token must be 2-D");
   if (N == 0) return MAC_OK;
   MAC_REQUIRE(a->q_post && a->q_pre && a->k_buffer && a->v_buffer && a->req_to_token && a->req_ids &&
@@ -1450,6 +1498,7 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   dp.group_tail_begin = a->group_tail_begin;
   dp.group_tail_end = a->group_tail_end;
   dp.group_mode = a->group_mode;
+  dp.task_counter = a->complete_task_tile + static_cast<int64_t>(N) * Hkv;
   dp.S = a->semantic_pos_ahead;
   dp.F = a->front_sink_tokens > 0 ? a->front_sink_tokens : 0;
   dp.gen_min_limit = a->gen_min_limit;
@@ -1494,6 +1543,7 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   ap.group_chunk = a->complete_task_go;
   ap.group_ntasks = a->complete_task_tile;
   ap.task_counts = a->task_counts;
+  ap.task_counter = dp.task_counter;
   ap.partial_o = a->partial_o;
   ap.partial_lse = a->partial_lse;
   ap.partial_bf16 = a->partial_o_is_bf16 ? 1 : 0;
@@ -1501,6 +1551,7 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   ap.cap = cap;
   ap.F = dp.F;
   ap.q_scale = static_cast<float>(a->sm_scale) * kLog2e;
+  ap.tile_tokens = a->tile_tokens;
 
   MergeParams mp{};
   mp.s = s;
