@@ -412,3 +412,64 @@ def plant_synthetic_hits(torch, dev: dict, *, hit_rate: float, bench_mode: int, 
         si = torch.tensor(ss, device=dev["q_pre"].device)
         dev["query_cache"][ni, si, hi] = dev["q_pre"][ni, hi]
     return len(ns)
+
+
+def device_ragged_case(torch, *, kv_lens, hq: int, hkv: int, capacity: int, seed: int = 0,
+                       device="cuda", q_post_separate: bool = True, chunk_rows: int = 1 << 20):
+    """Like ``device_case`` but with one context length per request (requests
+    stored back to back in the pool) and random finite ring entries
+    (o ~ N(0,1), lse ~ N(0,1)) so that reuse merges are non-trivial.  Ring
+    queries are randn + 10 (never matched unless planted)."""
+    kv_lens = [int(x) for x in kv_lens]
+    batch = len(kv_lens)
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    bf = torch.bfloat16
+    rows = sum(kv_lens)
+    k = torch.empty(rows, hkv, 128, device=device, dtype=bf)
+    v = torch.empty(rows, hkv, 128, device=device, dtype=bf)
+    for t in (k, v):
+        for i in range(0, rows, chunk_rows):
+            t[i:i + chunk_rows].normal_(generator=g)
+    cols = max(kv_lens)
+    r2t = torch.zeros(batch, cols, device=device, dtype=torch.int32)
+    ocl = torch.zeros(batch, device=device, dtype=torch.int64)
+    base = 0
+    for n, kv in enumerate(kv_lens):
+        r2t[n, :kv] = torch.arange(base, base + kv, device=device, dtype=torch.int32)
+        ocl[n] = base + kv - 1
+        base += kv
+    q_pre = torch.randn(batch, hq, 128, device=device, dtype=bf, generator=g)
+    q_post = (torch.randn(batch, hq, 128, device=device, dtype=bf, generator=g)
+              if q_post_separate else q_pre)
+    qc = torch.randn(batch, capacity, hq, 128, device=device, dtype=bf, generator=g) + 10
+    ac = torch.randn(batch, capacity, hq, 128, device=device, dtype=bf, generator=g)
+    lc = torch.randn(batch, capacity, hq, device=device, dtype=torch.float32, generator=g)
+    return dict(
+        q_post=q_post, q_pre=q_pre, k=k, v=v, req_to_token=r2t,
+        req_ids=torch.arange(batch, device=device, dtype=torch.int32),
+        past_lens=torch.tensor([x - 1 for x in kv_lens], device=device, dtype=torch.int32),
+        out_cache_loc=ocl, query_cache=qc.contiguous(), attn_cache=ac.contiguous(),
+        lse_cache=lc.contiguous(),
+        cache_ready=torch.empty(0, device=device), cache_epoch=torch.empty(0, device=device),
+        request_epoch=torch.empty(0, device=device),
+    )
+
+
+def plant_noisy_matches(torch, dev: dict, *, entries: dict, seed: int = 0):
+    """Plant ring rows that a head matches with similarity noise:
+    ``entries[(n, hq)] = (pos, eps)`` stores sqrt(1-eps^2) * q_pre + eps * N(0,1)
+    at the slot of logical position ``pos`` (BASELINE configs 0-2 hit
+    structure).  Small eps (<= 0.5) is a hit at threshold 0.45, eps >= 0.9 a
+    miss."""
+    if not entries:
+        return
+    g = torch.Generator(device=dev["q_pre"].device)
+    g.manual_seed(seed)
+    cap = dev["query_cache"].shape[1]
+    past = [int(x) for x in dev["past_lens"].cpu().tolist()]
+    for (n, h), (pos, eps) in sorted(entries.items()):
+        slot = pos_to_ring_slot(past[n], cap, pos)
+        q = dev["q_pre"][n, h].float()
+        z = torch.randn(q.shape, device=q.device, generator=g)
+        dev["query_cache"][n, slot, h] = (math.sqrt(1.0 - eps * eps) * q + eps * z).to(torch.bfloat16)

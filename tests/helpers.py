@@ -103,3 +103,47 @@ def oracle_run(case: syn.Case, **kw) -> orc.DecodeResult:
 
 def bits(x):
     return syn.from_bits(x)
+
+
+def host_subset(torch, dev: dict, requests, *, semantic_pos_ahead, front_sink_tokens=0,
+                threshold=0.45, gen_min_limit=0) -> syn.Case:
+    """Copies the rows a subset of requests reads from device tensors into a
+    self-contained CPU Case (its own compact KV pool and req_to_token), for
+    the oracle.  Decode steps of different requests are independent, so the
+    oracle's result for the subset equals the GPU's for those requests."""
+    f = lambda t: t.float().cpu().numpy()  # noqa: E731
+    req_ids = dev["req_ids"].cpu().numpy()
+    past = dev["past_lens"].cpu().numpy()
+    ocl = dev["out_cache_loc"].cpu().numpy()
+    kvs, vvs, rows_list = [], [], []
+    base = 0
+    r2t_rows = []
+    for n in requests:
+        p = int(past[n])
+        rows = dev["req_to_token"][int(req_ids[n]), :p].long()
+        rows = torch.cat([rows, torch.tensor([int(ocl[n])], device=rows.device)])
+        kvs.append(f(dev["k"][rows]))
+        vvs.append(f(dev["v"][rows]))
+        r2t_rows.append(np.arange(base, base + p + 1, dtype=np.int32))
+        rows_list.append(base + p)
+        base += p + 1
+    cols = max(len(r) for r in r2t_rows)
+    r2t = np.zeros((len(requests), cols), np.int32)
+    for i, r in enumerate(r2t_rows):
+        r2t[i, :len(r)] = r
+    rid = [int(req_ids[n]) for n in requests]
+    c = syn.Case(
+        q_post=f(dev["q_post"][list(requests)]), q_pre=f(dev["q_pre"][list(requests)]),
+        k=np.concatenate(kvs), v=np.concatenate(vvs), req_to_token=r2t,
+        req_ids=np.arange(len(requests), dtype=np.int32),
+        past_lens=past[list(requests)].astype(np.int32),
+        out_cache_loc=np.array(rows_list, np.int64),
+        query_cache=f(dev["query_cache"][rid]), attn_cache=f(dev["attn_cache"][rid]),
+        lse_cache=dev["lse_cache"][rid].cpu().numpy(), semantic_pos_ahead=semantic_pos_ahead,
+        front_sink_tokens=front_sink_tokens, threshold=threshold,
+        sm_scale=1.0 / np.sqrt(128.0), gen_min_limit=gen_min_limit)
+    for name in ("cache_ready", "cache_epoch", "request_epoch"):
+        t = dev[name]
+        if t.numel() > 0:
+            setattr(c, name, t[rid].cpu().numpy().astype(np.uint8 if name == "cache_ready" else np.int64))
+    return c

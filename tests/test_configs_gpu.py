@@ -1,0 +1,316 @@
+"""BASELINE.json configs 0-4 at their real shapes on the GPU, checked against
+the CPU oracle, plus hipGraph replay.
+
+Every request's decode step is independent, so the GPU runs the whole batch
+and the oracle re-runs a subset of requests from a compact copy of the rows
+they read (``helpers.host_subset``); outputs, ring rows and decisions of that
+subset must match (decisions exactly, values within 1e-2 relative L2).
+
+Config interpretations: S = 256 where a config does not name
+it; configs 0-2 keep 16 populated ring entries at the named match positions in
+a ring large enough to reach them (M = 4096 / 4096 / 32768); hits are planted
+as sqrt(1-eps^2) q + eps N(0,1) with eps = 0.3 (hit) or 0.9 (miss).
+"""
+
+import math
+import time
+
+import numpy as np
+import pytest
+
+from helpers import assert_close, bits, host_subset, oracle_run, rel_l2, syn
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ext():
+    from mac_attention.integrations.sglang.bridge import load_mac_persistent_decode_extension
+
+    return load_mac_persistent_decode_extension(False)
+
+
+@pytest.fixture(scope="module")
+def cache_ext():
+    from mac_attention.integrations.sglang.bridge import load_mac_prefill_update_cache_extension
+
+    return load_mac_prefill_update_cache_extension(False)
+
+
+def _np(t):
+    return t.float().cpu().numpy() if t.dtype == torch.bfloat16 else t.cpu().numpy()
+
+
+def _run(ext, dev, *, S, F, max_context, tile=32, partial=torch.float32, bench=None, ws=None):
+    n, hq, _ = dev["q_post"].shape
+    hkv = dev["k"].shape[1]
+    if ws is None:
+        ws = syn.workspace(torch, batch=n, hq=hq, hkv=hkv, capacity=dev["query_cache"].shape[1],
+                           max_context=max_context, tile_tokens=tile, match_tile_slots=32,
+                           semantic_pos_ahead=S, front_sink_tokens=F, partial_dtype=partial,
+                           device=dev["q_post"].device)
+    out = torch.empty_like(dev["q_post"])
+    out_lse = torch.empty(n, hq, device=out.device)
+    b = dict(bench_mode=0, bench_hit_rate=1.0, bench_hit_rate_std=0.0, bench_skip_ratio=-1.0,
+             bench_skip_ratio_std=0.0, bench_match_lag_mean=64.0, bench_match_lag_std=0.0,
+             bench_seed=1, bench_miss_mask=-1, bench_layer_id=0)
+    b.update(bench or {})
+    ext.mac_persistent_decode_bf16(
+        dev["q_post"], dev["q_pre"], dev["k"], dev["v"], dev["req_to_token"], dev["req_ids"],
+        dev["past_lens"], dev["out_cache_loc"], dev["query_cache"], dev["attn_cache"],
+        dev["lse_cache"], out, out_lse, *ws, max_context, tile, 32, S, F, 0, 0, 0, 0.45,
+        1.0 / math.sqrt(128.0), 0, b["bench_mode"], b["bench_hit_rate"], b["bench_hit_rate_std"],
+        b["bench_skip_ratio"], b["bench_skip_ratio_std"], b["bench_match_lag_mean"],
+        b["bench_match_lag_std"], b["bench_seed"], b["bench_miss_mask"], b["bench_layer_id"],
+        dev["query_cache"], dev["cache_ready"], dev["cache_epoch"], dev["request_epoch"])
+    return out, out_lse, ws
+
+
+def _check_subset(dev, out, out_lse, ws, sub, res, requests, what, tol=1e-2):
+    rid = [int(x) for x in dev["req_ids"][list(requests)].cpu().tolist()]
+    m = dev["query_cache"].shape[1]
+    for i, n in enumerate(requests):
+        tag = f"{what} request {n}"
+        np.testing.assert_array_equal(_np(ws[3])[n], res.head["hit"][i], err_msg=f"{tag} head_hit")
+        np.testing.assert_array_equal(_np(ws[5])[n], res.head["match_pos"][i], err_msg=f"{tag} match_pos")
+        np.testing.assert_array_equal(_np(ws[15])[n], res.group["mode"][i], err_msg=f"{tag} group_mode")
+        got = _np(out[n])
+        exp = bits(res.out[i])
+        assert rel_l2(got, exp) < tol, f"{tag} out rel_l2 {rel_l2(got, exp):.3e}"
+        assert_close(_np(out_lse[n]), res.out_lse[i], 2e-2, f"{tag} out_lse")
+        dest = int(sub.past_lens[i]) % m
+        ring = _np(dev["attn_cache"][rid[i], dest])
+        exp_ring = bits(res.attn_cache[i, dest])
+        assert rel_l2(ring, exp_ring) < tol or np.abs(exp_ring).max() == 0, f"{tag} ring"
+        np.testing.assert_array_equal(syn.to_bits(_np(dev["query_cache"][rid[i], dest])),
+                                      res.query_cache[i, dest], err_msg=f"{tag} ring q")
+        assert_close(_np(dev["lse_cache"][rid[i], dest]), res.lse_cache[i, dest], 2e-2, f"{tag} ring lse")
+
+
+def _plant_ring(dev, rng, *, positions, hit_heads_per_req, m):
+    """16 populated ring rows per request at ``positions``; every head gets a
+    noisy copy of its query at one of them (eps 0.3 for hit heads, 0.9 else);
+    rows at the other positions are plain N(0,1) queries; all other slots are
+    invalid (lse = -inf)."""
+    n_req, hq, _ = dev["q_pre"].shape
+    past = [int(x) for x in dev["past_lens"].cpu().tolist()]
+    dev["lse_cache"].fill_(-math.inf)
+    entries = {}
+    for n in range(n_req):
+        slots = [syn.pos_to_ring_slot(past[n], m, p) for p in positions[n]]
+        st = torch.tensor(slots, device=dev["q_pre"].device)
+        dev["query_cache"][n, st] = torch.randn(len(slots), hq, 128, device=st.device).to(torch.bfloat16)
+        dev["lse_cache"][n, st] = torch.randn(len(slots), hq, device=st.device)
+        for h in range(hq):
+            pos = int(rng.choice(positions[n]))
+            entries[(n, h)] = (pos, 0.3 if h in hit_heads_per_req[n] else 0.9)
+    syn.plant_noisy_matches(torch, dev, entries=entries, seed=int(rng.integers(1 << 30)))
+
+
+def _hit_heads(rng, hq, hit):
+    k = int(round(hit * hq))
+    return set(rng.choice(hq, size=k, replace=False).tolist())
+
+
+# ------------------------------------------------------------- config 0 ----
+
+
+def test_config0_cpu_plumbing_case(ext):
+    """B=1, GQA-4, context 4096, 16 cached queries at positions uniform in
+    [1024, 4000), Bernoulli(0.5) hit mask, F=0, seed 0."""
+    rng = np.random.default_rng(0)
+    m, ctx, S = 4096, 4096, 256
+    dev = syn.device_ragged_case(torch, kv_lens=[ctx + 1], hq=32, hkv=8, capacity=m, seed=0)
+    positions = [sorted(rng.choice(np.arange(1024, 4000), size=16, replace=False).tolist())]
+    hits = [set(np.nonzero(rng.random(32) < 0.5)[0].tolist())]
+    _plant_ring(dev, rng, positions=positions, hit_heads_per_req=hits, m=m)
+    sub = host_subset(torch, dev, [0], semantic_pos_ahead=S)
+    res = oracle_run(sub)
+    assert res.head["hit"][0].sum() == len(hits[0])
+    out, out_lse, ws = _run(ext, dev, S=S, F=0, max_context=ctx + 8)
+    torch.cuda.synchronize()
+    _check_subset(dev, out, out_lse, ws, sub, res, [0], "config0")
+
+
+# ------------------------------------------------------------- config 1 ----
+
+
+@pytest.mark.parametrize("hit", [0.0, 0.25, 0.5, 0.75, 0.9, 1.0])
+def test_config1_llama8b_hit_sweep(ext, hit):
+    """B=1, GQA-4, context 32768, S=256, F=64, hit ratio sweep."""
+    rng = np.random.default_rng(100 + int(hit * 100))
+    m, ctx, S, F = 4096, 32768, 256, 64
+    dev = syn.device_ragged_case(torch, kv_lens=[ctx + 1], hq=32, hkv=8, capacity=m, seed=1)
+    positions = [sorted(rng.choice(np.arange(ctx - 3000, ctx - 64), size=16, replace=False).tolist())]
+    _plant_ring(dev, rng, positions=positions, hit_heads_per_req=[_hit_heads(rng, 32, hit)], m=m)
+    sub = host_subset(torch, dev, [0], semantic_pos_ahead=S, front_sink_tokens=F)
+    res = oracle_run(sub)
+    out, out_lse, ws = _run(ext, dev, S=S, F=F, max_context=ctx + 8)
+    torch.cuda.synchronize()
+    _check_subset(dev, out, out_lse, ws, sub, res, [0], f"config1 hit {hit}")
+
+
+# ------------------------------------------------------------- config 2 ----
+
+
+@pytest.mark.parametrize("hit", [0.0, 0.5, 1.0])
+def test_config2_qwen3_gqa8(ext, hit):
+    """B=16, GQA-8 (Hkv=4), context 65536, match positions uniform in
+    [0.5 ctx, ctx-512), F=128; two requests checked against the oracle."""
+    rng = np.random.default_rng(200 + int(hit * 10))
+    b, m, ctx, S, F = 16, 32768, 65536, 256, 128
+    dev = syn.device_ragged_case(torch, kv_lens=[ctx + 1] * b, hq=32, hkv=4, capacity=m, seed=2)
+    positions = [sorted(rng.choice(np.arange(ctx // 2, ctx - 512), size=16, replace=False).tolist())
+                 for _ in range(b)]
+    hits = [_hit_heads(rng, 32, hit) for _ in range(b)]
+    _plant_ring(dev, rng, positions=positions, hit_heads_per_req=hits, m=m)
+    check = [0, 11]
+    sub = host_subset(torch, dev, check, semantic_pos_ahead=S, front_sink_tokens=F)
+    res = oracle_run(sub)
+    out, out_lse, ws = _run(ext, dev, S=S, F=F, max_context=ctx + 8)
+    torch.cuda.synchronize()
+    _check_subset(dev, out, out_lse, ws, sub, res, check, f"config2 hit {hit}")
+
+
+# ------------------------------------------------------------- config 3 ----
+
+
+@pytest.mark.parametrize("hkv", [8, 4])
+def test_config3_large_batch(ext, hkv):
+    """B=64, past_len 130048, ring 32, synthetic_head hit 0.8 (the bench
+    workload); three requests checked against the oracle, all 64 for finite
+    outputs and the exact-quota hit count."""
+    b, m, ctx, S = 64, 32, 130048, 256
+    dev = syn.device_ragged_case(torch, kv_lens=[ctx + 1] * b, hq=32, hkv=hkv, capacity=m, seed=3)
+    syn.plant_synthetic_hits(torch, dev, hit_rate=0.8, bench_mode=1, semantic_pos_ahead=S)
+    check = [0, 21, 63]
+    sub = host_subset(torch, dev, check, semantic_pos_ahead=S)
+    t0 = time.time()
+    res = oracle_run(sub)
+    print(f"oracle on {len(check)} requests: {time.time() - t0:.1f}s", flush=True)
+    out, out_lse, ws = _run(ext, dev, S=S, F=0, max_context=131072)
+    torch.cuda.synchronize()
+    _check_subset(dev, out, out_lse, ws, sub, res, check, f"config3 hkv {hkv}")
+    assert torch.isfinite(out.float()).all()
+    assert int(ws[3].sum()) == round(0.8 * b * 32)
+
+
+# ------------------------------------------------------------- config 4 ----
+
+
+def test_config4_ragged_serving_mix(ext, cache_ext):
+    """B=64 GQA-8, contexts log-uniform in [16K, 127K], F=128; 20% of the
+    requests not ready and 10% with an epoch mismatch (both must run exact
+    attention and leave their ring rows alone), hit 0.8 among ready ones; a
+    mac_prefill_update_cache call on 8192-row chunks between two decode steps."""
+    rng = np.random.default_rng(4)
+    b, m, S, F = 64, 32, 256, 128
+    kv_lens = np.exp(rng.uniform(np.log(16384), np.log(130048), b)).astype(int) + 1
+    dev = syn.device_ragged_case(torch, kv_lens=kv_lens.tolist(), hq=32, hkv=4, capacity=m, seed=4)
+    order = rng.permutation(b)
+    not_ready, mismatch = set(order[:13].tolist()), set(order[13:19].tolist())
+    ready = np.ones(b, np.uint8)
+    ready[list(not_ready)] = 0
+    cache_epoch = np.full(b, 7, np.int64)
+    request_epoch = cache_epoch.copy()
+    request_epoch[list(mismatch)] = 8
+    dev["cache_ready"] = torch.from_numpy(ready.astype(bool)).cuda()
+    dev["cache_epoch"] = torch.from_numpy(cache_epoch).cuda()
+    dev["request_epoch"] = torch.from_numpy(request_epoch).cuda()
+    # hit 0.8 among the requests: plant exact copies at lag 16 for the chosen heads
+    entries = {}
+    for n in range(b):
+        p = int(kv_lens[n]) - 1
+        for h in _hit_heads(rng, 32, 0.8):
+            entries[(n, h)] = (p - 16, 0.0)
+    syn.plant_noisy_matches(torch, dev, entries=entries, seed=5)
+    check = [int(order[0]), int(order[15]), int(order[40]), int(order[63])]  # not ready, mismatch, ready x2
+    before = _np(dev["attn_cache"]).copy()
+
+    # step 1
+    sub1 = host_subset(torch, dev, check, semantic_pos_ahead=S, front_sink_tokens=F)
+    res1 = oracle_run(sub1)
+    out, out_lse, ws = _run(ext, dev, S=S, F=F, max_context=131072)
+    torch.cuda.synchronize()
+    _check_subset(dev, out, out_lse, ws, sub1, res1, check, "config4 step1")
+    after = _np(dev["attn_cache"])
+    for n in not_ready | mismatch:
+        np.testing.assert_array_equal(after[n], before[n])
+        assert _np(ws[3])[n].sum() == 0
+
+    # prefill cache update on 8192-row chunks for four requests (ring by request)
+    upd = [int(order[20]), int(order[30]), int(order[40]), int(order[50])]
+    rows = 8192
+    src_q = torch.randn(len(upd) * rows, 32, 128, device="cuda").to(torch.bfloat16)
+    src_a = torch.randn_like(src_q)
+    src_l = torch.randn(len(upd) * rows, 32, device="cuda")
+    req_len = torch.from_numpy(kv_lens.astype(np.int32) - 1 - rows).cuda()
+    cache_ext.mac_prefill_update_cache(
+        dev["query_cache"], dev["attn_cache"], dev["lse_cache"], req_len,
+        torch.tensor(upd, dtype=torch.int32, device="cuda"), src_q, src_a, src_l,
+        torch.arange(0, (len(upd) + 1) * rows, rows, dtype=torch.int32, device="cuda"),
+        torch.full((len(upd),), rows, dtype=torch.int32, device="cuda"), m, 32, 128,
+        torch.empty(0, device="cuda", dtype=torch.bfloat16))
+    torch.cuda.synchronize()
+    for i, n in enumerate(upd):
+        base_len = int(kv_lens[n]) - 1 - rows
+        for r in range(rows - m, rows):
+            slot = (base_len + r) % m
+            assert torch.equal(dev["query_cache"][n, slot], src_q[i * rows + r])
+        assert int(req_len[n]) == base_len + rows
+
+    # step 2 on the updated rings
+    check2 = [int(order[40]), int(order[50]), int(order[63])]
+    sub2 = host_subset(torch, dev, check2, semantic_pos_ahead=S, front_sink_tokens=F)
+    res2 = oracle_run(sub2)
+    out2, out_lse2, ws2 = _run(ext, dev, S=S, F=F, max_context=131072, ws=ws)
+    torch.cuda.synchronize()
+    _check_subset(dev, out2, out_lse2, ws2, sub2, res2, check2, "config4 step2")
+
+
+# ------------------------------------------------------------ hipGraph ----
+
+
+def test_graph_replay_matches_eager(ext):
+    """The decode step captured in a graph and replayed (with eager work and
+    synchronisation between replays) gives the eager result every time,
+    including the ring-row writes and the readiness gate."""
+    b, m, S, F = 6, 32, 64, 16
+    kv_lens = [3000, 5000, 777, 4096, 2000, 10000]
+    pristine = syn.device_ragged_case(torch, kv_lens=kv_lens, hq=32, hkv=8, capacity=m, seed=9)
+    syn.plant_synthetic_hits(torch, pristine, hit_rate=0.6, bench_mode=1, semantic_pos_ahead=S,
+                             match_lag_mean=10.0)
+    pristine["cache_ready"] = torch.tensor([1, 1, 0, 1, 1, 1], dtype=torch.bool, device="cuda")
+    clone = lambda d: {k: v.clone() for k, v in d.items()}  # noqa: E731
+
+    eager = clone(pristine)
+    out_e, lse_e, _ = _run(ext, eager, S=S, F=F, max_context=10240)
+    torch.cuda.synchronize()
+
+    live = clone(pristine)
+    ws = syn.workspace(torch, batch=b, hq=32, hkv=8, capacity=m, max_context=10240,
+                       tile_tokens=32, match_tile_slots=32, semantic_pos_ahead=S,
+                       front_sink_tokens=F, device="cuda")
+    holder = {}
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        _run(ext, live, S=S, F=F, max_context=10240, ws=ws)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        holder["out"], holder["lse"], _ = _run(ext, live, S=S, F=F, max_context=10240, ws=ws)
+    for it in range(4):
+        for k in ("query_cache", "attn_cache", "lse_cache"):
+            live[k].copy_(pristine[k])
+        _ = torch.randn(1000, device="cuda").sum()  # unrelated eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(holder["out"], out_e), f"replay {it}: out differs from eager"
+        assert torch.equal(holder["lse"], lse_e), f"replay {it}: lse differs from eager"
+        for k in ("query_cache", "attn_cache", "lse_cache"):
+            assert torch.equal(live[k], eager[k]), f"replay {it}: {k} differs from eager"
