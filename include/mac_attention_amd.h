@@ -13,7 +13,9 @@
  *
  * Reference paths are relative to the reference repository root.  "DECODE"
  * stands for attention/src/mac_attention/integrations/sglang/csrc/
- * mac_decode_persistent.cu and "PREFILL" for .../csrc/mac_prefill_update_cache.cu.
+ * mac_decode_persistent.cu, "PREFILL" for .../csrc/mac_prefill_update_cache.cu,
+ * "MERGE" for .../csrc/mac_merge_downdate_cache.cu and "HOOKS" for
+ * attention/src/mac_attention/integrations/sglang/flashinfer_hooks.py.
  */
 #ifndef MAC_ATTENTION_AMD_H_
 #define MAC_ATTENTION_AMD_H_
@@ -193,6 +195,112 @@ MAC_API int mac_invalidate_persistent_ready(uint8_t* ready, int64_t* cache_epoch
 MAC_API int mac_update_request_state(int32_t* req_len, int32_t* match_req_len, int32_t* cache_lens,
                              const int32_t* req_ids, const int32_t* seq_lens,
                              const int32_t* cur_lens, int32_t B, int32_t R, void* stream);
+
+/* ------------------------------------------------ prefill rectification --- */
+
+/* Element types of lse tensors for mac_update_then_downdate_bf16_inplace. */
+enum { MAC_DTYPE_F32 = 0, MAC_DTYPE_BF16 = 1, MAC_DTYPE_F16 = 2 };
+
+/* Replaces mac_update_then_downdate_bf16_inplace (MERGE:320-401, kernel
+ * MERGE:116-288).  out1/out2 bf16 [rows, head_dim]; lse1/lse2 [rows] of type
+ * lse1_dtype/lse2_dtype (MAC_DTYPE_*), natural log.  Removes the state
+ * (out2, lse2) from the state (out1, lse1) and writes the result into
+ * out2/lse2:
+ *   |expm1(lse2 - lse1)| <= 1e-7 -> lse2 = -inf, out2 = 0 (nothing left);
+ *   lse2 > lse1 otherwise        -> lse2 = lse1, out2 = out1 (no-op);
+ *   else r = lse1 + log(max(1 - e^(lse2-lse1) + 1e-7, 1e-30)),
+ *        out2 = (out1 - e^(lse2-lse1) out2) e^(lse1 - r), lse2 = r. */
+MAC_API int mac_update_then_downdate_bf16_inplace(const void* out1, const void* lse1, int32_t lse1_dtype,
+                                                 void* out2, void* lse2, int32_t lse2_dtype,
+                                                 int64_t rows, int32_t head_dim, void* stream);
+
+/*
+ * Causal sliding-window attention over a ragged batch with a page-size-1 KV
+ * pool: the windowed prefill pass the reference runs through FlashInfer's
+ * paged prefill wrapper with window_left = semantic_pos_ahead - 1
+ * (HOOKS:2436-2466).  Request b owns query rows [qo_indptr[b], qo_indptr[b+1])
+ * and keys kv_indices[kv_indptr[b] .. kv_indptr[b+1]); query row i of the
+ * request sits at position kv_len - qo_len + i and attends to the keys at
+ * positions [pos - window_left, pos] (window_left < 0: [0, pos]).
+ *   q        bf16 [total_q, Hq, 128]
+ *   k_buffer, v_buffer bf16 [pool_tokens, Hkv, 128]
+ *   out      bf16 [total_q, Hq, 128]
+ *   out_lse  f32  [total_q, Hq], NATURAL log (FlashInfer returns log2; the
+ *            reference multiplies it by ln 2 right after, HOOKS:2467)
+ */
+typedef struct MacWindowAttentionArgs {
+  uint32_t struct_size; /* sizeof(MacWindowAttentionArgs) */
+  uint32_t abi_version; /* MAC_ABI_VERSION */
+  const void* q;
+  const void* k_buffer;
+  const void* v_buffer;
+  const int32_t* qo_indptr;  /* [B+1] */
+  const int32_t* kv_indptr;  /* [B+1] */
+  const int32_t* kv_indices; /* [kv_indptr[B]] pool rows */
+  void* out;
+  float* out_lse;
+  int64_t total_q;
+  int64_t pool_tokens;
+  int32_t B, Hq, Hkv, D;
+  int32_t window_left;
+  double sm_scale;
+} MacWindowAttentionArgs;
+
+MAC_API int mac_prefill_window_attention_bf16(const MacWindowAttentionArgs* args, void* stream);
+
+/*
+ * Fused prefill rectification + ring update: the composition
+ *   window attention (above, window_left = S - 1)
+ *   -> mac_update_then_downdate_bf16_inplace(o_full, lse_full, window)
+ *   -> mac_prefill_update_cache (offsets = qo_indptr, lens = its differences)
+ * of HOOKS:2436-2482, computed only for the rows the ring keeps (the last
+ * min(len_b, M) rows of each request; PREFILL:201-269 drops the others).
+ * Row i at position p gets the prefix state over [0, E), E = p + 1 - S, as
+ * full (o_full, lse_full) minus the window [E, p + 1); E <= 0 gives the empty
+ * state (o = 0, lse = -inf) exactly.
+ * front_sink_tokens F > 0:
+ *   sink_mode 0: as the reference (HOOKS:2205-2215), rows are written with
+ *                lse = -inf (never matched; o = full minus window);
+ *   sink_mode 1: the sink [0, min(F, E)) is removed as well, giving the state
+ *                over [min(F, E), E) that decode-written rows hold
+ *                (DECODE:4280-4685), with finite lse.
+ *   q_post       bf16 [total_q, Hq, 128]  queries of the attention (post-RoPE)
+ *   src_q        bf16 [total_q, Hq, 128]  rows stored as ring queries (pre-RoPE)
+ *   o_full       bf16 [total_q, Hq, 128], lse_full f32 [total_q, Hq] (natural log):
+ *                full causal prefill attention of the same rows
+ *   ring tensors, request_length, req_ids, q_post_cache: as in
+ *                mac_prefill_update_cache (request_length read before any bump;
+ *                bumped by len_b in the indexed-by-request form).
+ */
+typedef struct MacRectifyArgs {
+  uint32_t struct_size; /* sizeof(MacRectifyArgs) */
+  uint32_t abi_version; /* MAC_ABI_VERSION */
+  const void* q_post;
+  const void* src_q;
+  const void* o_full;
+  const float* lse_full;
+  const void* k_buffer;
+  const void* v_buffer;
+  const int32_t* qo_indptr;
+  const int32_t* kv_indptr;
+  const int32_t* kv_indices;
+  void* q_cache;
+  void* attn_cache;
+  float* lse_cache;
+  void* q_post_cache; /* NULL allowed */
+  int32_t* request_length;
+  const int32_t* req_ids;
+  int64_t total_q;
+  int64_t pool_tokens;
+  int32_t request_length_len;
+  int32_t B, R, M, Hq, Hkv, D;
+  int32_t semantic_pos_ahead;
+  int32_t front_sink_tokens;
+  int32_t sink_mode;
+  double sm_scale;
+} MacRectifyArgs;
+
+MAC_API int mac_prefill_rectify_update_cache_bf16(const MacRectifyArgs* args, void* stream);
 
 /* Profiling variant of mac_persistent_decode_bf16: same arguments and effects,
  * plus HIP events on `stream` around each of the three kernels; synchronises

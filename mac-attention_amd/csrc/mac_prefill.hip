@@ -1,0 +1,623 @@
+// mac_prefill.hip -- prefill rectification for MI355X (gfx950).
+//
+// A ring entry at logical position p holds the attention state of the query
+// of p over the keys [0, E), E = p + 1 - S (S = semantic_pos_ahead), so that a
+// later decode step that matches it only has to add the band [E, now).  The
+// prefill attention computes the state over [0, p + 1); the reference removes
+// the trailing window [E, p + 1) with a second, windowed FlashInfer pass and a
+// log-sum-exp "downdate" (flashinfer_hooks.py:2436-2482,
+// mac_merge_downdate_cache.cu:116-288).  This file provides:
+//
+//  * downdate_kernel: the reference's downdate op on its own (any head_dim,
+//    f32/bf16/f16 lse), for callers that keep the reference's three calls.
+//  * window_kernel<false>: causal sliding-window attention over a ragged
+//    batch with a page-size-1 KV pool (the windowed FlashInfer pass).
+//  * window_kernel<true>: the fused form.  Only the rows the ring keeps (the
+//    last min(len, M) of each request) are computed; for them the window
+//    state never leaves registers: it is downdated from the full state and
+//    stored straight into the ring with the pre-RoPE query, followed by the
+//    request_length bump (bump_kernel).
+//
+// Window kernel layout: one 64-lane wave owns 16 consecutive query rows of
+// one (request, query head) and walks the rows' key range in 32-key blocks.
+// S^T[key][row] = K Q^T and O^T[d][row] += V^T P^T run on
+// v_mfma_f32_16x16x32_bf16 exactly as in the decode kernel with query rows in
+// place of the GQA heads: the lane holding row l%16 keeps that row's softmax
+// state and 32 O^T accumulators.  K is read straight into the A operand (the
+// rows are shared by the 16 query rows of the wave and by the other heads of
+// the group, so they come from L2); Q stays in registers; V is staged in a
+// per-wave 8 KiB LDS tile for the transposed A-operand gather.
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+
+#include "mac_attention_amd.h"
+#include "mac_common.h"
+
+namespace mac {
+int fail(int code, const char* fmt, ...);
+}  // namespace mac
+
+namespace {
+
+using namespace mac;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& w) { return __builtin_bit_cast(bf16x8_t, w); }
+
+// ------------------------------------------------------------- downdate ----
+
+// Control scalars of the downdate (MERGE:148-176), fp32 as in the reference
+// so that its branch decisions are reproduced.
+struct Downdate {
+  float lse;    // new natural-log lse (-inf: nothing left)
+  float t;      // weight of the removed state
+  float scale;  // renormalisation
+};
+
+__device__ __forceinline__ Downdate downdate_control(float l1, float l2) {
+  const float diff = l2 - l1;
+  const bool last_block = fabsf(expm1f(diff)) <= 1e-7f;
+  const bool invalid = diff > 0.0f && !last_block;
+  Downdate d;
+  if (last_block) {
+    d.lse = -INFINITY;
+    d.t = 0.0f;
+    d.scale = 0.0f;
+  } else if (invalid) {
+    d.lse = l1;
+    d.t = 0.0f;
+    d.scale = 1.0f;
+  } else {
+    d.lse = l1 + logf(fmaxf(1.0f - expf(diff) + 1e-7f, 1e-30f));
+    d.t = expf(diff);
+    d.scale = expf(l1 - d.lse);
+  }
+  return d;
+}
+
+__device__ __forceinline__ float load_lse(const void* p, int dtype, int64_t i) {
+  if (dtype == MAC_DTYPE_F32) return static_cast<const float*>(p)[i];
+  const uint16_t b = static_cast<const uint16_t*>(p)[i];
+  if (dtype == MAC_DTYPE_BF16) return bf16_to_f32(b);
+  return static_cast<float>(__builtin_bit_cast(_Float16, b));
+}
+
+__device__ __forceinline__ void store_lse(void* p, int dtype, int64_t i, float v) {
+  if (dtype == MAC_DTYPE_F32) {
+    static_cast<float*>(p)[i] = v;
+  } else if (dtype == MAC_DTYPE_BF16) {
+    static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+  } else {
+    static_cast<uint16_t*>(p)[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+  }
+}
+
+// One 16-lane row group per row; 16 rows per 256-thread workgroup.  Every
+// lane reads lse2 before the group's lane 0 overwrites it (same wave, program
+// order), so no row reads a half-updated lse.
+__global__ void __launch_bounds__(256) downdate_kernel(const uint16_t* __restrict__ out1,
+                                                       const void* __restrict__ lse1, int dt1,
+                                                       uint16_t* __restrict__ out2, void* __restrict__ lse2,
+                                                       int dt2, int64_t rows, int D) {
+  const int sub = threadIdx.x & 15;
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4); row < rows;
+       row += static_cast<int64_t>(gridDim.x) * 16) {
+    const float l1 = load_lse(lse1, dt1, row);
+    const float l2 = load_lse(lse2, dt2, row);
+    const Downdate c = downdate_control(l1, l2);
+    const uint16_t* a = out1 + row * D;
+    uint16_t* b = out2 + row * D;
+    if ((D & 7) == 0) {
+      for (int e = sub * 8; e < D; e += 128) {
+        const uint4 wa = *reinterpret_cast<const uint4*>(a + e);
+        const uint4 wb = *reinterpret_cast<const uint4*>(b + e);
+        float fa[8], fb[8];
+        unpack8(wa, fa);
+        unpack8(wb, fb);
+        uint16_t r[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r[i] = f32_to_bf16((fa[i] - c.t * fb[i]) * c.scale);
+        uint4 w;
+        w.x = r[0] | (static_cast<uint32_t>(r[1]) << 16);
+        w.y = r[2] | (static_cast<uint32_t>(r[3]) << 16);
+        w.z = r[4] | (static_cast<uint32_t>(r[5]) << 16);
+        w.w = r[6] | (static_cast<uint32_t>(r[7]) << 16);
+        *reinterpret_cast<uint4*>(b + e) = w;
+      }
+    } else {
+      for (int e = sub; e < D; e += 16)
+        b[e] = f32_to_bf16((bf16_to_f32(a[e]) - c.t * bf16_to_f32(b[e])) * c.scale);
+    }
+    if (sub == 0) store_lse(lse2, dt2, row, c.lse);
+  }
+}
+
+// ------------------------------------------------------ window attention ----
+
+constexpr int kRows = 16;    // query rows per wave
+constexpr int kBlk = 32;     // keys per block
+constexpr int kMaxB = 4096;  // requests handled by the in-workgroup planner
+
+struct WindowParams {
+  const uint16_t* q;  // attention queries [total_q, Hq, 128]
+  const uint16_t* k;
+  const uint16_t* v;
+  const int32_t* qo_indptr;
+  const int32_t* kv_indptr;
+  const int32_t* kv_indices;
+  // plain window attention
+  uint16_t* out;
+  float* out_lse;
+  // fused rectification
+  const uint16_t* src_q;
+  const uint16_t* o_full;
+  const float* lse_full;
+  uint16_t* q_cache;
+  uint16_t* attn_cache;
+  float* lse_cache;
+  uint16_t* q_post_cache;
+  const int32_t* request_length;
+  const int32_t* req_ids;
+  int64_t pool_tokens;
+  int B, Hq, Hkv, R, M;
+  int window_left;  // plain mode: keys [pos - window_left, pos]; < 0: [0, pos]
+  int S, F, sink_mode;
+  int rl_by_batch;
+  float q_scale;  // sm_scale * log2(e)
+};
+
+// Rows of request b that the kernel computes: all of them, or (fused mode)
+// the last min(len, M) that the ring keeps.
+template <bool kRectify>
+__device__ __forceinline__ int first_row(int len, int M) {
+  return kRectify ? (len > M ? len - M : 0) : 0;
+}
+
+template <bool kRectify>
+__global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
+  __shared__ int s_boff[kMaxB + 1];  // row-block offsets per request
+  __shared__ int s_part[256];
+  __shared__ uint4 s_v[4][kBlk * 16];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int quad = lane >> 4;
+  const int col = lane & 15;
+
+  // ---- plan: s_boff[b] = sum over b' < b of ceil(rows(b') / 16) ----
+  const int B = p.B;
+  const int per = ceil_div(B, 256);
+  {
+    int sum = 0;
+    for (int b = tid * per; b < min(B, (tid + 1) * per); ++b) {
+      const int len = p.qo_indptr[b + 1] - p.qo_indptr[b];
+      const int kvlen = p.kv_indptr[b + 1] - p.kv_indptr[b];
+      const int rows = (len > 0 && kvlen >= len) ? len - first_row<kRectify>(len, p.M) : 0;
+      sum += ceil_div(rows, kRows);
+    }
+    s_part[tid] = sum;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {  // inclusive Hillis-Steele scan
+      const int x = tid >= off ? s_part[tid - off] : 0;
+      __syncthreads();
+      s_part[tid] += x;
+      __syncthreads();
+    }
+    int acc = tid > 0 ? s_part[tid - 1] : 0;
+    for (int b = tid * per; b < min(B, (tid + 1) * per); ++b) {
+      s_boff[b] = acc;
+      const int len = p.qo_indptr[b + 1] - p.qo_indptr[b];
+      const int kvlen = p.kv_indptr[b + 1] - p.kv_indptr[b];
+      const int rows = (len > 0 && kvlen >= len) ? len - first_row<kRectify>(len, p.M) : 0;
+      acc += ceil_div(rows, kRows);
+    }
+    if (tid == 255) s_boff[B] = s_part[255];
+    __syncthreads();
+  }
+  const int total_tasks = s_boff[B] * p.Hq;
+
+  const int Hq = p.Hq, Hkv = p.Hkv;
+  const int G = Hq / Hkv;
+  const int64_t kv_stride = static_cast<int64_t>(Hkv) * kHeadDim;
+  const unsigned pool_rows = static_cast<unsigned>(min(p.pool_tokens, static_cast<int64_t>(INT_MAX)));
+  const uint16_t* vtile = reinterpret_cast<const uint16_t*>(&s_v[wave][0]);
+
+  for (int task = blockIdx.x * 4 + wave; task < total_tasks; task += gridDim.x * 4) {
+    const int blk = task / Hq;
+    const int h = task - blk * Hq;
+    const int hkv = h / G;
+    // request of this row block: largest b with s_boff[b] <= blk
+    int lo = 0, hi = B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_boff[mid] <= blk) lo = mid;
+      else hi = mid - 1;
+    }
+    const int b = lo;
+    const int len = p.qo_indptr[b + 1] - p.qo_indptr[b];
+    const int kvlen = p.kv_indptr[b + 1] - p.kv_indptr[b];
+    const int64_t kv_begin = p.kv_indptr[b];
+    const int r_local = first_row<kRectify>(len, p.M) + kRows * (blk - s_boff[b]);
+    const int nrows = min(kRows, len - r_local);
+    const int pos0 = kvlen - len + r_local;
+    const int pos_last = pos0 + nrows - 1;
+    const bool row_ok = col < nrows;
+    const int pos = pos0 + col;                       // this lane's row position
+    const int64_t grow = static_cast<int64_t>(p.qo_indptr[b]) + r_local + (row_ok ? col : 0);
+
+    // window bounds of this lane's row and of the wave's key range
+    int w_lo, w_lo0;
+    if (kRectify) {
+      w_lo = max(pos + 1 - p.S, 0);
+      w_lo0 = max(pos0 + 1 - p.S, 0);
+    } else {
+      w_lo = p.window_left < 0 ? 0 : max(pos - p.window_left, 0);
+      w_lo0 = p.window_left < 0 ? 0 : max(pos0 - p.window_left, 0);
+    }
+    const bool sink = kRectify && p.sink_mode == 1 && p.F > 0;
+    const int s_hi = sink ? min(p.F, max(pos + 1 - p.S, 0)) : 0;             // this row's sink end
+    const int s_hi_last = sink ? min(p.F, max(pos_last + 1 - p.S, 0)) : 0;  // the wave's
+
+    // Q row (B operand): lane (quad, col) holds Q[row col][8*(4s+quad) .. +8]
+    uint4 qreg[4];
+    {
+      const uint16_t* qp = p.q + (grow * Hq + h) * kHeadDim;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        uint4 w = *reinterpret_cast<const uint4*>(qp + 8 * (4 * s + quad));
+        if (!row_ok) w = make_uint4(0, 0, 0, 0);
+        qreg[s] = w;
+      }
+    }
+
+    float m = kNegBig, l = 0.0f;
+    f32x4_t acc[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const uint16_t* kbase = p.k + static_cast<int64_t>(hkv) * kHeadDim;
+    const uint16_t* vbase = p.v + static_cast<int64_t>(hkv) * kHeadDim;
+    // segment 0: the front sink (fused mode, sink_mode 1); segment 1: the window
+    for (int seg = sink ? 0 : 1; seg < 2; ++seg) {
+      const int seg_lo = seg == 0 ? 0 : w_lo0;
+      const int seg_hi = seg == 0 ? s_hi_last : pos_last + 1;
+      const int r_lo = seg == 0 ? 0 : w_lo;      // this row's bounds in the segment
+      const int r_hi = seg == 0 ? s_hi : pos + 1;
+      for (int base = seg_lo; base < seg_hi; base += kBlk) {
+        // physical rows of keys base + 16 t + col (-1: masked)
+        int ph[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int key = base + 16 * t + col;
+          const int raw = p.kv_indices[kv_begin + min(key, kvlen - 1)];
+          ph[t] = (key < seg_hi && static_cast<unsigned>(raw) < pool_rows) ? raw : -1;
+        }
+        // K straight into the A operand: key 16 t + col, dims 8*(4s+quad) .. +8
+        uint4 ka[2][4];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            ka[t][s] = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(max(ph[t], 0)) * kv_stride +
+                                                       8 * (4 * s + quad));
+        // V rows: lane reads chunk col of token 8*quad + i
+        uint4 vr[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int src = 8 * (quad & 1) + i;
+          const int p0 = __shfl(ph[0], src), p1 = __shfl(ph[1], src);
+          const int pv = (quad >> 1) ? p1 : p0;
+          uint4 w = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(max(pv, 0)) * kv_stride + col * 8);
+          if (pv < 0) w = make_uint4(0, 0, 0, 0);
+          vr[i] = w;
+        }
+        uint32_t vmask = 0;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          vmask |= static_cast<uint32_t>(__ballot(ph[t] >= 0) & 0xffffu) << (16 * t);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int tok = 8 * quad + i;
+          s_v[wave][tok * 16 + (col ^ (2 * ((tok >> 2) & 3)))] = vr[i];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        // S^T = K Q^T; lane (quad, col): row col, keys 16 t + 4 quad + r
+        float sv[8];
+        float bmax = kNegBig;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          f32x4_t c4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[t][s]), as_bf16x8(qreg[s]), c4, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int kk = 16 * t + 4 * quad + r;
+            const int key = base + kk;
+            const bool ok = row_ok && ((vmask >> kk) & 1) && key >= r_lo && key < r_hi;
+            const float x = ok ? c4[r] * p.q_scale : -INFINITY;
+            sv[4 * t + r] = x;
+            bmax = fmaxf(bmax, x);
+          }
+        }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        if (bmax > m) {  // exact online softmax (per lane: its row's state)
+          const float alpha = fast_exp2(m - bmax);
+          m = bmax;
+          l *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+        }
+        // P as the B operand.  The fused form also feeds the bf16 rounding
+        // residual of P through a second MFMA (P = hi + lo, ~16 significant
+        // bits): the downdate divides the window's contribution by the
+        // prefix's share of the softmax mass, which amplifies any error of
+        // the window state.
+        bf16x8_t pb, pl;
+        float psum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float pe = fast_exp2(sv[e] - m);
+          psum += pe;
+          pb[e] = static_cast<__bf16>(pe);
+          if (kRectify) pl[e] = static_cast<__bf16>(pe - static_cast<float>(pb[e]));
+        }
+        l += psum;
+        // O^T += V^T P^T; k index e of the lane <-> key (e < 4 ? 4q+e : 16+4q+e-4)
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          const int chunk_pos = 2 * (dt ^ quad) + (col >> 3);
+          bf16x8_t va;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int tok = e < 4 ? 4 * quad + e : 16 + 4 * quad + (e - 4);
+            va[e] = __builtin_bit_cast(__bf16, vtile[(tok * 16 + chunk_pos) * 8 + (col & 7)]);
+          }
+          acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, acc[dt], 0, 0, 0);
+          if (kRectify) acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl, acc[dt], 0, 0, 0);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+      }
+    }
+
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const float lse_w = l > 0.0f ? (m + fast_log2(l)) * kLn2 : -INFINITY;
+    if (!row_ok) continue;
+
+    if (!kRectify) {
+      uint16_t* op = p.out + (grow * Hq + h) * kHeadDim + 4 * quad;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        uint2 w;
+        w.x = f32_to_bf16(acc[dt][0] * inv) | (static_cast<uint32_t>(f32_to_bf16(acc[dt][1] * inv)) << 16);
+        w.y = f32_to_bf16(acc[dt][2] * inv) | (static_cast<uint32_t>(f32_to_bf16(acc[dt][3] * inv)) << 16);
+        *reinterpret_cast<uint2*>(op + 16 * dt) = w;
+      }
+      if (quad == 0) p.out_lse[grow * Hq + h] = lse_w;
+      continue;
+    }
+
+    // ---- fused: downdate the full state, store the ring row ----
+    const int req = p.req_ids[b];
+    if (req < 0 || req >= p.R) continue;
+    int before = p.rl_by_batch ? p.request_length[b] : p.request_length[req];
+    if (before < 0) before = 0;
+    const int local = r_local + col;  // row index within the request
+    const int slot = static_cast<int>((static_cast<int64_t>(before) + local) % p.M);
+    const int64_t drow = static_cast<int64_t>(req) * p.M + slot;
+    const int e_end = pos + 1 - p.S;
+    const bool empty = e_end <= (sink ? p.F : 0);
+    Downdate c;
+    if (empty) {
+      c.lse = -INFINITY;
+      c.t = 0.0f;
+      c.scale = 0.0f;
+    } else {
+      c = downdate_control(p.lse_full[grow * Hq + h], lse_w);
+    }
+    const uint16_t* of = p.o_full + (grow * Hq + h) * kHeadDim + 4 * quad;
+    uint16_t* ap = p.attn_cache + (drow * Hq + h) * kHeadDim + 4 * quad;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const uint2 f = *reinterpret_cast<const uint2*>(of + 16 * dt);
+      float r[4];
+      const float fo[4] = {bf16_lo(f.x), bf16_hi(f.x), bf16_lo(f.y), bf16_hi(f.y)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[i] = empty ? 0.0f : (fo[i] - c.t * (acc[dt][i] * inv)) * c.scale;
+      uint2 w;
+      w.x = f32_to_bf16(r[0]) | (static_cast<uint32_t>(f32_to_bf16(r[1])) << 16);
+      w.y = f32_to_bf16(r[2]) | (static_cast<uint32_t>(f32_to_bf16(r[3])) << 16);
+      *reinterpret_cast<uint2*>(ap + 16 * dt) = w;
+    }
+    if (quad == 0) p.lse_cache[drow * Hq + h] = (p.sink_mode == 0 && p.F > 0) ? -INFINITY : c.lse;
+    // pre-RoPE query row and the NaN marker of the unknown post-RoPE row (PREFILL:251-262)
+    const uint16_t* sq = p.src_q + (grow * Hq + h) * kHeadDim;
+    uint16_t* dq = p.q_cache + (drow * Hq + h) * kHeadDim;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      *reinterpret_cast<uint4*>(dq + 8 * (4 * s + quad)) = *reinterpret_cast<const uint4*>(sq + 8 * (4 * s + quad));
+    if (p.q_post_cache != nullptr) {
+      uint16_t* pq = p.q_post_cache + (drow * Hq + h) * kHeadDim;
+      const uint4 nan4 = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) *reinterpret_cast<uint4*>(pq + 8 * (4 * s + quad)) = nan4;
+    }
+  }
+}
+
+// request_length[req] += len (indexed-by-request form), after the ring rows
+// were addressed with the old value.
+__global__ void bump_kernel(int32_t* request_length, const int32_t* req_ids, const int32_t* qo_indptr,
+                            int B, int R) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const int req = req_ids[b];
+  const int len = qo_indptr[b + 1] - qo_indptr[b];
+  if (len <= 0 || req < 0 || req >= R) return;
+  atomicAdd(&request_length[req], len);
+}
+
+int grid_for(int64_t tasks) {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+  }
+  const int64_t wgs = (tasks + 3) / 4;
+  return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(wgs, static_cast<int64_t>(cus) * 4)));
+}
+
+}  // namespace
+
+#define REQUIRE(cond, ...) \
+  do {                     \
+    if (!(cond)) return mac::fail(MAC_ERR_INVALID_ARGUMENT, __VA_ARGS__); \
+  } while (0)
+
+#define HIP_OK(call)                                                                      \
+  do {                                                                                    \
+    hipError_t e_ = (call);                                                               \
+    if (e_ != hipSuccess) return mac::fail(MAC_ERR_HIP, "%s: %s", #call, hipGetErrorString(e_)); \
+  } while (0)
+
+extern "C" int mac_update_then_downdate_bf16_inplace(const void* out1, const void* lse1, int32_t lse1_dtype,
+                                                     void* out2, void* lse2, int32_t lse2_dtype, int64_t rows,
+                                                     int32_t head_dim, void* stream) {
+  REQUIRE(rows >= 0, "rows must be >= 0");
+  REQUIRE(head_dim > 0, "head_dim must be > 0");
+  REQUIRE(lse1_dtype >= MAC_DTYPE_F32 && lse1_dtype <= MAC_DTYPE_F16, "lse1 must be float32, bfloat16, or float16");
+  REQUIRE(lse2_dtype >= MAC_DTYPE_F32 && lse2_dtype <= MAC_DTYPE_F16, "lse2 must be float32, bfloat16, or float16");
+  if (rows == 0) return MAC_OK;
+  REQUIRE(out1 && out2 && lse1 && lse2, "null pointer argument");
+  if ((head_dim & 7) == 0)
+    REQUIRE((reinterpret_cast<uintptr_t>(out1) & 15) == 0 && (reinterpret_cast<uintptr_t>(out2) & 15) == 0,
+            "out tensors must be 16-byte aligned");
+  const int64_t wgs = std::min<int64_t>((rows + 15) / 16, 65536);
+  hipLaunchKernelGGL(downdate_kernel, dim3(static_cast<unsigned>(wgs)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(out1), lse1, lse1_dtype,
+                     static_cast<uint16_t*>(out2), lse2, lse2_dtype, rows, head_dim);
+  HIP_OK(hipGetLastError());
+  return MAC_OK;
+}
+
+namespace {
+
+int check_window_common(int B, int Hq, int Hkv, int D, int64_t total_q, int64_t pool, const void* q,
+                        const void* k, const void* v, const int32_t* qo, const int32_t* kvp, const int32_t* kvi) {
+  REQUIRE(D == kHeadDim, "head_dim must be 128 (got %d)", D);
+  REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0, "Hq must be a positive multiple of Hkv");
+  REQUIRE(B >= 0 && B <= kMaxB, "B must be in [0, %d] (got %d)", kMaxB, B);
+  REQUIRE(total_q >= 0 && pool > 0, "bad total_q / pool_tokens");
+  REQUIRE(total_q * Hq <= static_cast<int64_t>(INT_MAX) * 64, "total_q too large");
+  REQUIRE(q && k && v && qo && kvp && kvi, "null pointer argument");
+  return MAC_OK;
+}
+
+}  // namespace
+
+extern "C" int mac_prefill_window_attention_bf16(const MacWindowAttentionArgs* a, void* stream) {
+  REQUIRE(a != nullptr, "args is NULL");
+  REQUIRE(a->struct_size == sizeof(MacWindowAttentionArgs), "struct_size mismatch (%u vs %zu)", a->struct_size,
+          sizeof(MacWindowAttentionArgs));
+  REQUIRE(a->abi_version == MAC_ABI_VERSION, "abi_version mismatch");
+  if (int rc = check_window_common(a->B, a->Hq, a->Hkv, a->D, a->total_q, a->pool_tokens, a->q, a->k_buffer,
+                                   a->v_buffer, a->qo_indptr, a->kv_indptr, a->kv_indices))
+    return rc;
+  REQUIRE(a->out && a->out_lse, "out / out_lse must not be NULL");
+  if (a->B == 0 || a->total_q == 0) return MAC_OK;
+  WindowParams p{};
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.k = static_cast<const uint16_t*>(a->k_buffer);
+  p.v = static_cast<const uint16_t*>(a->v_buffer);
+  p.qo_indptr = a->qo_indptr;
+  p.kv_indptr = a->kv_indptr;
+  p.kv_indices = a->kv_indices;
+  p.out = static_cast<uint16_t*>(a->out);
+  p.out_lse = a->out_lse;
+  p.pool_tokens = a->pool_tokens;
+  p.B = a->B;
+  p.Hq = a->Hq;
+  p.Hkv = a->Hkv;
+  p.M = 1;
+  p.window_left = a->window_left;
+  p.q_scale = static_cast<float>(a->sm_scale * 1.4426950408889634);
+  const int64_t blocks = (a->total_q + kRows - 1) / kRows + a->B;
+  hipLaunchKernelGGL(window_kernel<false>, dim3(grid_for(blocks * a->Hq)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), p);
+  HIP_OK(hipGetLastError());
+  return MAC_OK;
+}
+
+extern "C" int mac_prefill_rectify_update_cache_bf16(const MacRectifyArgs* a, void* stream) {
+  REQUIRE(a != nullptr, "args is NULL");
+  REQUIRE(a->struct_size == sizeof(MacRectifyArgs), "struct_size mismatch (%u vs %zu)", a->struct_size,
+          sizeof(MacRectifyArgs));
+  REQUIRE(a->abi_version == MAC_ABI_VERSION, "abi_version mismatch");
+  if (int rc = check_window_common(a->B, a->Hq, a->Hkv, a->D, a->total_q, a->pool_tokens, a->q_post, a->k_buffer,
+                                   a->v_buffer, a->qo_indptr, a->kv_indptr, a->kv_indices))
+    return rc;
+  REQUIRE(a->M > 0, "capacity (M) must be > 0");
+  REQUIRE(a->R > 0, "R must be > 0");
+  REQUIRE(a->semantic_pos_ahead >= 1, "semantic_pos_ahead must be >= 1 (the window is S keys)");
+  REQUIRE(a->front_sink_tokens >= 0, "front_sink_tokens must be >= 0");
+  REQUIRE(a->sink_mode == 0 || a->sink_mode == 1, "sink_mode must be 0 or 1");
+  REQUIRE(a->request_length_len == a->R || a->request_length_len == a->B, "request_length must be [R] or [B]");
+  REQUIRE(a->src_q && a->o_full && a->lse_full && a->q_cache && a->attn_cache && a->lse_cache &&
+              a->request_length && a->req_ids,
+          "null pointer argument");
+  if (a->B == 0 || a->total_q == 0) return MAC_OK;
+  WindowParams p{};
+  p.q = static_cast<const uint16_t*>(a->q_post);
+  p.k = static_cast<const uint16_t*>(a->k_buffer);
+  p.v = static_cast<const uint16_t*>(a->v_buffer);
+  p.qo_indptr = a->qo_indptr;
+  p.kv_indptr = a->kv_indptr;
+  p.kv_indices = a->kv_indices;
+  p.src_q = static_cast<const uint16_t*>(a->src_q);
+  p.o_full = static_cast<const uint16_t*>(a->o_full);
+  p.lse_full = a->lse_full;
+  p.q_cache = static_cast<uint16_t*>(a->q_cache);
+  p.attn_cache = static_cast<uint16_t*>(a->attn_cache);
+  p.lse_cache = a->lse_cache;
+  p.q_post_cache = static_cast<uint16_t*>(a->q_post_cache);
+  p.request_length = a->request_length;
+  p.req_ids = a->req_ids;
+  p.pool_tokens = a->pool_tokens;
+  p.B = a->B;
+  p.Hq = a->Hq;
+  p.Hkv = a->Hkv;
+  p.R = a->R;
+  p.M = a->M;
+  p.S = a->semantic_pos_ahead;
+  p.F = a->front_sink_tokens;
+  p.sink_mode = a->sink_mode;
+  // the by-batch form wins when R == B, as in mac_prefill_update_cache
+  p.rl_by_batch = a->request_length_len == a->B;
+  p.q_scale = static_cast<float>(a->sm_scale * 1.4426950408889634);
+  const int64_t kept = std::min<int64_t>(a->total_q, static_cast<int64_t>(a->B) * a->M);
+  const int64_t blocks = (kept + kRows - 1) / kRows + a->B;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(window_kernel<true>, dim3(grid_for(blocks * a->Hq)), dim3(256), 0, s, p);
+  HIP_OK(hipGetLastError());
+  if (!p.rl_by_batch) {
+    hipLaunchKernelGGL(bump_kernel, dim3((a->B + 255) / 256), dim3(256), 0, s, a->request_length, a->req_ids,
+                       a->qo_indptr, a->B, a->R);
+    HIP_OK(hipGetLastError());
+  }
+  return MAC_OK;
+}

@@ -77,9 +77,41 @@ EXPORTED_SYMBOLS = (
     "mac_mark_persistent_ready",
     "mac_invalidate_persistent_ready",
     "mac_update_request_state",
+    "mac_update_then_downdate_bf16_inplace",
+    "mac_prefill_window_attention_bf16",
+    "mac_prefill_rectify_update_cache_bf16",
     "mac_last_error",
     "mac_abi_version",
 )
+
+
+class MacWindowAttentionArgs(ctypes.Structure):
+    """ctypes mirror of ``MacWindowAttentionArgs``."""
+
+    _fields_ = [
+        ("struct_size", _u32), ("abi_version", _u32),
+        ("q", _p), ("k_buffer", _p), ("v_buffer", _p), ("qo_indptr", _p), ("kv_indptr", _p),
+        ("kv_indices", _p), ("out", _p), ("out_lse", _p),
+        ("total_q", _i64), ("pool_tokens", _i64),
+        ("B", _i32), ("Hq", _i32), ("Hkv", _i32), ("D", _i32), ("window_left", _i32),
+        ("sm_scale", _f64),
+    ]
+
+
+class MacRectifyArgs(ctypes.Structure):
+    """ctypes mirror of ``MacRectifyArgs``."""
+
+    _fields_ = [
+        ("struct_size", _u32), ("abi_version", _u32),
+        ("q_post", _p), ("src_q", _p), ("o_full", _p), ("lse_full", _p), ("k_buffer", _p),
+        ("v_buffer", _p), ("qo_indptr", _p), ("kv_indptr", _p), ("kv_indices", _p),
+        ("q_cache", _p), ("attn_cache", _p), ("lse_cache", _p), ("q_post_cache", _p),
+        ("request_length", _p), ("req_ids", _p),
+        ("total_q", _i64), ("pool_tokens", _i64),
+        ("request_length_len", _i32), ("B", _i32), ("R", _i32), ("M", _i32), ("Hq", _i32),
+        ("Hkv", _i32), ("D", _i32), ("semantic_pos_ahead", _i32), ("front_sink_tokens", _i32),
+        ("sink_mode", _i32), ("sm_scale", _f64),
+    ]
 
 
 @lru_cache(maxsize=1)
@@ -109,6 +141,12 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         fn.restype = ctypes.c_int
     lib.mac_update_request_state.argtypes = [_p, _p, _p, _p, _p, _p, _i32, _i32, _p]
     lib.mac_update_request_state.restype = ctypes.c_int
+    lib.mac_update_then_downdate_bf16_inplace.argtypes = [_p, _p, _i32, _p, _p, _i32, _i64, _i32, _p]
+    lib.mac_update_then_downdate_bf16_inplace.restype = ctypes.c_int
+    lib.mac_prefill_window_attention_bf16.argtypes = [ctypes.POINTER(MacWindowAttentionArgs), _p]
+    lib.mac_prefill_window_attention_bf16.restype = ctypes.c_int
+    lib.mac_prefill_rectify_update_cache_bf16.argtypes = [ctypes.POINTER(MacRectifyArgs), _p]
+    lib.mac_prefill_rectify_update_cache_bf16.restype = ctypes.c_int
     if lib.mac_abi_version() != ABI_VERSION:
         raise RuntimeError(
             f"{path} has ABI version {lib.mac_abi_version()}, binding expects {ABI_VERSION}"
@@ -536,3 +574,159 @@ def load_mac_persistent_decode_extension(verbose: bool = False, fast_math: bool 
 def load_mac_prefill_update_cache_extension(verbose: bool = False) -> Any:
     """Reference bridge.py:172-187."""
     return PrefillUpdateCacheExtension(load_library())
+
+
+# ------------------------------------------------- prefill rectification ---
+
+_LSE_DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+
+class MergeDowndateExtension:
+    """Replaces the module built from mac_merge_downdate_cache.cu
+    (reference bridge.py:191-209, binding mac_merge_downdate_cache.cu:320-407)."""
+
+    def __init__(self, lib: ctypes.CDLL):
+        self._lib = lib
+
+    def mac_update_then_downdate_bf16_inplace(self, out1_bf16, lse1_any, out2_bf16, lse2_any) -> None:
+        """(out2, lse2) <- (out1, lse1) minus (out2, lse2), in place.  Checks
+        and messages of mac_merge_downdate_cache.cu:324-347."""
+        _check(out1_bf16.is_cuda and out2_bf16.is_cuda, "out tensors must be CUDA")
+        _check(lse1_any.is_cuda and lse2_any.is_cuda, "lse tensors must be CUDA")
+        _check(out1_bf16.dtype == torch.bfloat16 and out2_bf16.dtype == torch.bfloat16,
+               "out tensors must be bfloat16")
+        _check(out1_bf16.dim() == 3, "out1 must be [N,H,D]")
+        _check(out2_bf16.shape == out1_bf16.shape, "out shapes must match [N,H,D]")
+        _check(lse1_any.dim() == 2, "lse1 must be [N,H]")
+        _check(lse2_any.shape == lse1_any.shape, "lse shapes must match [N,H]")
+        _check(out1_bf16.is_contiguous() and out2_bf16.is_contiguous(), "out tensors must be contiguous")
+        _check(lse1_any.is_contiguous() and lse2_any.is_contiguous(), "lse tensors must be contiguous")
+        _check(out1_bf16.device == out2_bf16.device, "out1/out2: tensors must be on the same device")
+        _check(out1_bf16.device == lse1_any.device, "out1/lse1: tensors must be on the same device")
+        _check(lse1_any.device == lse2_any.device, "lse1/lse2: tensors must be on the same device")
+        for name, t in (("lse1", lse1_any), ("lse2", lse2_any)):
+            _check(t.dtype in _LSE_DTYPES,
+                   f"{name} must be float32, bfloat16, or float16; got {t.dtype}")
+        n, h, d = (int(x) for x in out1_bf16.shape)
+        _check(tuple(lse1_any.shape) == (n, h), "lse1 must be [N,H]")
+        with torch.cuda.device(out1_bf16.device):
+            rc = self._lib.mac_update_then_downdate_bf16_inplace(
+                _ptr(out1_bf16), _ptr(lse1_any), _LSE_DTYPES[lse1_any.dtype], _ptr(out2_bf16),
+                _ptr(lse2_any), _LSE_DTYPES[lse2_any.dtype], n * h, d, _stream(out1_bf16.device))
+        _raise_on(self._lib, rc)
+
+
+def _check_ragged(q, k_buffer, v_buffer, qo_indptr, kv_indptr, kv_indices):
+    for name, t, dt in (("q", q, torch.bfloat16), ("k_buffer", k_buffer, torch.bfloat16),
+                        ("v_buffer", v_buffer, torch.bfloat16), ("qo_indptr", qo_indptr, torch.int32),
+                        ("kv_indptr", kv_indptr, torch.int32), ("kv_indices", kv_indices, torch.int32)):
+        _check(t.is_cuda, f"{name} must be CUDA")
+        _check(t.is_contiguous(), f"{name} must be contiguous")
+        _check(t.dtype == dt, f"{name} has wrong dtype")
+    _check(q.dim() == 3 and int(q.shape[2]) == _HEAD_DIM, "q must be [total_q,Hq,128]")
+    _check(k_buffer.dim() == 3 and k_buffer.shape == v_buffer.shape, "k/v buffers must be [pool,Hkv,128]")
+    _check(int(k_buffer.shape[2]) == _HEAD_DIM, "k/v head_dim mismatch")
+    _check(int(q.shape[1]) % int(k_buffer.shape[1]) == 0, "Hq must be a multiple of Hkv")
+    _check(qo_indptr.dim() == 1 and kv_indptr.shape == qo_indptr.shape, "indptr must be [B+1]")
+
+
+class PrefillRectifyExtension:
+    """Prefill rectification on gfx950.  ``window_attention_return_lse`` stands
+    in for the windowed FlashInfer pass of flashinfer_hooks.py:2436-2466
+    (returning natural-log lse, i.e. the value after the reference's ln 2
+    scaling at :2467); ``mac_prefill_rectify_update_cache`` fuses that pass,
+    the downdate (:2468-2472) and the ring write of _offload_fast_cache
+    (:2482) for the rows the ring keeps."""
+
+    def __init__(self, lib: ctypes.CDLL):
+        self._lib = lib
+
+    def window_attention_return_lse(self, q, k_buffer, v_buffer, qo_indptr, kv_indptr, kv_indices,
+                                    window_left: int, sm_scale: float, out=None, out_lse=None):
+        _check_ragged(q, k_buffer, v_buffer, qo_indptr, kv_indptr, kv_indices)
+        total_q, hq, _ = (int(x) for x in q.shape)
+        if out is None:
+            out = torch.empty_like(q)
+        if out_lse is None:
+            out_lse = torch.empty(total_q, hq, device=q.device, dtype=torch.float32)
+        _check(out.shape == q.shape and out.dtype == torch.bfloat16 and out.is_contiguous(),
+               "out must be a contiguous bf16 tensor shaped like q")
+        _check(tuple(out_lse.shape) == (total_q, hq) and out_lse.dtype == torch.float32
+               and out_lse.is_contiguous(), "out_lse must be contiguous f32 [total_q,Hq]")
+        a = MacWindowAttentionArgs()
+        a.struct_size = ctypes.sizeof(MacWindowAttentionArgs)
+        a.abi_version = ABI_VERSION
+        a.q, a.k_buffer, a.v_buffer = _ptr(q), _ptr(k_buffer), _ptr(v_buffer)
+        a.qo_indptr, a.kv_indptr, a.kv_indices = _ptr(qo_indptr), _ptr(kv_indptr), _ptr(kv_indices)
+        a.out, a.out_lse = _ptr(out), _ptr(out_lse)
+        a.total_q, a.pool_tokens = total_q, int(k_buffer.shape[0])
+        a.B, a.Hq, a.Hkv, a.D = int(qo_indptr.shape[0]) - 1, hq, int(k_buffer.shape[1]), _HEAD_DIM
+        a.window_left, a.sm_scale = int(window_left), float(sm_scale)
+        with torch.cuda.device(q.device):
+            rc = self._lib.mac_prefill_window_attention_bf16(ctypes.byref(a), _stream(q.device))
+        _raise_on(self._lib, rc)
+        return out, out_lse
+
+    def mac_prefill_rectify_update_cache(self, q_post, src_q, o_full, lse_full, k_buffer, v_buffer,
+                                         qo_indptr, kv_indptr, kv_indices, q_cache, attn_cache,
+                                         lse_cache, request_length, req_ids, semantic_pos_ahead: int,
+                                         front_sink_tokens: int, sm_scale: float, q_post_cache=None,
+                                         sink_mode: int = 0) -> None:
+        _check_ragged(q_post, k_buffer, v_buffer, qo_indptr, kv_indptr, kv_indices)
+        for name, t, dt in (("src_q", src_q, torch.bfloat16), ("o_full", o_full, torch.bfloat16),
+                            ("lse_full", lse_full, torch.float32), ("q_cache", q_cache, torch.bfloat16),
+                            ("attn_cache", attn_cache, torch.bfloat16),
+                            ("lse_cache", lse_cache, torch.float32),
+                            ("request_length", request_length, torch.int32),
+                            ("req_ids", req_ids, torch.int32)):
+            _check(t.is_cuda, f"{name} must be a CUDA tensor")
+            _check(t.is_contiguous(), f"{name} must be contiguous")
+            _check(t.dtype == dt, f"{name} has wrong dtype")
+        _check(src_q.shape == q_post.shape and o_full.shape == q_post.shape,
+               "src_q / o_full must match q_post [total_q,Hq,128]")
+        total_q, hq, _ = (int(x) for x in q_post.shape)
+        _check(tuple(lse_full.shape) == (total_q, hq), "lse_full must be [total_q,Hq]")
+        _check(q_cache.dim() == 4 and int(q_cache.shape[2]) == hq and int(q_cache.shape[3]) == _HEAD_DIM,
+               "q_cache must be [R,M,Hq,128]")
+        _check(attn_cache.shape == q_cache.shape, "attn_cache must match q_cache")
+        R, M = int(q_cache.shape[0]), int(q_cache.shape[1])
+        _check(tuple(lse_cache.shape) == (R, M, hq), "lse_cache shape mismatch")
+        B = int(qo_indptr.shape[0]) - 1
+        _check(int(req_ids.shape[0]) == B, "req_ids must be [B]")
+        _check(int(request_length.shape[0]) in (R, B), "request_length must be [R] or [B]")
+        qpc = None
+        if q_post_cache is not None and q_post_cache.numel() > 0:
+            _check(q_post_cache.is_cuda and q_post_cache.is_contiguous()
+                   and q_post_cache.dtype == torch.bfloat16 and q_post_cache.shape == q_cache.shape,
+                   "q_post_cache must be a contiguous bf16 CUDA tensor matching q_cache")
+            qpc = q_post_cache
+        a = MacRectifyArgs()
+        a.struct_size = ctypes.sizeof(MacRectifyArgs)
+        a.abi_version = ABI_VERSION
+        a.q_post, a.src_q, a.o_full, a.lse_full = _ptr(q_post), _ptr(src_q), _ptr(o_full), _ptr(lse_full)
+        a.k_buffer, a.v_buffer = _ptr(k_buffer), _ptr(v_buffer)
+        a.qo_indptr, a.kv_indptr, a.kv_indices = _ptr(qo_indptr), _ptr(kv_indptr), _ptr(kv_indices)
+        a.q_cache, a.attn_cache, a.lse_cache = _ptr(q_cache), _ptr(attn_cache), _ptr(lse_cache)
+        a.q_post_cache = _ptr(qpc)
+        a.request_length, a.req_ids = _ptr(request_length), _ptr(req_ids)
+        a.total_q, a.pool_tokens = total_q, int(k_buffer.shape[0])
+        a.request_length_len = int(request_length.shape[0])
+        a.B, a.R, a.M, a.Hq, a.Hkv, a.D = B, R, M, hq, int(k_buffer.shape[1]), _HEAD_DIM
+        a.semantic_pos_ahead, a.front_sink_tokens = int(semantic_pos_ahead), int(front_sink_tokens)
+        a.sink_mode, a.sm_scale = int(sink_mode), float(sm_scale)
+        with torch.cuda.device(q_post.device):
+            rc = self._lib.mac_prefill_rectify_update_cache_bf16(ctypes.byref(a), _stream(q_post.device))
+        _raise_on(self._lib, rc)
+
+
+@lru_cache(maxsize=1)
+def load_mac_merge_downdate_cache_extension(verbose: bool = False) -> Any:
+    """Reference bridge.py:191-209."""
+    return MergeDowndateExtension(load_library())
+
+
+@lru_cache(maxsize=1)
+def load_mac_prefill_rectify_extension(verbose: bool = False) -> Any:
+    """No reference counterpart (the reference uses FlashInfer's prefill
+    wrapper for the windowed pass)."""
+    return PrefillRectifyExtension(load_library())

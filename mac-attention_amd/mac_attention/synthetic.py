@@ -473,3 +473,45 @@ def plant_noisy_matches(torch, dev: dict, *, entries: dict, seed: int = 0):
         q = dev["q_pre"][n, h].float()
         z = torch.randn(q.shape, device=q.device, generator=g)
         dev["query_cache"][n, slot, h] = (math.sqrt(1.0 - eps * eps) * q + eps * z).to(torch.bfloat16)
+
+
+# ------------------------------------------------ prefill rectification ----
+
+
+@dataclass
+class PrefillCase:
+    """A ragged prefill chunk over a page-size-1 pool.  Request b has kv_lens[b]
+    keys (its prefix plus the chunk) and qo_lens[b] query rows, the last
+    qo_lens[b] positions.  Values are float32 holding bf16-exact numbers."""
+
+    q: np.ndarray            # [total_q, Hq, D]
+    k: np.ndarray            # [pool, Hkv, D]
+    v: np.ndarray            # [pool, Hkv, D]
+    qo_indptr: np.ndarray    # [B+1] int32
+    kv_indptr: np.ndarray    # [B+1] int32
+    kv_indices: np.ndarray   # [kv_indptr[B]] int32, a random permutation of pool rows
+    sm_scale: float = 1.0 / math.sqrt(128.0)
+
+    def positions(self, b: int) -> np.ndarray:
+        qlen = int(self.qo_indptr[b + 1] - self.qo_indptr[b])
+        kvlen = int(self.kv_indptr[b + 1] - self.kv_indptr[b])
+        return np.arange(kvlen - qlen, kvlen)
+
+
+def prefill_case(*, qo_lens, kv_lens, hq: int, hkv: int, seed: int = 0, spare_rows: int = 7,
+                 dim: int = 128, scale: float = 1.0) -> PrefillCase:
+    rng = np.random.default_rng(seed)
+    qo_lens = [int(x) for x in qo_lens]
+    kv_lens = [int(x) for x in kv_lens]
+    assert all(q <= k for q, k in zip(qo_lens, kv_lens))
+    total_kv = sum(kv_lens)
+    pool = total_kv + spare_rows
+    perm = rng.permutation(pool)[:total_kv].astype(np.int32)
+    return PrefillCase(
+        q=bf16_round(rng.standard_normal((sum(qo_lens), hq, dim)) * scale),
+        k=bf16_round(rng.standard_normal((pool, hkv, dim))),
+        v=bf16_round(rng.standard_normal((pool, hkv, dim))),
+        qo_indptr=np.concatenate([[0], np.cumsum(qo_lens)]).astype(np.int32),
+        kv_indptr=np.concatenate([[0], np.cumsum(kv_lens)]).astype(np.int32),
+        kv_indices=perm,
+    )

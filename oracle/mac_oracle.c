@@ -638,3 +638,261 @@ EXPORT void mac_oracle_update_request_state(int32_t* req_len, int32_t* match_req
     match_req_len[req] = c;
   }
 }
+
+/* ------------------------------------------- prefill rectification ---- */
+
+static float lse_in(const void* p, int dtype, int64_t i) {
+  if (dtype == 0) return ((const float*)p)[i];
+  uint16_t b = ((const uint16_t*)p)[i];
+  if (dtype == 1) return (float)bf16_to_d(b);
+  /* IEEE half */
+  uint32_t s = (uint32_t)(b >> 15), e = (uint32_t)((b >> 10) & 31), m = (uint32_t)(b & 1023);
+  float v;
+  if (e == 0) v = ldexpf((float)m, -24);
+  else if (e == 31) v = m ? NAN : INFINITY;
+  else v = ldexpf((float)(m | 1024), (int)e - 25);
+  return s ? -v : v;
+}
+
+static uint16_t f_to_half(float f) {
+  /* round to nearest even via float arithmetic on the scaled mantissa */
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  float a = fabsf(f);
+  if (isnan(f)) return (uint16_t)(sign | 0x7e00u);
+  if (a >= 65520.0f) return (uint16_t)(sign | 0x7c00u);
+  if (a < ldexpf(1.0f, -14)) { /* subnormal: multiple of 2^-24 */
+    float q = nearbyintf(ldexpf(a, 24));
+    return (uint16_t)(sign | (uint16_t)q);
+  }
+  int ex;
+  float fr = frexpf(a, &ex); /* a = fr * 2^ex, fr in [0.5, 1) */
+  float mant = nearbyintf(ldexpf(fr, 11)); /* 11 significant bits */
+  if (mant >= 2048.0f) { mant = 1024.0f; ex += 1; }
+  int he = ex - 1 + 15;
+  if (he >= 31) return (uint16_t)(sign | 0x7c00u);
+  return (uint16_t)(sign | (uint16_t)(he << 10) | ((uint16_t)mant - 1024u));
+}
+
+static void lse_out(void* p, int dtype, int64_t i, float v) {
+  if (dtype == 0) ((float*)p)[i] = v;
+  else if (dtype == 1) ((uint16_t*)p)[i] = f_to_bf16(v);
+  else ((uint16_t*)p)[i] = f_to_half(v);
+}
+
+/* Downdate control of MERGE:148-176: returns 0 = nothing left, 1 = no-op
+ * (keep state 1), 2 = regular, with t = e^(l2-l1) and r the new lse.  The
+ * branch tests run in float32 as in the reference so that decisions match. */
+static int downdate_control(float l1, float l2, double* t, double* r) {
+  float diff = l2 - l1;
+  float em1 = expm1f(diff);
+  int last_block = fabsf(em1) <= 1e-7f;
+  int invalid = (diff > 0.0f) && !last_block;
+  if (last_block) return 0;
+  if (invalid) return 1;
+  double dd = (double)l2 - (double)l1;
+  double one_minus = 1.0 - exp(dd);
+  double x = one_minus + 1e-7;
+  if (x < 1e-30) x = 1e-30;
+  *r = (double)l1 + log(x);
+  *t = exp(dd);
+  return 2;
+}
+
+/*
+ * MERGE:116-288 (kernel) and MERGE:320-401 (binding): in-place downdate of
+ * (out2, lse2) from (out1, lse1), rows x D, bf16 outputs, lse of dtype codes
+ * 0 = f32, 1 = bf16, 2 = f16.
+ */
+EXPORT void mac_oracle_update_then_downdate(const uint16_t* out1, const void* lse1, int lse1_dtype,
+                                            uint16_t* out2, void* lse2, int lse2_dtype,
+                                            int64_t rows, int D) {
+  for (int64_t g = 0; g < rows; ++g) {
+    float l1 = lse_in(lse1, lse1_dtype, g), l2 = lse_in(lse2, lse2_dtype, g);
+    double t = 0.0, r = 0.0;
+    int c = downdate_control(l1, l2, &t, &r);
+    const uint16_t* a = out1 + g * D;
+    uint16_t* b = out2 + g * D;
+    if (c == 0) {
+      /* scale 0: (o1 - 0 * o2) * 0 */
+      for (int i = 0; i < D; ++i) b[i] = d_to_bf16((bf16_to_d(a[i]) - 0.0 * bf16_to_d(b[i])) * 0.0);
+      lse_out(lse2, lse2_dtype, g, -INFINITY);
+    } else if (c == 1) {
+      for (int i = 0; i < D; ++i) b[i] = d_to_bf16(bf16_to_d(a[i]));
+      lse_out(lse2, lse2_dtype, g, l1);
+    } else {
+      double scale = exp((double)l1 - r);
+      for (int i = 0; i < D; ++i) b[i] = d_to_bf16((bf16_to_d(a[i]) - t * bf16_to_d(b[i])) * scale);
+      lse_out(lse2, lse2_dtype, g, (float)r);
+    }
+  }
+}
+
+/* Exact attention of one query row over the key positions [lo, hi) of
+ * request b (page size 1: position j is pool row kv_indices[kv_begin + j]),
+ * merged into st.  Natural-log lse. */
+static void window_state(const uint16_t* q, const uint16_t* k_buffer, const uint16_t* v_buffer,
+                         const int32_t* kv_indices, int64_t kv_begin, int Hkv, int hkv, int D,
+                         int lo, int hi, double sm_scale, State* st, double* logits) {
+  State w;
+  state_empty(&w, D);
+  if (hi > lo) {
+    double qd[128];
+    for (int i = 0; i < D; ++i) qd[i] = bf16_to_d(q[i]);
+    double m = -INFINITY;
+    for (int j = lo; j < hi; ++j) {
+      int64_t row = kv_indices[kv_begin + j];
+      const uint16_t* kr = k_buffer + (row * Hkv + hkv) * D;
+      double dot = 0.0;
+      for (int i = 0; i < D; ++i) dot += qd[i] * bf16_to_d(kr[i]);
+      logits[j - lo] = dot * sm_scale;
+      if (logits[j - lo] > m) m = logits[j - lo];
+    }
+    double sum = 0.0;
+    for (int i = 0; i < D; ++i) w.o[i] = 0.0;
+    for (int j = lo; j < hi; ++j) {
+      double p = exp(logits[j - lo] - m);
+      sum += p;
+      int64_t row = kv_indices[kv_begin + j];
+      const uint16_t* vr = v_buffer + (row * Hkv + hkv) * D;
+      for (int i = 0; i < D; ++i) w.o[i] += p * bf16_to_d(vr[i]);
+    }
+    for (int i = 0; i < D; ++i) w.o[i] /= sum;
+    w.lse = m + log(sum);
+  }
+  state_merge(st, &w, D);
+}
+
+/*
+ * Causal sliding-window prefill attention over a ragged batch with a
+ * page-size-1 pool (the FlashInfer call of HOOKS:2436-2466 with
+ * window_left = S - 1): query row i of request b sits at position
+ * kv_len - qo_len + i and attends to [pos - window_left, pos]
+ * (window_left < 0: [0, pos]).  out bf16, out_lse natural log.
+ */
+EXPORT void mac_oracle_window_attention(const uint16_t* q, const uint16_t* k_buffer,
+                                        const uint16_t* v_buffer, const int32_t* qo_indptr,
+                                        const int32_t* kv_indptr, const int32_t* kv_indices, int B,
+                                        int Hq, int Hkv, int D, int window_left, double sm_scale,
+                                        uint16_t* out, float* out_lse) {
+  const int G = Hq / Hkv;
+  int maxkv = 1;
+  for (int b = 0; b < B; ++b)
+    if (kv_indptr[b + 1] - kv_indptr[b] > maxkv) maxkv = kv_indptr[b + 1] - kv_indptr[b];
+  double* logits = (double*)malloc(sizeof(double) * (size_t)maxkv);
+  State* st = (State*)malloc(sizeof(State));
+  for (int b = 0; b < B; ++b) {
+    int qlen = qo_indptr[b + 1] - qo_indptr[b];
+    int kvlen = kv_indptr[b + 1] - kv_indptr[b];
+    for (int i = 0; i < qlen; ++i) {
+      int pos = kvlen - qlen + i;
+      int lo = window_left < 0 ? 0 : pos - window_left;
+      if (lo < 0) lo = 0;
+      int64_t row = (int64_t)qo_indptr[b] + i;
+      for (int h = 0; h < Hq; ++h) {
+        state_empty(st, D);
+        window_state(q + (row * Hq + h) * D, k_buffer, v_buffer, kv_indices, kv_indptr[b], Hkv,
+                     h / G, D, lo, pos + 1, sm_scale, st, logits);
+        for (int d = 0; d < D; ++d) out[(row * Hq + h) * D + d] = d_to_bf16(st->o[d]);
+        out_lse[row * Hq + h] = (float)st->lse;
+      }
+    }
+  }
+  free(st);
+  free(logits);
+}
+
+/*
+ * Fused rectification + ring update: for the rows the ring keeps (the last
+ * min(len_b, M) rows of request b, PREFILL:201-269), the prefix state over
+ * [0, E) (sink_mode 1: [min(F, E), E)), E = pos + 1 - S, obtained as the full
+ * causal state (o_full, lse_full) minus the window [E, pos + 1) (and the sink)
+ * with the downdate of MERGE:148-176, then stored like mac_prefill_update_cache
+ * with offsets = qo_indptr.  The composition is HOOKS:2436-2482; sink_mode 0
+ * with F > 0 writes lse = -inf as HOOKS:2205-2215 does.  E <= 0 (or E <= F
+ * in sink_mode 1) leaves nothing: o = 0, lse = -inf.
+ */
+EXPORT void mac_oracle_rectify_update_cache(
+    const uint16_t* q_post, const uint16_t* src_q, const uint16_t* o_full, const float* lse_full,
+    const uint16_t* k_buffer, const uint16_t* v_buffer, const int32_t* qo_indptr,
+    const int32_t* kv_indptr, const int32_t* kv_indices, uint16_t* q_cache, uint16_t* attn_cache,
+    float* lse_cache, uint16_t* q_post_cache, int32_t* request_length, int request_length_len,
+    const int32_t* req_ids, int B, int R, int M, int Hq, int Hkv, int D, int S, int F,
+    int sink_mode, double sm_scale) {
+  if (M <= 0 || B == 0) return;
+  const int G = Hq / Hkv;
+  const int by_batch = request_length_len == B;
+  const size_t rowsz = (size_t)Hq * D;
+  int maxkv = 1;
+  for (int b = 0; b < B; ++b)
+    if (kv_indptr[b + 1] - kv_indptr[b] > maxkv) maxkv = kv_indptr[b + 1] - kv_indptr[b];
+  double* logits = (double*)malloc(sizeof(double) * (size_t)maxkv);
+  State* st = (State*)malloc(sizeof(State));
+  int32_t* before = (int32_t*)malloc(sizeof(int32_t) * (size_t)B);
+  for (int b = 0; b < B; ++b) {
+    int req = req_ids[b];
+    before[b] = 0;
+    if (by_batch) before[b] = request_length[b];
+    else if (req >= 0 && req < R) before[b] = request_length[req];
+  }
+  for (int b = 0; b < B; ++b) {
+    int req = req_ids[b];
+    int Ni = qo_indptr[b + 1] - qo_indptr[b];
+    if (Ni <= 0 || req < 0 || req >= R) continue;
+    int kvlen = kv_indptr[b + 1] - kv_indptr[b];
+    int start = Ni > M ? Ni - M : 0;
+    int L = before[b] < 0 ? 0 : before[b];
+    int base_dest = (int)(((int64_t)L + start) % M);
+    for (int i = start; i < Ni; ++i) {
+      int dst = base_dest + (i - start);
+      if (dst >= M) dst -= M;
+      size_t drow = (size_t)req * M + dst;
+      int64_t srow = (int64_t)qo_indptr[b] + i;
+      int pos = kvlen - Ni + i;
+      int E = pos + 1 - S;
+      int floor_e = (sink_mode == 1 && F > 0) ? F : 0;
+      for (int h = 0; h < Hq; ++h) {
+        double o[128];
+        double lse;
+        if (E <= floor_e) {
+          for (int d = 0; d < D; ++d) o[d] = 0.0;
+          lse = -INFINITY;
+        } else {
+          state_empty(st, D);
+          const uint16_t* qh = q_post + (srow * Hq + h) * D;
+          window_state(qh, k_buffer, v_buffer, kv_indices, kv_indptr[b], Hkv, h / G, D, E, pos + 1,
+                       sm_scale, st, logits);
+          if (sink_mode == 1 && F > 0)
+            window_state(qh, k_buffer, v_buffer, kv_indices, kv_indptr[b], Hkv, h / G, D, 0,
+                         F < E ? F : E, sm_scale, st, logits);
+          float l1 = lse_full[srow * Hq + h], l2 = (float)st->lse;
+          const uint16_t* of = o_full + (srow * Hq + h) * D;
+          double t = 0.0, r = 0.0;
+          int c = downdate_control(l1, l2, &t, &r);
+          if (c == 0) {
+            for (int d = 0; d < D; ++d) o[d] = 0.0;
+            lse = -INFINITY;
+          } else if (c == 1) {
+            for (int d = 0; d < D; ++d) o[d] = bf16_to_d(of[d]);
+            lse = l1;
+          } else {
+            double scale = exp((double)l1 - r);
+            for (int d = 0; d < D; ++d) o[d] = (bf16_to_d(of[d]) - t * st->o[d]) * scale;
+            lse = r;
+          }
+          if (sink_mode == 0 && F > 0) lse = -INFINITY;
+        }
+        for (int d = 0; d < D; ++d) attn_cache[drow * rowsz + (size_t)h * D + d] = d_to_bf16(o[d]);
+        lse_cache[drow * Hq + h] = (float)lse;
+      }
+      memcpy(q_cache + drow * rowsz, src_q + (size_t)srow * rowsz, rowsz * 2);
+      if (q_post_cache)
+        for (size_t j = 0; j < rowsz; ++j) q_post_cache[drow * rowsz + j] = 0x7fc0;
+    }
+    if (!by_batch) request_length[req] += Ni;
+  }
+  free(before);
+  free(st);
+  free(logits);
+}

@@ -267,3 +267,75 @@ def update_request_state(req_len, match_req_len, cache_lens, req_ids, seq_lens, 
         _ptr(req_len, _i32p), _ptr(match_req_len, _i32p), _ptr(cache_lens, _i32p),
         _ptr(req_ids, _i32p), _ptr(seq_lens, _i32p), _ptr(cur_lens, _i32p),
         int(req_ids.shape[0]), int(req_len.shape[0]))
+
+
+# ------------------------------------------------- prefill rectification ---
+
+_LSE_CODES = {np.dtype(np.float32): 0, "bf16": 1, np.dtype(np.float16): 2}
+
+
+def update_then_downdate(out1, lse1, out2, lse2, *, lse1_bf16=False, lse2_bf16=False):
+    """In-place restatement of ``mac_update_then_downdate_bf16_inplace`` on
+    numpy arrays: out1/out2 uint16 bf16 bits [..., D]; lse arrays float32,
+    float16, or uint16 bf16 bits (flagged by ``lse*_bf16``).  Writes out2/lse2."""
+    assert out1.dtype == np.uint16 and out2.dtype == np.uint16 and out2.flags["C_CONTIGUOUS"]
+    assert lse2.flags["C_CONTIGUOUS"]
+    out1 = np.ascontiguousarray(out1)
+    lse1 = np.ascontiguousarray(lse1)
+    c1 = 1 if lse1_bf16 else _LSE_CODES[lse1.dtype]
+    c2 = 1 if lse2_bf16 else _LSE_CODES[lse2.dtype]
+    D = int(out1.shape[-1])
+    rows = int(out1.size // D)
+    assert out2.size == out1.size and lse1.size == rows and lse2.size == rows
+    lib().mac_oracle_update_then_downdate(
+        _ptr(out1, _u16p), lse1.ctypes.data_as(ctypes.c_void_p), c1, _ptr(out2, _u16p),
+        lse2.ctypes.data_as(ctypes.c_void_p), c2, ctypes.c_int64(rows), D)
+
+
+def window_attention(q, k_buffer, v_buffer, qo_indptr, kv_indptr, kv_indices, *, window_left,
+                     sm_scale):
+    """Causal sliding-window attention over a ragged batch (bf16 bits in,
+    bf16 bits out, natural-log lse)."""
+    c = np.ascontiguousarray
+    q = c(q, dtype=np.uint16)
+    k_buffer = c(k_buffer, dtype=np.uint16)
+    v_buffer = c(v_buffer, dtype=np.uint16)
+    qo_indptr = c(qo_indptr, dtype=np.int32)
+    kv_indptr = c(kv_indptr, dtype=np.int32)
+    kv_indices = c(kv_indices, dtype=np.int32)
+    total_q, hq, d = q.shape
+    hkv = k_buffer.shape[1]
+    out = np.zeros_like(q)
+    lse = np.zeros((total_q, hq), np.float32)
+    lib().mac_oracle_window_attention(
+        _ptr(q, _u16p), _ptr(k_buffer, _u16p), _ptr(v_buffer, _u16p), _ptr(qo_indptr, _i32p),
+        _ptr(kv_indptr, _i32p), _ptr(kv_indices, _i32p), int(qo_indptr.shape[0] - 1), hq, hkv, d,
+        int(window_left), ctypes.c_double(sm_scale), _ptr(out, _u16p), _ptr(lse, _f32p))
+    return out, lse
+
+
+def rectify_update_cache(q_post, src_q, o_full, lse_full, k_buffer, v_buffer, qo_indptr,
+                         kv_indptr, kv_indices, q_cache, attn_cache, lse_cache, request_length,
+                         req_ids, *, semantic_pos_ahead, front_sink_tokens=0, sink_mode=0,
+                         sm_scale, q_post_cache=None):
+    """In-place restatement of ``mac_prefill_rectify_update_cache_bf16``
+    (ring arrays and request_length are updated)."""
+    c = np.ascontiguousarray
+    for arr, dt in ((q_cache, np.uint16), (attn_cache, np.uint16), (lse_cache, np.float32),
+                    (request_length, np.int32)):
+        assert arr.dtype == dt and arr.flags["C_CONTIGUOUS"]
+    q_post, src_q, o_full = (c(x, dtype=np.uint16) for x in (q_post, src_q, o_full))
+    lse_full = c(lse_full, dtype=np.float32)
+    k_buffer = c(k_buffer, dtype=np.uint16)
+    v_buffer = c(v_buffer, dtype=np.uint16)
+    qo_indptr, kv_indptr, kv_indices, req_ids = (
+        c(x, dtype=np.int32) for x in (qo_indptr, kv_indptr, kv_indices, req_ids))
+    r, m, hq, d = q_cache.shape
+    lib().mac_oracle_rectify_update_cache(
+        _ptr(q_post, _u16p), _ptr(src_q, _u16p), _ptr(o_full, _u16p), _ptr(lse_full, _f32p),
+        _ptr(k_buffer, _u16p), _ptr(v_buffer, _u16p), _ptr(qo_indptr, _i32p),
+        _ptr(kv_indptr, _i32p), _ptr(kv_indices, _i32p), _ptr(q_cache, _u16p),
+        _ptr(attn_cache, _u16p), _ptr(lse_cache, _f32p), _ptr(q_post_cache, _u16p),
+        _ptr(request_length, _i32p), int(request_length.shape[0]), _ptr(req_ids, _i32p),
+        int(req_ids.shape[0]), r, m, hq, int(k_buffer.shape[1]), d, int(semantic_pos_ahead),
+        int(front_sink_tokens), int(sink_mode), ctypes.c_double(sm_scale))

@@ -42,12 +42,14 @@ def test_library_exports_every_declared_symbol(bridge):
     assert lib.mac_abi_version() == bridge.ABI_VERSION
 
 
-def test_struct_layout_matches_header(bridge, tmp_path):
-    fields = [f[0] for f in bridge.MacDecodeArgs._fields_]
+@pytest.mark.parametrize("struct", ["MacDecodeArgs", "MacWindowAttentionArgs", "MacRectifyArgs"])
+def test_struct_layout_matches_header(bridge, tmp_path, struct):
+    cls = getattr(bridge, struct)
+    fields = [f[0] for f in cls._fields_]
     src = ['#include <stdio.h>', '#include <stddef.h>', '#include "mac_attention_amd.h"',
-           'int main(void) {', 'printf("size %zu\\n", sizeof(MacDecodeArgs));']
+           'int main(void) {', f'printf("size %zu\\n", sizeof({struct}));']
     for f in fields:
-        src.append(f'printf("{f} %zu\\n", offsetof(MacDecodeArgs, {f}));')
+        src.append(f'printf("{f} %zu\\n", offsetof({struct}, {f}));')
     src.append("return 0; }")
     c = tmp_path / "layout.c"
     c.write_text("\n".join(src))
@@ -55,9 +57,9 @@ def test_struct_layout_matches_header(bridge, tmp_path):
     subprocess.run(["gcc", "-I", os.path.dirname(HEADER), str(c), "-o", str(exe)], check=True)
     out = dict(l.split() for l in subprocess.run([str(exe)], capture_output=True, text=True,
                                                   check=True).stdout.splitlines())
-    assert int(out["size"]) == ctypes.sizeof(bridge.MacDecodeArgs)
+    assert int(out["size"]) == ctypes.sizeof(cls)
     for f in fields:
-        assert int(out[f]) == getattr(bridge.MacDecodeArgs, f).offset, f
+        assert int(out[f]) == getattr(cls, f).offset, f
 
 
 def test_bad_arguments_return_error_and_message(bridge):
@@ -80,6 +82,23 @@ def test_bad_arguments_return_error_and_message(bridge):
     assert lib.mac_mark_persistent_ready(None, None, None, None, 0, 4, None) == 0
     assert lib.mac_mark_persistent_ready(None, None, None, None, 2, 4, None) == 1
     assert b"NULL" in lib.mac_last_error()
+
+
+def test_prefill_entry_points_reject_bad_arguments(bridge):
+    lib = bridge.load_library()
+    assert lib.mac_update_then_downdate_bf16_inplace(None, None, 0, None, None, 5, 4, 128, None) == 1
+    assert b"lse2 must be float32, bfloat16, or float16" in lib.mac_last_error()
+    assert lib.mac_update_then_downdate_bf16_inplace(None, None, 0, None, None, 0, 0, 128, None) == 0
+    w = bridge.MacWindowAttentionArgs()
+    w.struct_size = ctypes.sizeof(w)
+    w.abi_version = bridge.ABI_VERSION
+    w.B, w.Hq, w.Hkv, w.D = 1, 8, 2, 64
+    assert lib.mac_prefill_window_attention_bf16(ctypes.byref(w), None) == 1
+    assert b"head_dim must be 128" in lib.mac_last_error()
+    r = bridge.MacRectifyArgs()
+    r.struct_size = ctypes.sizeof(r) - 4
+    assert lib.mac_prefill_rectify_update_cache_bf16(ctypes.byref(r), None) == 1
+    assert b"struct_size mismatch" in lib.mac_last_error()
 
 
 def test_binding_rejects_host_tensors(bridge):
