@@ -14,7 +14,8 @@
  * Reference paths are relative to the reference repository root.  "DECODE"
  * stands for attention/src/mac_attention/integrations/sglang/csrc/
  * mac_decode_persistent.cu, "PREFILL" for .../csrc/mac_prefill_update_cache.cu,
- * "MERGE" for .../csrc/mac_merge_downdate_cache.cu and "HOOKS" for
+ * "MERGE" for .../csrc/mac_merge_downdate_cache.cu, "ROPE" for
+ * .../csrc/mac_decode_rope_preserve.cu and "HOOKS" for
  * attention/src/mac_attention/integrations/sglang/flashinfer_hooks.py.
  */
 #ifndef MAC_ATTENTION_AMD_H_
@@ -301,6 +302,31 @@ typedef struct MacRectifyArgs {
 } MacRectifyArgs;
 
 MAC_API int mac_prefill_rectify_update_cache_bf16(const MacRectifyArgs* args, void* stream);
+
+/* ------------------------------------------------- decode RoPE + scatter --- */
+
+/* Replaces mac_decode_rope_preserve_q_bf16 (ROPE:174-269, kernel ROPE:36-156).
+ * For each decode token n < N (position positions[n], pool row cache_locs[n]):
+ * q_pre[n] = q[n] (all head_dim dims, before RoPE); q[n] and k[n] get RoPE on
+ * their first rotary_dim dims in place; k_buffer[cache_locs[n]] = RoPE(k[n]);
+ * v_buffer[cache_locs[n]] = v[n].  RoPE of pair (x0, x1) with c =
+ * cos_sin[pos][i], s = cos_sin[pos][rotary_dim/2 + i] is (x0 c - x1 s,
+ * x1 c + x0 s) in fp32 rounded to bf16; pairs are (i, i + rotary_dim/2) when
+ * is_neox, else (2i, 2i+1).
+ *   q bf16 [N, Hq*head_dim] with row stride q_stride0 (elements), likewise k, v
+ *   q_pre bf16 [q_pre_rows >= N, Hq, head_dim]; k_buffer/v_buffer bf16
+ *   [pool_tokens, Hkv, head_dim]; cos_sin_cache f32 [cos_sin_rows, >= rotary_dim]
+ *   with row stride cos_sin_stride0; positions / cache_locs i32 or i64 [>= N].
+ * Positions outside the table are clamped into it and pool rows outside
+ * [0, pool_tokens) are not written (the reference does not check either). */
+MAC_API int mac_decode_rope_preserve_q_bf16(void* q, int64_t q_stride0, void* k, int64_t k_stride0,
+                                            const void* v, int64_t v_stride0, void* q_pre, int64_t q_pre_rows,
+                                            void* k_buffer, void* v_buffer, int64_t pool_tokens,
+                                            const float* cos_sin_cache, int64_t cos_sin_rows,
+                                            int64_t cos_sin_stride0, int32_t rotary_dim, const void* positions,
+                                            int32_t positions_is_i64, const void* cache_locs,
+                                            int32_t cache_locs_is_i64, int64_t N, int32_t Hq, int32_t Hkv,
+                                            int32_t head_dim, int32_t is_neox, void* stream);
 
 /* Profiling variant of mac_persistent_decode_bf16: same arguments and effects,
  * plus HIP events on `stream` around each of the three kernels; synchronises

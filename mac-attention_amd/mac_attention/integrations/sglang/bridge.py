@@ -80,6 +80,7 @@ EXPORTED_SYMBOLS = (
     "mac_update_then_downdate_bf16_inplace",
     "mac_prefill_window_attention_bf16",
     "mac_prefill_rectify_update_cache_bf16",
+    "mac_decode_rope_preserve_q_bf16",
     "mac_last_error",
     "mac_abi_version",
 )
@@ -147,6 +148,10 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.mac_prefill_window_attention_bf16.restype = ctypes.c_int
     lib.mac_prefill_rectify_update_cache_bf16.argtypes = [ctypes.POINTER(MacRectifyArgs), _p]
     lib.mac_prefill_rectify_update_cache_bf16.restype = ctypes.c_int
+    lib.mac_decode_rope_preserve_q_bf16.argtypes = [
+        _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i32, _p, _i32, _p, _i32,
+        _i64, _i32, _i32, _i32, _i32, _p]
+    lib.mac_decode_rope_preserve_q_bf16.restype = ctypes.c_int
     if lib.mac_abi_version() != ABI_VERSION:
         raise RuntimeError(
             f"{path} has ABI version {lib.mac_abi_version()}, binding expects {ABI_VERSION}"
@@ -730,3 +735,72 @@ def load_mac_prefill_rectify_extension(verbose: bool = False) -> Any:
     """No reference counterpart (the reference uses FlashInfer's prefill
     wrapper for the windowed pass)."""
     return PrefillRectifyExtension(load_library())
+
+
+# ---------------------------------------------------- decode RoPE + scatter ---
+
+
+class DecodeRopePreserveExtension:
+    """Replaces the module built from mac_decode_rope_preserve.cu (reference
+    bridge.py:273-290, binding mac_decode_rope_preserve.cu:174-276)."""
+
+    def __init__(self, lib: ctypes.CDLL):
+        self._lib = lib
+
+    def mac_decode_rope_preserve_q_bf16(self, q, k, v, q_pre, k_buffer, v_buffer, cos_sin_cache,
+                                        positions, cache_locs, head_dim: int, is_neox: bool) -> None:
+        """Checks and messages of mac_decode_rope_preserve.cu:158-221."""
+        for name, t in (("q", q), ("k", k), ("v", v)):
+            _check(t.is_cuda, f"{name} must be CUDA")
+            _check(t.dtype == torch.bfloat16, f"{name} has wrong dtype")
+            _check(t.dim() == 2, f"{name} must have rank 2")
+            _check(t.stride(1) == 1, f"{name} must have contiguous last dimension")
+        for name, t in (("q_pre", q_pre), ("k_buffer", k_buffer), ("v_buffer", v_buffer)):
+            _check(t.is_cuda, f"{name} must be CUDA")
+            _check(t.dtype == torch.bfloat16, f"{name} has wrong dtype")
+            _check(t.dim() == 3, f"{name} must have rank 3")
+            _check(t.is_contiguous(), f"{name} must be contiguous")
+        _check(cos_sin_cache.is_cuda, "cos_sin_cache must be CUDA")
+        _check(cos_sin_cache.dtype == torch.float32, "cos_sin_cache has wrong dtype")
+        _check(cos_sin_cache.dim() == 2, "cos_sin_cache must have rank 2")
+        _check(cos_sin_cache.stride(1) == 1, "cos_sin_cache must have contiguous last dimension")
+        _check(positions.is_cuda, "positions must be CUDA")
+        _check(cache_locs.is_cuda, "cache_locs must be CUDA")
+        _check(positions.dim() == 1, "positions must have rank 1")
+        _check(cache_locs.dim() == 1, "cache_locs must have rank 1")
+        _check(positions.dtype in (torch.int32, torch.int64), "positions must be int32 or int64")
+        _check(cache_locs.dtype in (torch.int32, torch.int64), "cache_locs must be int32 or int64")
+        _check(positions.is_contiguous() and cache_locs.is_contiguous(),
+               "positions / cache_locs must be contiguous")
+        n = int(q.shape[0])
+        _check(int(k.shape[0]) == n and int(v.shape[0]) == n, "q/k/v batch mismatch")
+        _check(int(positions.shape[0]) >= n and int(cache_locs.shape[0]) >= n, "metadata batch too small")
+        head_dim = int(head_dim)
+        _check(head_dim > 0 and int(q.shape[1]) % head_dim == 0 and int(k.shape[1]) % head_dim == 0,
+               "invalid head_dim")
+        hq, hkv = int(q.shape[1]) // head_dim, int(k.shape[1]) // head_dim
+        _check(int(v.shape[1]) == hkv * head_dim, "v shape mismatch")
+        _check(int(q_pre.shape[0]) >= n and int(q_pre.shape[1]) == hq and int(q_pre.shape[2]) == head_dim,
+               "q_pre shape mismatch")
+        _check(int(k_buffer.shape[1]) == hkv and int(k_buffer.shape[2]) == head_dim,
+               "k_buffer shape mismatch")
+        _check(v_buffer.shape == k_buffer.shape, "v_buffer shape mismatch")
+        rot = int(cos_sin_cache.shape[1])
+        _check(0 < rot <= head_dim and rot % 2 == 0, "invalid rotary_dim")
+        if n == 0:
+            return
+        with torch.cuda.device(q.device):
+            rc = self._lib.mac_decode_rope_preserve_q_bf16(
+                _ptr(q), int(q.stride(0)), _ptr(k), int(k.stride(0)), _ptr(v), int(v.stride(0)),
+                _ptr(q_pre), int(q_pre.shape[0]), _ptr(k_buffer), _ptr(v_buffer), int(k_buffer.shape[0]),
+                _ptr(cos_sin_cache), int(cos_sin_cache.shape[0]), int(cos_sin_cache.stride(0)), rot,
+                _ptr(positions), int(positions.dtype == torch.int64), _ptr(cache_locs),
+                int(cache_locs.dtype == torch.int64), n, hq, hkv, head_dim, int(bool(is_neox)),
+                _stream(q.device))
+        _raise_on(self._lib, rc)
+
+
+@lru_cache(maxsize=1)
+def load_mac_decode_rope_preserve_extension(verbose: bool = False) -> Any:
+    """Reference bridge.py:273-290."""
+    return DecodeRopePreserveExtension(load_library())

@@ -896,3 +896,52 @@ EXPORT void mac_oracle_rectify_update_cache(
   free(st);
   free(logits);
 }
+
+/* -------------------------------------------- decode RoPE + scatter ---- */
+
+/*
+ * ROPE:36-156 decode_rope_preserve_kernel.  q/k rows have row strides
+ * q_stride0/k_stride0/v_stride0 (elements); positions and cache_locs are
+ * int64 here.  The rotation is evaluated in double and rounded once to bf16
+ * through float (the GPU evaluates it in fp32: results may differ by one bf16
+ * ulp on values next to a rounding boundary).  Positions outside the table
+ * are clamped, pool rows outside [0, pool) skipped.
+ */
+EXPORT void mac_oracle_rope_preserve(uint16_t* q, int64_t q_stride0, uint16_t* k, int64_t k_stride0,
+                                     const uint16_t* v, int64_t v_stride0, uint16_t* q_pre,
+                                     uint16_t* k_buffer, uint16_t* v_buffer, int64_t pool,
+                                     const float* cs, int64_t cs_rows, int64_t cs_stride0, int rot,
+                                     const int64_t* positions, const int64_t* cache_locs, int64_t N,
+                                     int Hq, int Hkv, int D, int neox) {
+  const int half = rot / 2;
+  for (int64_t n = 0; n < N; ++n) {
+    int64_t pos = positions[n];
+    if (pos < 0) pos = 0;
+    if (pos >= cs_rows) pos = cs_rows - 1;
+    const float* c = cs + pos * cs_stride0;
+    int64_t loc = cache_locs[n];
+    int loc_ok = loc >= 0 && loc < pool;
+    for (int pass = 0; pass < 2; ++pass) {
+      int H = pass == 0 ? Hq : Hkv;
+      uint16_t* row = pass == 0 ? q + n * q_stride0 : k + n * k_stride0;
+      for (int h = 0; h < H; ++h) {
+        uint16_t* x = row + (int64_t)h * D;
+        if (pass == 0)
+          for (int d = 0; d < D; ++d) q_pre[(n * Hq + h) * D + d] = x[d];
+        for (int i = 0; i < half; ++i) {
+          int d0 = neox ? i : 2 * i, d1 = neox ? i + half : 2 * i + 1;
+          double x0 = bf16_to_d(x[d0]), x1 = bf16_to_d(x[d1]);
+          double cc = c[i], ss = c[half + i];
+          x[d0] = d_to_bf16(x0 * cc - x1 * ss);
+          x[d1] = d_to_bf16(x1 * cc + x0 * ss);
+        }
+        if (pass == 1 && loc_ok)
+          for (int d = 0; d < D; ++d) k_buffer[(loc * Hkv + h) * D + d] = x[d];
+      }
+    }
+    if (loc_ok)
+      for (int h = 0; h < Hkv; ++h)
+        for (int d = 0; d < D; ++d)
+          v_buffer[(loc * Hkv + h) * D + d] = v[n * v_stride0 + (int64_t)h * D + d];
+  }
+}

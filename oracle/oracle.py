@@ -339,3 +339,31 @@ def rectify_update_cache(q_post, src_q, o_full, lse_full, k_buffer, v_buffer, qo
         _ptr(request_length, _i32p), int(request_length.shape[0]), _ptr(req_ids, _i32p),
         int(req_ids.shape[0]), r, m, hq, int(k_buffer.shape[1]), d, int(semantic_pos_ahead),
         int(front_sink_tokens), int(sink_mode), ctypes.c_double(sm_scale))
+
+
+# ---------------------------------------------------- decode RoPE + scatter ---
+
+
+def rope_preserve(q, k, v, q_pre, k_buffer, v_buffer, cos_sin_cache, positions, cache_locs, *,
+                  head_dim, is_neox):
+    """In-place restatement of ``mac_decode_rope_preserve_q_bf16``: q/k/v are
+    uint16 bf16-bit arrays [N, H*head_dim] (row views allowed: the row stride
+    is taken from the array), q_pre/k_buffer/v_buffer uint16 arrays."""
+    for a in (q, k, q_pre, k_buffer, v_buffer):
+        assert a.dtype == np.uint16
+    for a in (q, k, v):
+        assert a.strides[1] == 2
+    for a in (q_pre, k_buffer, v_buffer):
+        assert a.flags["C_CONTIGUOUS"]
+    cs = np.ascontiguousarray(cos_sin_cache, dtype=np.float32)
+    positions = np.ascontiguousarray(positions, dtype=np.int64)
+    cache_locs = np.ascontiguousarray(cache_locs, dtype=np.int64)
+    n = q.shape[0]
+    lib().mac_oracle_rope_preserve(
+        q.ctypes.data_as(_u16p), ctypes.c_int64(q.strides[0] // 2), k.ctypes.data_as(_u16p),
+        ctypes.c_int64(k.strides[0] // 2), v.ctypes.data_as(_u16p), ctypes.c_int64(v.strides[0] // 2),
+        _ptr(q_pre, _u16p), _ptr(k_buffer, _u16p), _ptr(v_buffer, _u16p),
+        ctypes.c_int64(k_buffer.shape[0]), _ptr(cs, _f32p), ctypes.c_int64(cs.shape[0]),
+        ctypes.c_int64(cs.shape[1]), int(cs.shape[1]), _ptr(positions, _i64p),
+        _ptr(cache_locs, _i64p), ctypes.c_int64(n), int(q.shape[1] // head_dim),
+        int(k.shape[1] // head_dim), int(head_dim), int(bool(is_neox)))
