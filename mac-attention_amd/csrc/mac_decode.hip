@@ -125,6 +125,7 @@ struct AttnParams {
   int cap;                 // task slots per group
   int F;
   int tile_tokens;  // the caller's tile size (task_counts[3] only)
+  int tasks_per_wg;  // target tasks per workgroup of the plan
   float q_scale;  // sm_scale * log2(e)
 };
 
@@ -467,6 +468,12 @@ __device__ __forceinline__ GroupSpans load_spans(const int32_t* rect_begin, cons
   return s;
 }
 
+// Band pieces of a group that span a full chunk (the first ones; only the
+// last band piece can be shorter).
+__device__ __forceinline__ int full_band_pieces(const GroupSpans& s) {
+  return (s.new_end - s.band_begin) / s.chunk;
+}
+
 // Block-wide exclusive scan of per-thread values (256 threads).
 __device__ __forceinline__ int block_exclusive_scan(int v, int* s_tmp, int& total) {
   const int lane = threadIdx.x & 63;
@@ -494,16 +501,21 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* s_tmp, int& tota
 // tasks per workgroup bounds the end-of-kernel imbalance to a few percent,
 // while a task of at least kMinChunk tokens amortises its fixed cost (plan
 // lookup, Q staging, pipeline fill, partial write).
-constexpr int kTasksPerWorkgroup = 12;
+constexpr int kTasksPerWorkgroup = 12;  // default of AttnParams::tasks_per_wg
 constexpr int kMinChunk = 256;
 constexpr int kMaxChunk = 16384;
 
 // Every workgroup of span_attention derives the same task list: the chunk C
 // from the total token count of all groups (kTasksPerWorkgroup tasks per
-// workgroup, a multiple of 64 tokens in [kMinChunk, kMaxChunk]), then
-// per-group task counts and their exclusive prefix sums in s_off[0..NG).
-// Workgroup 0 also publishes the per-group chunk and task counts for
-// merge_write and the task counters.
+// workgroup, a multiple of 64 tokens in [kMinChunk, kMaxChunk]), then the
+// tasks in two classes, largest first: class A holds the band pieces of full
+// chunk length, class B everything shorter (sinks, band remainders, tails,
+// and the whole bands of hit groups).  Workgroups fetch A tasks before B
+// tasks, so the end of the kernel is filled with short tasks and the idle
+// time of the last workgroups is bounded by a short task, not a full chunk.
+// s_off[0..NG] holds the exclusive prefix sums of the per-group A counts,
+// s_off[NG+1 .. 2NG+1] those of the B counts.  Workgroup 0 also publishes the
+// per-group chunk and task counts for merge_write and the task counters.
 __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& total_tasks_out,
                            int& chunk_out) {
   const int tid = threadIdx.x;
@@ -532,24 +544,35 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
     for (int w = 0; w < kWaves; ++w) tok += s_tok[w];
     __syncthreads();
   }
-  const long long target_tasks = static_cast<long long>(kTasksPerWorkgroup) * W;
+  const long long target_tasks = static_cast<long long>(p.tasks_per_wg) * W;
   int chunk = static_cast<int>((tok + target_tasks - 1) / target_tasks);
   chunk = ceil_div(max(chunk, kMinChunk), 64) * 64;
   chunk = min(chunk, kMaxChunk);
-  int my_tasks = 0;
+  int* s_offb = s_off + NG + 1;
+  int my_a = 0, my_b = 0;
   for (int g = g_lo; g < g_hi; ++g) {
     GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, g, p.F, chunk, p.cap);
-    s_off[g] = sp.n_sink + sp.n_band + sp.n_tail;
-    my_tasks += s_off[g];
+    const int na = full_band_pieces(sp);
+    s_off[g] = na;
+    s_offb[g] = sp.n_sink + sp.n_band + sp.n_tail - na;
+    my_a += na;
+    my_b += s_offb[g];
   }
-  int total_tasks = 0;
-  int base = block_exclusive_scan(my_tasks, s_tmp, total_tasks);
+  int total_a = 0, total_b = 0;
+  int base_a = block_exclusive_scan(my_a, s_tmp, total_a);
+  int base_b = block_exclusive_scan(my_b, s_tmp, total_b);
   for (int g = g_lo; g < g_hi; ++g) {
-    const int cnt = s_off[g];
-    s_off[g] = base;
-    base += cnt;
+    const int ca = s_off[g], cb = s_offb[g];
+    s_off[g] = base_a;
+    s_offb[g] = total_a + base_b;
+    base_a += ca;
+    base_b += cb;
   }
-  if (tid == 0) s_off[NG] = total_tasks;
+  const int total_tasks = total_a + total_b;
+  if (tid == 0) {
+    s_off[NG] = total_a;
+    s_offb[NG] = total_tasks;
+  }
   __syncthreads();
 
   if (blockIdx.x == 0) {
@@ -620,7 +643,10 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
 // Dynamic task fetch: the counter is zeroed by match_decide, which runs
 // before this kernel on the same stream, so every step (and every graph
 // replay) starts from task 0.  Ends with a barrier, so the previous task's
-// LDS use is complete before the caller starts the next one.
+// LDS use is complete before the caller starts the next one.  (Claiming the
+// next task one task ahead hides the atomic's round trip but hands two tasks
+// to the first workgroups when there are about as many tasks as workgroups,
+// which measured slower.)
 __device__ __forceinline__ int next_task(const AttnParams& p, int& s_task) {
   __syncthreads();
   if (threadIdx.x == 0) s_task = atomicAdd(p.task_counter, 1);
@@ -640,16 +666,28 @@ struct TaskInfo {
 __device__ __forceinline__ TaskInfo decode_task(const AttnParams& p, const int* s_off, int NG, int chunk,
                                                 int t) {
   TaskInfo ti;
-  int lo = 0, hi = NG - 1;  // last g with s_off[g] <= t
+  const bool class_a = t < s_off[NG];
+  const int* off = class_a ? s_off : s_off + NG + 1;
+  int lo = 0, hi = NG - 1;  // last g with off[g] <= t
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if (s_off[mid] <= t) lo = mid; else hi = mid - 1;
+    if (off[mid] <= t) lo = mid; else hi = mid - 1;
   }
   ti.g = lo;
-  ti.j = t - s_off[lo];
   ti.n = lo / p.s.Hkv;
   ti.hkv = lo - ti.n * p.s.Hkv;
   const GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, lo, p.F, chunk, p.cap);
+  // piece index j of the group (sink pieces, band pieces, tail pieces), which
+  // is also the partial's slot: class A takes the full band pieces, class B
+  // the sink pieces, the band remainder and the tail pieces, in that order
+  const int k = t - off[lo];
+  const int na = full_band_pieces(sp);
+  if (class_a)
+    ti.j = sp.n_sink + k;
+  else if (k < sp.n_sink)
+    ti.j = k;
+  else
+    ti.j = k + na;
   ti.band = false;
   if (ti.j < sp.n_sink) {
     ti.a = ti.j * sp.chunk;
@@ -707,7 +745,7 @@ template <int G>
 __global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
   constexpr int U = 2;                 // tokens per row per iteration
   constexpr int kStep = kWaves * 4 * U;  // tokens per workgroup iteration
-  extern __shared__ int s_off[];  // NG + 1 task offsets (dynamic)
+  extern __shared__ int s_off[];  // 2 (NG + 1) task offsets (dynamic)
   __shared__ int s_tmp[kWaves];
   __shared__ float s_o[kWaves][G][kHeadDim];
   __shared__ float s_ml[kWaves][G][2];
@@ -920,7 +958,7 @@ __device__ __forceinline__ uint4 load_stream16(const uint16_t* ptr) {
 template <int G>
 __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnParams p) {
   constexpr int kBlk = 32;  // tokens per wave block
-  extern __shared__ int s_off[];  // NG + 1 task offsets (dynamic)
+  extern __shared__ int s_off[];  // 2 (NG + 1) task offsets (dynamic)
   __shared__ int s_tmp[kWaves];
   __shared__ uint4 s_k[kWaves][kBlk * 16];
   __shared__ uint4 s_v[kWaves][kBlk * 16];
@@ -1307,6 +1345,16 @@ int fail(int code, const char* fmt, ...) {
 
 // MAC_AMD_ATTN_IMPL=valu selects the VALU span-attention kernel; the default
 // is the MFMA kernel.  Read once per process.
+// Target tasks per workgroup (MAC_AMD_TASKS_PER_WG, read once; 4..64).
+int tasks_per_wg() {
+  static const int v = [] {
+    const char* e = std::getenv("MAC_AMD_TASKS_PER_WG");
+    const int x = e != nullptr ? std::atoi(e) : kTasksPerWorkgroup;
+    return x < 4 ? 4 : (x > 64 ? 64 : x);
+  }();
+  return v;
+}
+
 int attn_impl() {
   static const int impl = [] {
     const char* e = std::getenv("MAC_AMD_ATTN_IMPL");
@@ -1366,7 +1414,7 @@ int launch_all(const DecideParams& dp, const AttnParams& ap, const MergeParams& 
   hipLaunchKernelGGL(match_decide_kernel<G>, dim3(NG), dim3(kBlock), 0, stream, dp);
   MAC_HIP(hipGetLastError());
   if (ev) MAC_HIP(hipEventRecord(ev[1], stream));
-  const size_t plan_lds = sizeof(int) * (static_cast<size_t>(NG) + 1);
+  const size_t plan_lds = 2 * sizeof(int) * (static_cast<size_t>(NG) + 1);
   if (impl)
     hipLaunchKernelGGL(span_attention_mfma_kernel<G>, dim3(attn_grid), dim3(kBlock), plan_lds, stream, ap);
   else
@@ -1456,7 +1504,7 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   MAC_HIP(hipGetDevice(&dev));
   int cus = 0, per_cu = 0;
   const int impl = attn_impl();
-  const size_t plan_lds = sizeof(int) * (static_cast<size_t>(N) * Hkv + 1);
+  const size_t plan_lds = 2 * sizeof(int) * (static_cast<size_t>(N) * Hkv + 1);
   int rc = attn_residency(dev, G, impl, plan_lds, &cus, &per_cu);
   if (rc != MAC_OK) return rc;
 
@@ -1552,6 +1600,7 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   ap.F = dp.F;
   ap.q_scale = static_cast<float>(a->sm_scale) * kLog2e;
   ap.tile_tokens = a->tile_tokens;
+  ap.tasks_per_wg = tasks_per_wg();
 
   MergeParams mp{};
   mp.s = s;
