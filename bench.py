@@ -62,6 +62,8 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--phase-runs", type=int, default=5)
     ap.add_argument("--json-out", default=None)
+    ap.add_argument("--no-aux", action="store_true",
+                    help="skip the prefill-rectification and decode-RoPE measurements")
     return ap.parse_args()
 
 
@@ -232,6 +234,106 @@ def cpu_baseline(args, hit):
 PMC_SUMMARY = os.path.join(REPO, "profiles", "span_attention_config3_gqa4_hit0.8_pmc.txt")
 
 
+def _time_us(torch, fn, reps):
+    """Average µs of fn() over reps launches, HIP events on the current stream."""
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / reps
+
+
+def measure_aux(torch):
+    """The rows beside the decode step, at BASELINE config 4's prefill shape:
+    64 requests, one 8192-token chunk each, GQA-8, S = 256, ring 32.
+      prefill_rectify -- the fused op (kept rows only) against the reference's
+                         three calls on the GPU (window attention of every row,
+                         downdate of every row, mac_prefill_update_cache);
+      decode_rope     -- fused RoPE + q preserve + KV write for a 64-token decode
+                         batch (GQA-4, rotary_dim 128, NeoX)."""
+    from mac_attention.integrations.sglang import bridge
+
+    rect = bridge.load_mac_prefill_rectify_extension()
+    merge = bridge.load_mac_merge_downdate_cache_extension()
+    cache = bridge.load_mac_prefill_update_cache_extension()
+    rope = bridge.load_mac_decode_rope_preserve_extension()
+    B, chunk, hq, hkv, S, M = 64, 8192, 32, 4, 256, 32
+    rows = B * chunk
+    bf = torch.bfloat16
+    dev = "cuda"
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    k = torch.randn(rows, hkv, D, device=dev, dtype=bf, generator=g)
+    v = torch.randn(rows, hkv, D, device=dev, dtype=bf, generator=g)
+    q = torch.randn(rows, hq, D, device=dev, dtype=bf, generator=g)
+    src_q = torch.randn(rows, hq, D, device=dev, dtype=bf, generator=g)
+    o_full = torch.randn(rows, hq, D, device=dev, dtype=bf, generator=g)
+    lse_full = torch.randn(rows, hq, device=dev, generator=g) + 8.0
+    qo = torch.arange(0, rows + 1, chunk, device=dev, dtype=torch.int32)
+    idx = torch.randperm(rows, device=dev, generator=g).to(torch.int32)
+    qc = torch.zeros(B, M, hq, D, device=dev, dtype=bf)
+    ac = torch.zeros_like(qc)
+    lc = torch.zeros(B, M, hq, device=dev)
+    req = torch.arange(B, device=dev, dtype=torch.int32)
+    rl = torch.zeros(B + 1, device=dev, dtype=torch.int32)  # indexed by request (R = B + 1 rows)
+    qc2, ac2, lc2 = (torch.zeros(B + 1, M, hq, D, device=dev, dtype=bf), torch.zeros(B + 1, M, hq, D, device=dev, dtype=bf),
+                     torch.zeros(B + 1, M, hq, device=dev))
+    scale = 1.0 / math.sqrt(D)
+
+    def fused():
+        rect.mac_prefill_rectify_update_cache(q, src_q, o_full, lse_full, k, v, qo, qo, idx, qc2, ac2, lc2,
+                                              rl, req, S, 0, scale)
+
+    wo = torch.empty_like(q)
+    wl = torch.empty(rows, hq, device=dev)
+    lens = torch.full((B,), chunk, device=dev, dtype=torch.int32)
+    empty = torch.empty(0, device=dev, dtype=bf)
+
+    def composed():
+        rect.window_attention_return_lse(q, k, v, qo, qo, idx, S - 1, scale, out=wo, out_lse=wl)
+        merge.mac_update_then_downdate_bf16_inplace(o_full, lse_full, wo, wl)
+        cache.mac_prefill_update_cache(qc, ac, lc, rl[:B], req, src_q, wo, wl, qo, lens, M, hq, D, empty)
+
+    fused_us = _time_us(torch, fused, 20)
+    comp_us = _time_us(torch, composed, 5)
+    # algorithmic bytes of the fused op: per (request, kv head) the K/V rows
+    # of the window of the kept rows (M + S - 1 tokens), per kept row and
+    # head q_post, src_q, o_full (256 B each) + lse_full read, ring q and o
+    # (256 B each) + lse written
+    kept = B * M
+    fused_bytes = B * hkv * (M + S - 1) * 2 * D * 2 + kept * hq * (5 * 2 * D + 8)
+    out = {"prefill_rectify": {
+        "workload": f"B={B} requests x {chunk}-token chunk, GQA-8 (Hq={hq}, Hkv={hkv}), S={S}, ring={M}",
+        "fused_us": round(fused_us, 2), "reference_three_calls_us": round(comp_us, 2),
+        "speedup": round(comp_us / fused_us, 1), "fused_algorithmic_bytes": fused_bytes,
+        "fused_gbs": round(fused_bytes / fused_us / 1e3, 1)}}
+    del k, v, q, src_q, o_full, wo
+    torch.cuda.empty_cache()
+
+    n, hq4, hkv4, pool = 64, 32, 8, 1 << 16
+    qkv = torch.randn(n, (hq4 + 2 * hkv4) * D, device=dev, dtype=bf, generator=g)
+    qv, kv_, vv = qkv[:, :hq4 * D], qkv[:, hq4 * D:(hq4 + hkv4) * D], qkv[:, (hq4 + hkv4) * D:]
+    q_pre = torch.empty(n, hq4, D, device=dev, dtype=bf)
+    kb = torch.empty(pool, hkv4, D, device=dev, dtype=bf)
+    vb = torch.empty_like(kb)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, D, 2, device=dev, dtype=torch.float32) / D))
+    ang = torch.arange(131072, device=dev, dtype=torch.float32)[:, None] * inv[None, :]
+    cs = torch.cat([ang.cos(), ang.sin()], dim=1).contiguous()
+    pos = torch.randint(0, 131072, (n,), device=dev, generator=g)
+    loc = torch.randperm(pool, device=dev, generator=g)[:n].contiguous()
+    rope_us = _time_us(torch, lambda: rope.mac_decode_rope_preserve_q_bf16(qv, kv_, vv, q_pre, kb, vb, cs, pos, loc,
+                                                                             D, True), 50)
+    rope_bytes = n * ((hq4 + 2 * hkv4) * D * 2 + (2 * hq4 + 3 * hkv4) * D * 2)
+    out["decode_rope"] = {"workload": f"{n} decode tokens, Hq={hq4}, Hkv={hkv4}, rotary_dim {D}, NeoX",
+                          "us": round(rope_us, 2), "algorithmic_bytes": rope_bytes}
+    return out
+
+
 def pmc_traffic(args):
     """HBM bytes per span_attention launch from the committed rocprofv3
     FETCH_SIZE/WRITE_SIZE summary (scaled by the copy-kernel calibration it
@@ -292,6 +394,12 @@ def main():
         del dev
         torch.cuda.empty_cache()
 
+    aux = None
+    if not args.no_aux:
+        aux = measure_aux(torch)
+        log(f"[bench] aux {aux}")
+        torch.cuda.empty_cache()
+
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU oracle sample")
@@ -333,6 +441,7 @@ def main():
         "cpu_baseline": cpu,
         "headline": headline,
         "sweep": sweep,
+        "aux": aux,
     }
     text = json.dumps(line)
     if args.json_out:
