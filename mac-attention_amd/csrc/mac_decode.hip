@@ -192,11 +192,13 @@ __device__ __forceinline__ float clampf(float v, float lo, float hi) { return fm
 // Lanes of a wave form four rows of 16; row r of pass p scans query head
 // r + 4p of the group, lane c of the row owns dims [8c, 8c+8).  Each wave
 // takes slots wave, wave+4, ... in batches of kSlotBatch whose 16-byte loads
-// are all issued before any reduction (the scan is latency-bound).
+// (of every pass) are all issued before any reduction: with one workgroup per
+// group the scan of a large ring is bound by the loads each lane keeps in
+// flight.
 template <int G>
 __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
   constexpr int kPasses = (G + 3) / 4;
-  constexpr int kSlotBatch = 8;
+  constexpr int kSlotBatch = 16 / kPasses;  // 16 row loads in flight per lane
   const int g = blockIdx.x;
   const int n = g / p.s.Hkv;
   const int hkv = g - n * p.s.Hkv;
@@ -241,28 +243,36 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
   if (eligible) {
     const int64_t cache_req = static_cast<int64_t>(req) * M;
     for (int s0 = wave; s0 < M; s0 += kWaves * kSlotBatch) {
+      // every pass's loads of the batch are in flight before any reduction
+      uint4 w[kPasses][kSlotBatch];
+      int pos[kSlotBatch];
+      bool in_window[kSlotBatch];
+#pragma unroll
+      for (int u = 0; u < kSlotBatch; ++u) {
+        const int slot = s0 + u * kWaves;
+        pos[u] = ring_slot_to_pos(P, M, slot);
+        in_window[u] = slot < M && pos[u] >= cand_begin && pos[u] < cand_end;
+      }
 #pragma unroll
       for (int ps = 0; ps < kPasses; ++ps) {
         const int hl = row + 4 * ps;
-        uint4 w[kSlotBatch];
-        int pos[kSlotBatch];
-        bool ok[kSlotBatch];
 #pragma unroll
         for (int u = 0; u < kSlotBatch; ++u) {
-          const int slot = s0 + u * kWaves;
-          pos[u] = ring_slot_to_pos(P, M, slot);
-          ok[u] = slot < M && pos[u] >= cand_begin && pos[u] < cand_end && hl < G;
-          w[u] = make_uint4(0, 0, 0, 0);
-          if (ok[u]) {
+          w[ps][u] = make_uint4(0, 0, 0, 0);
+          if (in_window[u] && hl < G) {
             const int64_t off =
-                ((cache_req + slot) * Hq + hkv * G + hl) * kHeadDim + c * 8;
-            w[u] = *reinterpret_cast<const uint4*>(p.query_cache + off);
+                ((cache_req + s0 + u * kWaves) * Hq + hkv * G + hl) * kHeadDim + c * 8;
+            w[ps][u] = *reinterpret_cast<const uint4*>(p.query_cache + off);
           }
         }
+      }
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps) {
+        const int hl = row + 4 * ps;
 #pragma unroll
         for (int u = 0; u < kSlotBatch; ++u) {
           float cf[8];
-          unpack8(w[u], cf);
+          unpack8(w[ps][u], cf);
           float acc = 0.0f;
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
@@ -270,7 +280,7 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
             acc = fmaf(df, df, acc);
           }
           acc = row16_sum(acc);
-          if (ok[u] && better_pair(acc, pos[u], best_d[ps], best_p[ps])) {
+          if (in_window[u] && hl < G && better_pair(acc, pos[u], best_d[ps], best_p[ps])) {
             best_d[ps] = acc;
             best_p[ps] = pos[u];
             best_s[ps] = s0 + u * kWaves;
