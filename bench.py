@@ -44,7 +44,7 @@ def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--ctx", type=int, default=130048)
     ap.add_argument("--hq", type=int, default=32)
@@ -387,7 +387,7 @@ def main():
                 for h in ([0.0] if exact else hits):
                     step = Step(torch, ext, dev, args=args, hkv=hkv, ring=args.ring, hit=h,
                                 exact=exact)
-                    r = measure(torch, step, 5, args.sweep_replays, 3)
+                    r = measure(torch, step, 15, args.sweep_replays, 3)
                     sweep.append(r)
                     log(f"[bench] sweep {r}")
                     del step
