@@ -314,3 +314,42 @@ def test_graph_replay_matches_eager(ext):
         assert torch.equal(holder["lse"], lse_e), f"replay {it}: lse differs from eager"
         for k in ("query_cache", "attn_cache", "lse_cache"):
             assert torch.equal(live[k], eager[k]), f"replay {it}: {k} differs from eager"
+
+
+# ------------------------------------------- the reference's bench config ----
+
+
+@pytest.mark.parametrize("hkv,candidate_mode", [(8, 0), (4, 1)])
+def test_reference_bench_config_ring_2048(ext, hkv, candidate_mode):
+    """The reference benchmark's own shape (ring capacity 2048, context
+    126976, bench_mac_vs_flashinfer_direct.py:809): 16 requests with fully
+    populated rings (finite lse everywhere), half of the heads with a noisy
+    copy somewhere in the ring, exclude_recent_right candidates in one case;
+    two requests checked against the oracle."""
+    rng = np.random.default_rng(2048 + hkv)
+    b, m, ctx, S = 16, 2048, 126976, 256
+    dev = syn.device_ragged_case(torch, kv_lens=[ctx + 1] * b, hq=32, hkv=hkv, capacity=m, seed=5)
+    entries = {}
+    for n in range(b):
+        for h in _hit_heads(rng, 32, 0.5):
+            entries[(n, h)] = (ctx - int(rng.integers(40, m)), 0.3)
+    syn.plant_noisy_matches(torch, dev, entries=entries, seed=6)
+    check = [3, 12]
+    lookback = 64 if candidate_mode == 1 else 0
+    sub = host_subset(torch, dev, check, semantic_pos_ahead=S)
+    sub.candidate_mode, sub.lookback_right = candidate_mode, lookback
+    res = oracle_run(sub)
+    n_, hq_, _ = dev["q_post"].shape
+    ws = syn.workspace(torch, batch=b, hq=32, hkv=hkv, capacity=m, max_context=131072, tile_tokens=32,
+                       match_tile_slots=32, semantic_pos_ahead=S, device="cuda")
+    out = torch.empty_like(dev["q_post"])
+    out_lse = torch.empty(b, 32, device="cuda")
+    ext.mac_persistent_decode_bf16(
+        dev["q_post"], dev["q_pre"], dev["k"], dev["v"], dev["req_to_token"], dev["req_ids"],
+        dev["past_lens"], dev["out_cache_loc"], dev["query_cache"], dev["attn_cache"], dev["lse_cache"],
+        out, out_lse, *ws, 131072, 32, 32, S, 0, 0, lookback, candidate_mode, 0.45, 1.0 / math.sqrt(128.0),
+        0, 0, 1.0, 0.0, -1.0, 0.0, 64.0, 0.0, 1, -1, 0, dev["query_cache"], dev["cache_ready"],
+        dev["cache_epoch"], dev["request_epoch"])
+    torch.cuda.synchronize()
+    _check_subset(dev, out, out_lse, ws, sub, res, check, f"ring2048 hkv {hkv} mode {candidate_mode}")
+    assert res.head["hit"].sum() > 0
