@@ -56,7 +56,7 @@ constexpr float kLn2 = 0.6931471805599453f;
 // exp2(kNegBig - kNegBig) == 1, so empty states merge without NaNs.
 constexpr float kNegBig = -1.0e30f;
 
-__device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
+__host__ __device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 // DECODE:713-716
 __device__ __forceinline__ int cache_end_for_pos(int p, int s) {

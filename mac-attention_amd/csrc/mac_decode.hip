@@ -90,6 +90,7 @@ struct DecideParams {
   int32_t* group_tail_end;
   int32_t* group_mode;
   int32_t* task_counter;  // zeroed here for span_attention's dynamic fetch
+  int splits;             // slot ranges of the ring scan (1: scan inside match_decide)
   int S, F, gen_min_limit, lookback_right, candidate_mode;
   float thr_dist;
   int mixed_group_fallback;
@@ -187,6 +188,13 @@ __device__ __forceinline__ float pseudo_normal_u32(uint32_t x) {
 }
 __device__ __forceinline__ float clampf(float v, float lo, float hi) { return fminf(fmaxf(v, lo), hi); }
 
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte non-temporal (streaming) global load.
+__device__ __forceinline__ uint4 load_stream16(const uint16_t* ptr) {
+  return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(ptr)));
+}
+
 // =========================================================== 1. decide ====
 
 // Lanes of a wave form four rows of 16; row r of pass p scans query head
@@ -195,7 +203,15 @@ __device__ __forceinline__ float clampf(float v, float lo, float hi) { return fm
 // (of every pass) are all issued before any reduction: with one workgroup per
 // group the scan of a large ring is bound by the loads each lane keeps in
 // flight.
-template <int G>
+//
+// Large rings are scanned by a separate launch over (group, slot range)
+// (kMode 1, `splits` ranges of about kSplitSlots slots) that writes each
+// range's best into tile `range` of match_dist/pos/slot; match_decide then
+// reduces the tiles (kMode 2) instead of scanning.  kMode 0 scans and decides
+// in one workgroup per group.
+constexpr int kSplitSlots = 256;
+
+template <int G, int kMode>
 __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
   constexpr int kPasses = (G + 3) / 4;
   constexpr int kSlotBatch = 16 / kPasses;  // 16 row loads in flight per lane
@@ -240,9 +256,12 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
     unpack8(w, q[ps]);
   }
 
-  if (eligible) {
+  const int per_split = ceil_div(M, p.splits);
+  const int s_lo = kMode == 1 ? static_cast<int>(blockIdx.y) * per_split : 0;
+  const int s_hi = kMode == 1 ? min(M, s_lo + per_split) : M;
+  if (kMode != 2 && eligible) {
     const int64_t cache_req = static_cast<int64_t>(req) * M;
-    for (int s0 = wave; s0 < M; s0 += kWaves * kSlotBatch) {
+    for (int s0 = s_lo + wave; s0 < s_hi; s0 += kWaves * kSlotBatch) {
       // every pass's loads of the batch are in flight before any reduction
       uint4 w[kPasses][kSlotBatch];
       int pos[kSlotBatch];
@@ -251,7 +270,7 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
       for (int u = 0; u < kSlotBatch; ++u) {
         const int slot = s0 + u * kWaves;
         pos[u] = ring_slot_to_pos(P, M, slot);
-        in_window[u] = slot < M && pos[u] >= cand_begin && pos[u] < cand_end;
+        in_window[u] = slot < s_hi && pos[u] >= cand_begin && pos[u] < cand_end;
       }
 #pragma unroll
       for (int ps = 0; ps < kPasses; ++ps) {
@@ -262,7 +281,7 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
           if (in_window[u] && hl < G) {
             const int64_t off =
                 ((cache_req + s0 + u * kWaves) * Hq + hkv * G + hl) * kHeadDim + c * 8;
-            w[ps][u] = *reinterpret_cast<const uint4*>(p.query_cache + off);
+            w[ps][u] = load_stream16(p.query_cache + off);  // ring rows are read once per step
           }
         }
       }
@@ -317,8 +336,28 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
     }
   }
   const int64_t ho = static_cast<int64_t>(n) * Hq + hq;
-  if (head_lane) {
-    const int64_t mo = ho * p.s.max_match_tiles;
+  const int64_t mo = ho * p.s.max_match_tiles;
+  if (kMode == 1) {  // this range's best -> its tile
+    if (head_lane) {
+      p.match_dist[mo + blockIdx.y] = bd;
+      p.match_pos[mo + blockIdx.y] = bp;
+      p.match_slot[mo + blockIdx.y] = bs;
+    }
+    return;
+  }
+  if (kMode == 2) {  // best over the ranges' tiles
+    if (head_lane && eligible) {
+      for (int r = 0; r < p.splits; ++r) {
+        const float d = p.match_dist[mo + r];
+        const int ps = p.match_pos[mo + r];
+        if (p.match_slot[mo + r] >= 0 && better_pair(d, ps, bd, bp)) {
+          bd = d;
+          bp = ps;
+          bs = p.match_slot[mo + r];
+        }
+      }
+    }
+  } else if (head_lane) {
     p.match_dist[mo] = bd;
     p.match_pos[mo] = bp;
     p.match_slot[mo] = bs;
@@ -956,14 +995,8 @@ __global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& w) { return __builtin_bit_cast(bf16x8_t, w); }
-
-// 16-byte non-temporal (streaming) global load.
-__device__ __forceinline__ uint4 load_stream16(const uint16_t* ptr) {
-  return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(ptr)));
-}
 
 template <int G>
 __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnParams p) {
@@ -1421,7 +1454,13 @@ int launch_all(const DecideParams& dp, const AttnParams& ap, const MergeParams& 
                int impl, hipStream_t stream, hipEvent_t* ev) {
   const int NG = dp.s.N * dp.s.Hkv;
   if (ev) MAC_HIP(hipEventRecord(ev[0], stream));
-  hipLaunchKernelGGL(match_decide_kernel<G>, dim3(NG), dim3(kBlock), 0, stream, dp);
+  if (dp.splits > 1) {
+    hipLaunchKernelGGL((match_decide_kernel<G, 1>), dim3(NG, dp.splits), dim3(kBlock), 0, stream, dp);
+    MAC_HIP(hipGetLastError());
+    hipLaunchKernelGGL((match_decide_kernel<G, 2>), dim3(NG), dim3(kBlock), 0, stream, dp);
+  } else {
+    hipLaunchKernelGGL((match_decide_kernel<G, 0>), dim3(NG), dim3(kBlock), 0, stream, dp);
+  }
   MAC_HIP(hipGetLastError());
   if (ev) MAC_HIP(hipEventRecord(ev[1], stream));
   const size_t plan_lds = 2 * sizeof(int) * (static_cast<size_t>(NG) + 1);
@@ -1557,6 +1596,10 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   dp.group_tail_end = a->group_tail_end;
   dp.group_mode = a->group_mode;
   dp.task_counter = a->complete_task_tile + static_cast<int64_t>(N) * Hkv;
+  // rings of more than two ranges of kSplitSlots slots are scanned by a
+  // separate (group, range) launch, one match tile per range
+  dp.splits = std::max(1, std::min(a->max_match_tiles, ceil_div(M, kSplitSlots)));
+  if (dp.splits < 3) dp.splits = 1;
   dp.S = a->semantic_pos_ahead;
   dp.F = a->front_sink_tokens > 0 ? a->front_sink_tokens : 0;
   dp.gen_min_limit = a->gen_min_limit;
