@@ -222,7 +222,10 @@ MAC_API int mac_update_then_downdate_bf16_inplace(const void* out1, const void* 
  * (HOOKS:2436-2466).  Request b owns query rows [qo_indptr[b], qo_indptr[b+1])
  * and keys kv_indices[kv_indptr[b] .. kv_indptr[b+1]); query row i of the
  * request sits at position kv_len - qo_len + i and attends to the keys at
- * positions [pos - window_left, pos] (window_left < 0: [0, pos]).
+ * positions [pos - window_left, pos] (window_left < 0: [0, pos]).  Requests
+ * whose ranges are not within [0, total_q) / [0, kv_indices_len), or with
+ * kv_len < qo_len, are skipped (their rows are not written); keys whose pool
+ * row is outside [0, pool_tokens) are masked.
  *   q        bf16 [total_q, Hq, 128]
  *   k_buffer, v_buffer bf16 [pool_tokens, Hkv, 128]
  *   out      bf16 [total_q, Hq, 128]
@@ -242,6 +245,7 @@ typedef struct MacWindowAttentionArgs {
   float* out_lse;
   int64_t total_q;
   int64_t pool_tokens;
+  int64_t kv_indices_len; /* entries of kv_indices */
   int32_t B, Hq, Hkv, D;
   int32_t window_left;
   double sm_scale;
@@ -293,6 +297,7 @@ typedef struct MacRectifyArgs {
   const int32_t* req_ids;
   int64_t total_q;
   int64_t pool_tokens;
+  int64_t kv_indices_len; /* entries of kv_indices */
   int32_t request_length_len;
   int32_t B, R, M, Hq, Hkv, D;
   int32_t semantic_pos_ahead;

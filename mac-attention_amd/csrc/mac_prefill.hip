@@ -166,6 +166,7 @@ struct WindowParams {
   const int32_t* request_length;
   const int32_t* req_ids;
   int64_t pool_tokens;
+  int64_t total_q, kv_len_total;  // rows of q, entries of kv_indices
   int B, Hq, Hkv, R, M;
   int window_left;  // plain mode: keys [pos - window_left, pos]; < 0: [0, pos]
   int S, F, sink_mode;
@@ -178,6 +179,18 @@ struct WindowParams {
 template <bool kRectify>
 __device__ __forceinline__ int first_row(int len, int M) {
   return kRectify ? (len > M ? len - M : 0) : 0;
+}
+
+// Rows of request b the kernel computes; 0 for requests whose query or key
+// ranges fall outside the buffers the caller described, or with fewer keys
+// than queries.
+template <bool kRectify>
+__device__ __forceinline__ int request_rows(const WindowParams& p, int b) {
+  const int q0 = p.qo_indptr[b], q1 = p.qo_indptr[b + 1];
+  const int k0 = p.kv_indptr[b], k1 = p.kv_indptr[b + 1];
+  const int len = q1 - q0, kvlen = k1 - k0;
+  const bool ok = q0 >= 0 && q1 <= p.total_q && k0 >= 0 && k1 <= p.kv_len_total && len > 0 && kvlen >= len;
+  return ok ? len - first_row<kRectify>(len, p.M) : 0;
 }
 
 template <bool kRectify>
@@ -198,9 +211,7 @@ __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
   {
     int sum = 0;
     for (int b = tid * per; b < min(B, (tid + 1) * per); ++b) {
-      const int len = p.qo_indptr[b + 1] - p.qo_indptr[b];
-      const int kvlen = p.kv_indptr[b + 1] - p.kv_indptr[b];
-      const int rows = (len > 0 && kvlen >= len) ? len - first_row<kRectify>(len, p.M) : 0;
+      const int rows = request_rows<kRectify>(p, b);
       sum += ceil_div(rows, kRows);
     }
     s_part[tid] = sum;
@@ -214,9 +225,7 @@ __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
     int acc = tid > 0 ? s_part[tid - 1] : 0;
     for (int b = tid * per; b < min(B, (tid + 1) * per); ++b) {
       s_boff[b] = acc;
-      const int len = p.qo_indptr[b + 1] - p.qo_indptr[b];
-      const int kvlen = p.kv_indptr[b + 1] - p.kv_indptr[b];
-      const int rows = (len > 0 && kvlen >= len) ? len - first_row<kRectify>(len, p.M) : 0;
+      const int rows = request_rows<kRectify>(p, b);
       acc += ceil_div(rows, kRows);
     }
     if (tid == 255) s_boff[B] = s_part[255];
@@ -522,7 +531,7 @@ int check_window_common(int B, int Hq, int Hkv, int D, int64_t total_q, int64_t 
   REQUIRE(D == kHeadDim, "head_dim must be 128 (got %d)", D);
   REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0, "Hq must be a positive multiple of Hkv");
   REQUIRE(B >= 0 && B <= kMaxB, "B must be in [0, %d] (got %d)", kMaxB, B);
-  REQUIRE(total_q >= 0 && pool > 0, "bad total_q / pool_tokens");
+  REQUIRE(total_q >= 0 && total_q <= INT_MAX && pool > 0, "bad total_q / pool_tokens");
   REQUIRE(total_q * Hq <= static_cast<int64_t>(INT_MAX) * 64, "total_q too large");
   REQUIRE(q && k && v && qo && kvp && kvi, "null pointer argument");
   return MAC_OK;
@@ -550,6 +559,8 @@ extern "C" int mac_prefill_window_attention_bf16(const MacWindowAttentionArgs* a
   p.out = static_cast<uint16_t*>(a->out);
   p.out_lse = a->out_lse;
   p.pool_tokens = a->pool_tokens;
+  p.total_q = a->total_q;
+  p.kv_len_total = a->kv_indices_len;
   p.B = a->B;
   p.Hq = a->Hq;
   p.Hkv = a->Hkv;
@@ -598,6 +609,8 @@ extern "C" int mac_prefill_rectify_update_cache_bf16(const MacRectifyArgs* a, vo
   p.request_length = a->request_length;
   p.req_ids = a->req_ids;
   p.pool_tokens = a->pool_tokens;
+  p.total_q = a->total_q;
+  p.kv_len_total = a->kv_indices_len;
   p.B = a->B;
   p.Hq = a->Hq;
   p.Hkv = a->Hkv;

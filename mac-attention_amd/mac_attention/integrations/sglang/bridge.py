@@ -93,7 +93,7 @@ class MacWindowAttentionArgs(ctypes.Structure):
         ("struct_size", _u32), ("abi_version", _u32),
         ("q", _p), ("k_buffer", _p), ("v_buffer", _p), ("qo_indptr", _p), ("kv_indptr", _p),
         ("kv_indices", _p), ("out", _p), ("out_lse", _p),
-        ("total_q", _i64), ("pool_tokens", _i64),
+        ("total_q", _i64), ("pool_tokens", _i64), ("kv_indices_len", _i64),
         ("B", _i32), ("Hq", _i32), ("Hkv", _i32), ("D", _i32), ("window_left", _i32),
         ("sm_scale", _f64),
     ]
@@ -108,7 +108,7 @@ class MacRectifyArgs(ctypes.Structure):
         ("v_buffer", _p), ("qo_indptr", _p), ("kv_indptr", _p), ("kv_indices", _p),
         ("q_cache", _p), ("attn_cache", _p), ("lse_cache", _p), ("q_post_cache", _p),
         ("request_length", _p), ("req_ids", _p),
-        ("total_q", _i64), ("pool_tokens", _i64),
+        ("total_q", _i64), ("pool_tokens", _i64), ("kv_indices_len", _i64),
         ("request_length_len", _i32), ("B", _i32), ("R", _i32), ("M", _i32), ("Hq", _i32),
         ("Hkv", _i32), ("D", _i32), ("semantic_pos_ahead", _i32), ("front_sink_tokens", _i32),
         ("sink_mode", _i32), ("sm_scale", _f64),
@@ -665,6 +665,7 @@ class PrefillRectifyExtension:
         a.qo_indptr, a.kv_indptr, a.kv_indices = _ptr(qo_indptr), _ptr(kv_indptr), _ptr(kv_indices)
         a.out, a.out_lse = _ptr(out), _ptr(out_lse)
         a.total_q, a.pool_tokens = total_q, int(k_buffer.shape[0])
+        a.kv_indices_len = int(kv_indices.shape[0])
         a.B, a.Hq, a.Hkv, a.D = int(qo_indptr.shape[0]) - 1, hq, int(k_buffer.shape[1]), _HEAD_DIM
         a.window_left, a.sm_scale = int(window_left), float(sm_scale)
         with torch.cuda.device(q.device):
@@ -715,6 +716,7 @@ class PrefillRectifyExtension:
         a.q_post_cache = _ptr(qpc)
         a.request_length, a.req_ids = _ptr(request_length), _ptr(req_ids)
         a.total_q, a.pool_tokens = total_q, int(k_buffer.shape[0])
+        a.kv_indices_len = int(kv_indices.shape[0])
         a.request_length_len = int(request_length.shape[0])
         a.B, a.R, a.M, a.Hq, a.Hkv, a.D = B, R, M, hq, int(k_buffer.shape[1]), _HEAD_DIM
         a.semantic_pos_ahead, a.front_sink_tokens = int(semantic_pos_ahead), int(front_sink_tokens)

@@ -284,3 +284,23 @@ def test_rectify_config4_chunk(rect_ext):
         _compare_ring(e, g, f"config4 sink_mode={sink_mode}")
         if sink_mode == 1:
             assert np.isfinite(g["l"].cpu().numpy()).all()
+
+
+def test_window_attention_skips_requests_outside_the_buffers(rect_ext):
+    """A request whose query range runs past total_q (or key range past
+    kv_indices) is skipped: its rows stay untouched, the others are exact."""
+    case = syn.prefill_case(qo_lens=[5, 5], kv_lens=[9, 7], hq=4, hkv=2, seed=51)
+    d = _dev_case(case)
+    qo_bad = case.qo_indptr.copy()
+    qo_bad[2] = 5000  # request 1 claims rows far beyond the 10 query rows
+    out = torch.zeros_like(d["q"])
+    lse = torch.full((10, 4), 7.0, device="cuda")
+    rect_ext.window_attention_return_lse(d["q"], d["k"], d["v"], _i32(qo_bad), d["kv"], d["idx"], -1,
+                                         case.sm_scale, out=out, out_lse=lse)
+    torch.cuda.synchronize()
+    eo, el = orc.window_attention(_bf(case.q), _bf(case.k), _bf(case.v), case.qo_indptr, case.kv_indptr,
+                                  case.kv_indices, window_left=-1, sm_scale=case.sm_scale)
+    got = bits(_host_bits(out))
+    assert rel_l2(got[:5], bits(eo[:5])) < 1e-2
+    assert not got[5:].any() and (lse[5:] == 7.0).all()
+    np.testing.assert_allclose(lse[:5].cpu().numpy(), el[:5], atol=2e-4)
