@@ -1337,7 +1337,7 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
   merge_range(st, n_sink, n_sink + n_band);
   combine(st);  // also orders every entry read before the ring write below
 
-  if (ready && wave == 0) {
+  if (ready && P >= 0 && wave == 0) {  // (a negative past_len has no ring slot)
     const int64_t rowi = (static_cast<int64_t>(req) * M + dest) * Hq + hq;
     const bool valid = isfinite(st.lse);
     *reinterpret_cast<uint32_t*>(p.query_cache + rowi * kHeadDim + d0) =
