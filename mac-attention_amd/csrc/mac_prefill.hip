@@ -197,7 +197,9 @@ template <bool kRectify>
 __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
   __shared__ int s_boff[kMaxB + 1];  // row-block offsets per request
   __shared__ int s_part[256];
-  __shared__ uint4 s_v[4][kBlk * 16];
+  __shared__ uint4 s_k[2][kBlk * 16];  // double-buffered K / V tiles of 32 keys, shared by the four waves
+  __shared__ uint4 s_v[2][kBlk * 16];
+  __shared__ int s_ok[2][kBlk];        // key has a pool row
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -231,18 +233,23 @@ __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
     if (tid == 255) s_boff[B] = s_part[255];
     __syncthreads();
   }
-  const int total_tasks = s_boff[B] * p.Hq;
-
   const int Hq = p.Hq, Hkv = p.Hkv;
   const int G = Hq / Hkv;
+  const int nquads = ceil_div(G, 4);  // workgroups per (row block, KV head): 4 query heads each
+  const int total_tasks = s_boff[B] * Hkv * nquads;
   const int64_t kv_stride = static_cast<int64_t>(Hkv) * kHeadDim;
   const unsigned pool_rows = static_cast<unsigned>(min(p.pool_tokens, static_cast<int64_t>(INT_MAX)));
-  const uint16_t* vtile = reinterpret_cast<const uint16_t*>(&s_v[wave][0]);
+  // loader side: thread t stages 16-byte chunk t%16 of keys t/16 and t/16 + 16
+  const int ld_key = tid >> 4, ld_chunk = tid & 15;
 
-  for (int task = blockIdx.x * 4 + wave; task < total_tasks; task += gridDim.x * 4) {
-    const int blk = task / Hq;
-    const int h = task - blk * Hq;
-    const int hkv = h / G;
+  for (int task = blockIdx.x; task < total_tasks; task += gridDim.x) {
+    __syncthreads();  // the previous task's waves are done with the tiles
+    const int blk = task / (Hkv * nquads);
+    const int rem = task - blk * Hkv * nquads;
+    const int hkv = rem / nquads;
+    const int hg = 4 * (rem - hkv * nquads) + wave;  // head within the group
+    const bool head_valid = hg < G;                   // wave-uniform
+    const int h = hkv * G + (head_valid ? hg : 0);
     // request of this row block: largest b with s_boff[b] <= blk
     int lo = 0, hi = B - 1;
     while (lo < hi) {
@@ -259,10 +266,10 @@ __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
     const int pos0 = kvlen - len + r_local;
     const int pos_last = pos0 + nrows - 1;
     const bool row_ok = col < nrows;
-    const int pos = pos0 + col;                       // this lane's row position
+    const int pos = pos0 + col;  // this lane's row position
     const int64_t grow = static_cast<int64_t>(p.qo_indptr[b]) + r_local + (row_ok ? col : 0);
 
-    // window bounds of this lane's row and of the wave's key range
+    // window bounds of this lane's row and of the workgroup's key range
     int w_lo, w_lo0;
     if (kRectify) {
       w_lo = max(pos + 1 - p.S, 0);
@@ -273,7 +280,7 @@ __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
     }
     const bool sink = kRectify && p.sink_mode == 1 && p.F > 0;
     const int s_hi = sink ? min(p.F, max(pos + 1 - p.S, 0)) : 0;             // this row's sink end
-    const int s_hi_last = sink ? min(p.F, max(pos_last + 1 - p.S, 0)) : 0;  // the wave's
+    const int s_hi_last = sink ? min(p.F, max(pos_last + 1 - p.S, 0)) : 0;  // the workgroup's
 
     // Q row (B operand): lane (quad, col) holds Q[row col][8*(4s+quad) .. +8]
     uint4 qreg[4];
@@ -282,7 +289,7 @@ __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         uint4 w = *reinterpret_cast<const uint4*>(qp + 8 * (4 * s + quad));
-        if (!row_ok) w = make_uint4(0, 0, 0, 0);
+        if (!row_ok || !head_valid) w = make_uint4(0, 0, 0, 0);
         qreg[s] = w;
       }
     }
@@ -292,54 +299,61 @@ __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const uint16_t* kbase = p.k + static_cast<int64_t>(hkv) * kHeadDim;
-    const uint16_t* vbase = p.v + static_cast<int64_t>(hkv) * kHeadDim;
+    const uint16_t* kbase = p.k + static_cast<int64_t>(hkv) * kHeadDim + ld_chunk * 8;
+    const uint16_t* vbase = p.v + static_cast<int64_t>(hkv) * kHeadDim + ld_chunk * 8;
     // segment 0: the front sink (fused mode, sink_mode 1); segment 1: the window
     for (int seg = sink ? 0 : 1; seg < 2; ++seg) {
       const int seg_lo = seg == 0 ? 0 : w_lo0;
       const int seg_hi = seg == 0 ? s_hi_last : pos_last + 1;
-      const int r_lo = seg == 0 ? 0 : w_lo;      // this row's bounds in the segment
+      const int r_lo = seg == 0 ? 0 : w_lo;  // this row's bounds in the segment
       const int r_hi = seg == 0 ? s_hi : pos + 1;
-      for (int base = seg_lo; base < seg_hi; base += kBlk) {
-        // physical rows of keys base + 16 t + col (-1: masked)
-        int ph[2];
+      const int nblk = seg_hi > seg_lo ? ceil_div(seg_hi - seg_lo, kBlk) : 0;
+      // rows of the loader's two keys of block i (-1: masked)
+      auto rows_of = [&](int i, int (&r)[2]) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          const int key = base + 16 * t + col;
+          const int key = seg_lo + i * kBlk + ld_key + 16 * t;
           const int raw = p.kv_indices[kv_begin + min(key, kvlen - 1)];
-          ph[t] = (key < seg_hi && static_cast<unsigned>(raw) < pool_rows) ? raw : -1;
+          r[t] = (key < seg_hi && static_cast<unsigned>(raw) < pool_rows) ? raw : -1;
         }
-        // K straight into the A operand: key 16 t + col, dims 8*(4s+quad) .. +8
-        uint4 ka[2][4];
+      };
+      uint4 kq[2], vq[2];  // the loader's K/V chunks of the block in flight
+      auto issue = [&](const int (&r)[2]) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int s = 0; s < 4; ++s)
-            ka[t][s] = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(max(ph[t], 0)) * kv_stride +
-                                                       8 * (4 * s + quad));
-        // V rows: lane reads chunk col of token 8*quad + i
-        uint4 vr[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int src = 8 * (quad & 1) + i;
-          const int p0 = __shfl(ph[0], src), p1 = __shfl(ph[1], src);
-          const int pv = (quad >> 1) ? p1 : p0;
-          uint4 w = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(max(pv, 0)) * kv_stride + col * 8);
-          if (pv < 0) w = make_uint4(0, 0, 0, 0);
-          vr[i] = w;
+        for (int t = 0; t < 2; ++t) {
+          kq[t] = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(max(r[t], 0)) * kv_stride);
+          vq[t] = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(max(r[t], 0)) * kv_stride);
         }
-        uint32_t vmask = 0;
+      };
+      int rc[2], rn[2];
+      if (nblk > 0) {
+        rows_of(0, rc);
+        issue(rc);
+        if (nblk > 1) rows_of(1, rn);
+      }
+      for (int i = 0; i < nblk; ++i) {
+        const int buf = i & 1;
+        // stage block i (V of masked keys zeroed) and its key validity
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-          vmask |= static_cast<uint32_t>(__ballot(ph[t] >= 0) & 0xffffu) << (16 * t);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int tok = 8 * quad + i;
-          s_v[wave][tok * 16 + (col ^ (2 * ((tok >> 2) & 3)))] = vr[i];
+        for (int t = 0; t < 2; ++t) {
+          const int tok = ld_key + 16 * t;
+          uint4 w = vq[t];
+          if (rc[t] < 0) w = make_uint4(0, 0, 0, 0);
+          s_k[buf][tok * 16 + (ld_chunk ^ (tok & 15))] = kq[t];
+          s_v[buf][tok * 16 + (ld_chunk ^ (2 * ((tok >> 2) & 3)))] = w;
+          if (ld_chunk == 0) s_ok[buf][tok] = rc[t] >= 0 ? 1 : 0;
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        __syncthreads();  // block i visible; every wave is done with block i - 2 (same buffer)
+        // block i + 1 in flight while block i is computed
+        if (i + 1 < nblk) {
+          rc[0] = rn[0];
+          rc[1] = rn[1];
+          issue(rc);
+          if (i + 2 < nblk) rows_of(i + 2, rn);
+        }
+        if (!head_valid) continue;
+        const int base = seg_lo + i * kBlk;
+        const uint16_t* vtile = reinterpret_cast<const uint16_t*>(&s_v[buf][0]);
 
         // S^T = K Q^T; lane (quad, col): row col, keys 16 t + 4 quad + r
         float sv[8];
@@ -347,14 +361,16 @@ __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           f32x4_t c4 = {0.0f, 0.0f, 0.0f, 0.0f};
+          const int tok = 16 * t + col;
 #pragma unroll
           for (int s = 0; s < 4; ++s)
-            c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[t][s]), as_bf16x8(qreg[s]), c4, 0, 0, 0);
+            c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(s_k[buf][tok * 16 + ((4 * s + quad) ^ col)]),
+                                                        as_bf16x8(qreg[s]), c4, 0, 0, 0);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int kk = 16 * t + 4 * quad + r;
             const int key = base + kk;
-            const bool ok = row_ok && ((vmask >> kk) & 1) && key >= r_lo && key < r_hi;
+            const bool ok = row_ok && s_ok[buf][kk] != 0 && key >= r_lo && key < r_hi;
             const float x = ok ? c4[r] * p.q_scale : -INFINITY;
             sv[4 * t + r] = x;
             bmax = fmaxf(bmax, x);
@@ -397,10 +413,10 @@ __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
           acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, acc[dt], 0, 0, 0);
           if (kRectify) acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl, acc[dt], 0, 0, 0);
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
       }
+      __syncthreads();  // the segment's last tiles are read before the next segment stages into them
     }
+    if (!head_valid) continue;
 
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
@@ -481,14 +497,19 @@ __global__ void bump_kernel(int32_t* request_length, const int32_t* req_ids, con
   atomicAdd(&request_length[req], len);
 }
 
-int grid_for(int64_t tasks) {
-  int dev = 0, cus = 256;
+// Workgroups for `tasks` wave-sized units of work (4 per workgroup), at most
+// as many as are resident at once (`kernel`'s occupancy on every CU), since
+// the kernels loop over their tasks.
+int grid_for(int64_t tasks, const void* kernel) {
+  int dev = 0, cus = 256, per_cu = 2;
   if (hipGetDevice(&dev) == hipSuccess) {
     int v = 0;
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, 256, 0) == hipSuccess && occ > 0) per_cu = occ;
   }
   const int64_t wgs = (tasks + 3) / 4;
-  return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(wgs, static_cast<int64_t>(cus) * 4)));
+  return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(wgs, static_cast<int64_t>(cus) * per_cu)));
 }
 
 }  // namespace
@@ -568,7 +589,7 @@ extern "C" int mac_prefill_window_attention_bf16(const MacWindowAttentionArgs* a
   p.window_left = a->window_left;
   p.q_scale = static_cast<float>(a->sm_scale * 1.4426950408889634);
   const int64_t blocks = (a->total_q + kRows - 1) / kRows + a->B;
-  hipLaunchKernelGGL(window_kernel<false>, dim3(grid_for(blocks * a->Hq)), dim3(256), 0,
+  hipLaunchKernelGGL(window_kernel<false>, dim3(grid_for(4 * blocks * a->Hkv * ceil_div(a->Hq / a->Hkv, 4), reinterpret_cast<const void*>(&window_kernel<false>))), dim3(256), 0,
                      static_cast<hipStream_t>(stream), p);
   HIP_OK(hipGetLastError());
   return MAC_OK;
@@ -625,7 +646,7 @@ extern "C" int mac_prefill_rectify_update_cache_bf16(const MacRectifyArgs* a, vo
   const int64_t kept = std::min<int64_t>(a->total_q, static_cast<int64_t>(a->B) * a->M);
   const int64_t blocks = (kept + kRows - 1) / kRows + a->B;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(window_kernel<true>, dim3(grid_for(blocks * a->Hq)), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(window_kernel<true>, dim3(grid_for(4 * blocks * a->Hkv * ceil_div(a->Hq / a->Hkv, 4), reinterpret_cast<const void*>(&window_kernel<true>))), dim3(256), 0, s, p);
   HIP_OK(hipGetLastError());
   if (!p.rl_by_batch) {
     hipLaunchKernelGGL(bump_kernel, dim3((a->B + 255) / 256), dim3(256), 0, s, a->request_length, a->req_ids,
