@@ -127,6 +127,7 @@ struct AttnParams {
   int F;
   int tile_tokens;  // the caller's tile size (task_counts[3] only)
   int tasks_per_wg;  // target tasks per workgroup of the plan
+  int min_chunk;     // smallest chunk of the plan (tokens)
   float q_scale;  // sm_scale * log2(e)
 };
 
@@ -551,7 +552,7 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* s_tmp, int& tota
 // while a task of at least kMinChunk tokens amortises its fixed cost (plan
 // lookup, Q staging, pipeline fill, partial write).
 constexpr int kTasksPerWorkgroup = 12;  // default of AttnParams::tasks_per_wg
-constexpr int kMinChunk = 256;
+constexpr int kMinChunk = 2048;
 constexpr int kMaxChunk = 16384;
 
 // Every workgroup of span_attention derives the same task list: the chunk C
@@ -595,7 +596,7 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
   }
   const long long target_tasks = static_cast<long long>(p.tasks_per_wg) * W;
   int chunk = static_cast<int>((tok + target_tasks - 1) / target_tasks);
-  chunk = ceil_div(max(chunk, kMinChunk), 64) * 64;
+  chunk = ceil_div(max(chunk, p.min_chunk), 64) * 64;
   chunk = min(chunk, kMaxChunk);
   int* s_offb = s_off + NG + 1;
   int my_a = 0, my_b = 0;
@@ -1398,6 +1399,16 @@ int tasks_per_wg() {
   return v;
 }
 
+// Smallest plan chunk in tokens (MAC_AMD_MIN_CHUNK, read once; 256..16384).
+int min_chunk() {
+  static const int v = [] {
+    const char* e = std::getenv("MAC_AMD_MIN_CHUNK");
+    const int x = e != nullptr ? std::atoi(e) : kMinChunk;
+    return x < 256 ? 256 : (x > kMaxChunk ? kMaxChunk : x);
+  }();
+  return v;
+}
+
 int attn_impl() {
   static const int impl = [] {
     const char* e = std::getenv("MAC_AMD_ATTN_IMPL");
@@ -1654,6 +1665,7 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   ap.q_scale = static_cast<float>(a->sm_scale) * kLog2e;
   ap.tile_tokens = a->tile_tokens;
   ap.tasks_per_wg = tasks_per_wg();
+  ap.min_chunk = min_chunk();
 
   MergeParams mp{};
   mp.s = s;
