@@ -18,7 +18,9 @@ decode step (lower is better), plus
                    bounded sample of the same workload, scaled to µs per step;
   sweep         -- µs/step and achieved GB/s across hit ratios for GQA-4 and
                    GQA-8, and the same kernel forced to exact attention through
-                   the readiness gate (the hit-0 path).
+                   the readiness gate (the hit-0 path);
+  reference_shape -- the same step at the reference's published benchmark
+                   shape (ring 2048, past_len 126976) beside its H100 times.
 """
 
 from __future__ import annotations
@@ -62,6 +64,9 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--phase-runs", type=int, default=5)
     ap.add_argument("--json-out", default=None)
+    ap.add_argument("--ref-shape-hits", default="0,0.5,0.8,0.9,1.0",
+                    help="hit ratios measured at the reference's published benchmark shape "
+                         "(ring 2048, past_len 126976); empty to skip")
     ap.add_argument("--no-aux", action="store_true",
                     help="skip the prefill-rectification and decode-RoPE measurements")
     return ap.parse_args()
@@ -231,6 +236,16 @@ def cpu_baseline(args, hit):
                 sample_head_hits=int(res.head["hit"].sum()))
 
 
+# The reference's published MAC decode-step times on H100 80GB (CUDA-graph
+# replay, B=64, past_len 126976, ring 2048, S=256, F=0, synthetic_head):
+# results/cuda_graph_hit_curves/gqa4.csv:156-169 and gqa8.csv:156-169.
+REF_H100_MS = {
+    4: {0.0: 19.107, 0.5: 13.806, 0.8: 6.261, 0.9: 3.556, 1.0: 0.969},
+    8: {0.0: 13.228, 0.5: 8.557, 0.8: 3.694, 0.9: 2.374, 1.0: 0.708},
+}
+REF_SHAPE_CTX, REF_SHAPE_RING = 126976, 2048
+
+
 PMC_SUMMARY = os.path.join(REPO, "profiles", "span_attention_config3_gqa4_hit0.8_pmc.txt")
 
 
@@ -394,6 +409,34 @@ def main():
         del dev
         torch.cuda.empty_cache()
 
+    # the reference's own benchmark shape, next to its published H100 times
+    ref_shape = []
+    ref_hits = [float(x) for x in args.ref_shape_hits.split(",") if x.strip()]
+    if ref_hits:
+        rargs = argparse.Namespace(**vars(args))
+        rargs.ctx, rargs.ring = REF_SHAPE_CTX, REF_SHAPE_RING
+        for hkv in (args.hkv, args.hq // 8):
+            gqa = args.hq // hkv
+            # hit decisions come from the synthetic_head override, so one input
+            # set serves every hit ratio (planted copies are cosmetic there)
+            dev = syn.device_case(torch, batch=args.batch, hq=args.hq, hkv=hkv, ctx=REF_SHAPE_CTX,
+                                  capacity=REF_SHAPE_RING, seed=0)
+            syn.plant_synthetic_hits(torch, dev, hit_rate=args.hit, bench_mode=1,
+                                     semantic_pos_ahead=args.semantic_pos_ahead)
+            for h in ref_hits:
+                step = Step(torch, ext, dev, args=rargs, hkv=hkv, ring=REF_SHAPE_RING, hit=h, exact=False)
+                r = measure(torch, step, 15, args.sweep_replays, 3)
+                ref_ms = REF_H100_MS.get(gqa, {}).get(h)
+                r["ctx"] = REF_SHAPE_CTX
+                r["reference_h100_us"] = None if ref_ms is None else round(ref_ms * 1e3, 1)
+                r["speedup_vs_reference_h100"] = (None if ref_ms is None
+                                                  else round(ref_ms * 1e3 / r["us_per_step"], 2))
+                ref_shape.append(r)
+                log(f"[bench] reference shape {r}")
+                del step
+            del dev
+            torch.cuda.empty_cache()
+
     aux = None
     if not args.no_aux:
         aux = measure_aux(torch)
@@ -441,6 +484,7 @@ def main():
         "cpu_baseline": cpu,
         "headline": headline,
         "sweep": sweep,
+        "reference_shape": ref_shape,
         "aux": aux,
     }
     text = json.dumps(line)
