@@ -6,9 +6,11 @@ and the oracle re-runs a subset of requests from a compact copy of the rows
 they read (``helpers.host_subset``); outputs, ring rows and decisions of that
 subset must match (decisions exactly, values within 1e-2 relative L2).
 
-Config interpretations: S = 256 where a config does not name
-it; configs 0-2 keep 16 populated ring entries at the named match positions in
-a ring large enough to reach them (M = 4096 / 4096 / 32768); hits are planted
+Config interpretations: S = 256 where a config does not name it (the
+reference's default semantic_pos_ahead); a match position is the logical
+position of a ring slot, which lies in [P - M, P), so configs 0-2 keep 16
+populated ring entries at the named match positions in a ring large enough to
+reach them (M = 4096 / 4096 / 32768); hits are planted
 as sqrt(1-eps^2) q + eps N(0,1) with eps = 0.3 (hit) or 0.9 (miss).
 """
 
