@@ -9,6 +9,7 @@ values within the reference's tolerances and 1e-2 relative L2.
 import numpy as np
 import pytest
 
+import golden_cases
 import kat_cases
 from helpers import assert_close, bits, oracle_run, rel_l2, syn
 
@@ -51,7 +52,7 @@ def _check_against_oracle(case, dev, out, out_lse, ws, res, tol=1e-2, what=""):
 
 
 @pytest.mark.parametrize("partial", ["f32", "bf16"])
-@pytest.mark.parametrize("builder", kat_cases.ALL, ids=lambda f: f.__name__)
+@pytest.mark.parametrize("builder", kat_cases.ALL + golden_cases.LOADERS, ids=lambda f: f.__name__)
 def test_reference_kat(builder, partial, ext, monkeypatch):
     kat = builder()
     for k, v in kat.env.items():

@@ -5,6 +5,7 @@ import os
 import numpy as np
 import pytest
 
+import golden_cases
 import kat_cases
 from helpers import assert_close, bits, oracle_run, rel_l2
 
@@ -14,7 +15,7 @@ def _apply_env(monkeypatch, env):
         monkeypatch.setenv(k, v)
 
 
-@pytest.mark.parametrize("builder", kat_cases.ALL, ids=lambda f: f.__name__)
+@pytest.mark.parametrize("builder", kat_cases.ALL + golden_cases.LOADERS, ids=lambda f: f.__name__)
 def test_oracle_reproduces_reference_kat(builder, monkeypatch):
     kat = builder()
     _apply_env(monkeypatch, kat.env)
