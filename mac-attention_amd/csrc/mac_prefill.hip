@@ -10,23 +10,21 @@
 //
 //  * downdate_kernel: the reference's downdate op on its own (any head_dim,
 //    f32/bf16/f16 lse), for callers that keep the reference's three calls.
-//  * window_kernel<false>: causal sliding-window attention over a ragged
+//  * window_plain_kernel: causal sliding-window attention over a ragged
 //    batch with a page-size-1 KV pool (the windowed FlashInfer pass).
-//  * window_kernel<true>: the fused form.  Only the rows the ring keeps (the
-//    last min(len, M) of each request) are computed; for them the window
-//    state never leaves registers: it is downdated from the full state and
-//    stored straight into the ring with the pre-RoPE query, followed by the
+//  * rectify_kernel: the fused form.  Only the rows the ring keeps (the last
+//    min(len, M) of each request) are computed; for them the window state
+//    never leaves registers: it is downdated from the full state and stored
+//    straight into the ring with the pre-RoPE query, followed by the
 //    request_length bump (bump_kernel).
 //
-// Window kernel layout: one 64-lane wave owns 16 consecutive query rows of
-// one (request, query head) and walks the rows' key range in 32-key blocks.
-// S^T[key][row] = K Q^T and O^T[d][row] += V^T P^T run on
-// v_mfma_f32_16x16x32_bf16 exactly as in the decode kernel with query rows in
+// Both run S^T[key][row] = K Q^T and O^T[d][row] += V^T P^T on
+// v_mfma_f32_16x16x32_bf16 as the decode kernel does, with 16 query rows in
 // place of the GQA heads: the lane holding row l%16 keeps that row's softmax
-// state and 32 O^T accumulators.  K is read straight into the A operand (the
-// rows are shared by the 16 query rows of the wave and by the other heads of
-// the group, so they come from L2); Q stays in registers; V is staged in a
-// per-wave 8 KiB LDS tile for the transposed A-operand gather.
+// state and 32 O^T accumulators per head.  A workgroup takes 16 rows of one
+// request and several query heads of one KV head; its four waves share
+// double-buffered LDS K/V tiles of 32 keys.  The layouts of each kernel are
+// described above it.
 
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
@@ -174,8 +172,8 @@ struct WindowParams {
   float q_scale;  // sm_scale * log2(e)
 };
 
-// Rows of request b that the kernel computes: all of them, or (fused mode)
-// the last min(len, M) that the ring keeps.
+// First row of request b that a kernel computes: 0 (plain form: every row),
+// or the first of the last min(len, M) rows, which the ring keeps (fused form).
 template <bool kRectify>
 __device__ __forceinline__ int first_row(int len, int M) {
   return kRectify ? (len > M ? len - M : 0) : 0;
@@ -193,8 +191,7 @@ __device__ __forceinline__ int request_rows(const WindowParams& p, int b) {
   return ok ? len - first_row<kRectify>(len, p.M) : 0;
 }
 
-template <bool kRectify>
-__global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
+__global__ void __launch_bounds__(256) rectify_kernel(WindowParams p) {
   __shared__ int s_boff[kMaxB + 1];  // row-block offsets per request
   __shared__ int s_part[256];
   __shared__ uint4 s_k[2][kBlk * 16];  // double-buffered K / V tiles of 32 keys, shared by the four waves
@@ -213,7 +210,7 @@ __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
   {
     int sum = 0;
     for (int b = tid * per; b < min(B, (tid + 1) * per); ++b) {
-      const int rows = request_rows<kRectify>(p, b);
+      const int rows = request_rows<true>(p, b);
       sum += ceil_div(rows, kRows);
     }
     s_part[tid] = sum;
@@ -227,7 +224,7 @@ __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
     int acc = tid > 0 ? s_part[tid - 1] : 0;
     for (int b = tid * per; b < min(B, (tid + 1) * per); ++b) {
       s_boff[b] = acc;
-      const int rows = request_rows<kRectify>(p, b);
+      const int rows = request_rows<true>(p, b);
       acc += ceil_div(rows, kRows);
     }
     if (tid == 255) s_boff[B] = s_part[255];
@@ -261,7 +258,7 @@ __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
     const int len = p.qo_indptr[b + 1] - p.qo_indptr[b];
     const int kvlen = p.kv_indptr[b + 1] - p.kv_indptr[b];
     const int64_t kv_begin = p.kv_indptr[b];
-    const int r_local = first_row<kRectify>(len, p.M) + kRows * (blk - s_boff[b]);
+    const int r_local = first_row<true>(len, p.M) + kRows * (blk - s_boff[b]);
     const int nrows = min(kRows, len - r_local);
     const int pos0 = kvlen - len + r_local;
     const int pos_last = pos0 + nrows - 1;
@@ -270,15 +267,9 @@ __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
     const int64_t grow = static_cast<int64_t>(p.qo_indptr[b]) + r_local + (row_ok ? col : 0);
 
     // window bounds of this lane's row and of the workgroup's key range
-    int w_lo, w_lo0;
-    if (kRectify) {
-      w_lo = max(pos + 1 - p.S, 0);
-      w_lo0 = max(pos0 + 1 - p.S, 0);
-    } else {
-      w_lo = p.window_left < 0 ? 0 : max(pos - p.window_left, 0);
-      w_lo0 = p.window_left < 0 ? 0 : max(pos0 - p.window_left, 0);
-    }
-    const bool sink = kRectify && p.sink_mode == 1 && p.F > 0;
+    const int w_lo = max(pos + 1 - p.S, 0);
+    const int w_lo0 = max(pos0 + 1 - p.S, 0);
+    const bool sink = p.sink_mode == 1 && p.F > 0;
     const int s_hi = sink ? min(p.F, max(pos + 1 - p.S, 0)) : 0;             // this row's sink end
     const int s_hi_last = sink ? min(p.F, max(pos_last + 1 - p.S, 0)) : 0;  // the workgroup's
 
@@ -397,7 +388,7 @@ __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
           const float pe = fast_exp2(sv[e] - m);
           psum += pe;
           pb[e] = static_cast<__bf16>(pe);
-          if (kRectify) pl[e] = static_cast<__bf16>(pe - static_cast<float>(pb[e]));
+          pl[e] = static_cast<__bf16>(pe - static_cast<float>(pb[e]));
         }
         l += psum;
         // O^T += V^T P^T; k index e of the lane <-> key (e < 4 ? 4q+e : 16+4q+e-4)
@@ -411,7 +402,7 @@ __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
             va[e] = __builtin_bit_cast(__bf16, vtile[(tok * 16 + chunk_pos) * 8 + (col & 7)]);
           }
           acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, acc[dt], 0, 0, 0);
-          if (kRectify) acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl, acc[dt], 0, 0, 0);
+          acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl, acc[dt], 0, 0, 0);
         }
       }
       __syncthreads();  // the segment's last tiles are read before the next segment stages into them
@@ -423,19 +414,6 @@ __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     const float lse_w = l > 0.0f ? (m + fast_log2(l)) * kLn2 : -INFINITY;
     if (!row_ok) continue;
-
-    if (!kRectify) {
-      uint16_t* op = p.out + (grow * Hq + h) * kHeadDim + 4 * quad;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        uint2 w;
-        w.x = f32_to_bf16(acc[dt][0] * inv) | (static_cast<uint32_t>(f32_to_bf16(acc[dt][1] * inv)) << 16);
-        w.y = f32_to_bf16(acc[dt][2] * inv) | (static_cast<uint32_t>(f32_to_bf16(acc[dt][3] * inv)) << 16);
-        *reinterpret_cast<uint2*>(op + 16 * dt) = w;
-      }
-      if (quad == 0) p.out_lse[grow * Hq + h] = lse_w;
-      continue;
-    }
 
     // ---- fused: downdate the full state, store the ring row ----
     const int req = p.req_ids[b];
@@ -481,6 +459,310 @@ __global__ void __launch_bounds__(256) window_kernel(WindowParams p) {
       const uint4 nan4 = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
 #pragma unroll
       for (int s = 0; s < 4; ++s) *reinterpret_cast<uint4*>(pq + 8 * (4 * s + quad)) = nan4;
+    }
+  }
+}
+
+// Plain sliding-window attention (the windowed FlashInfer pass) for GQA
+// groups of any size.  A workgroup takes 16 consecutive query rows of one
+// request and 4 * HPW query heads of one KV head (HPW heads per wave), so
+// every 32-key K/V tile it stages in LDS serves 16 rows x 4 HPW heads.  Per
+// wave and block:
+//  * S^T = K Q^T: the A operand (K rows) is read once and used for the
+//    wave's HPW heads.  Tile t's MFMA row m = 4a + i holds key 8a + 4t + i,
+//    so the lane holding row (query) col ends up with the scores of keys
+//    8q .. 8q + 7 (q = lane / 16) -- consecutive keys, which is what the PV
+//    product's B operand needs.
+//  * O^T += V^T P^T: V stays token-major in LDS; the A operand of each
+//    16-dim tile, V^T[16 dt + col][8q .. 8q + 7], is two transposing LDS
+//    reads (ds_read_b64_tr_b16: in each 16-lane group, lane i receives
+//    element i & 3 of the 4-element vectors of lanes 4e + (i >> 2), e < 4),
+//    again shared by the wave's heads.
+// LDS layouts: K chunk c (16 bytes) of key k at position c ^ (4 ((k >> 3) &
+// 3) + (k & 3)) of its 256-byte row, which puts the 16 keys one A-operand
+// read touches on 16 different 16-byte bank groups; V rows padded to 288
+// bytes, which does the same for the 4 keys x 32 bytes of a transposing read
+// and keeps its address an immediate offset per 16-dim tile.
+// Key validity of a block is one 32-bit mask in LDS; a lane turns it into
+// the mask of its 8 keys with the row's window bounds by shifts.  The running
+// maximum is moved lazily (only when a block exceeds it by 2^8), which leaves
+// the result exact and skips most accumulator rescales.
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x4_t lds_read_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_t*)(p));
+}
+
+constexpr int kVRow = 18;  // 16-byte units per staged V row: 256 bytes + 32 of padding
+
+template <int HPW>
+__global__ void __launch_bounds__(256, 2) window_plain_kernel(WindowParams p) {
+  __shared__ int s_boff[kMaxB + 1];
+  __shared__ int s_part[256];
+  __shared__ uint4 s_k[2][kBlk * 16];  // K rows of a 32-key block (swizzled)
+  __shared__ uint4 s_v[2][kBlk * kVRow];  // V rows of the block (padded rows)
+  __shared__ uint32_t s_okw[2][kWaves];  // per wave: bits of its 8 keys that have a pool row
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int quad = lane >> 4;
+  const int col = lane & 15;
+
+  // ---- plan: s_boff[b] = sum over b' < b of ceil(rows(b') / 16) ----
+  const int B = p.B;
+  const int per = ceil_div(B, 256);
+  {
+    int sum = 0;
+    for (int b = tid * per; b < min(B, (tid + 1) * per); ++b) sum += ceil_div(request_rows<false>(p, b), kRows);
+    s_part[tid] = sum;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {  // inclusive Hillis-Steele scan
+      const int x = tid >= off ? s_part[tid - off] : 0;
+      __syncthreads();
+      s_part[tid] += x;
+      __syncthreads();
+    }
+    int acc = tid > 0 ? s_part[tid - 1] : 0;
+    for (int b = tid * per; b < min(B, (tid + 1) * per); ++b) {
+      s_boff[b] = acc;
+      acc += ceil_div(request_rows<false>(p, b), kRows);
+    }
+    if (tid == 255) s_boff[B] = s_part[255];
+    __syncthreads();
+  }
+  const int Hq = p.Hq, Hkv = p.Hkv;
+  const int G = Hq / Hkv;
+  constexpr int kHeadsPerTask = 4 * HPW;
+  const int nchunks = ceil_div(G, kHeadsPerTask);
+  const int total_tasks = s_boff[B] * Hkv * nchunks;
+  const int64_t kv_stride = static_cast<int64_t>(Hkv) * kHeadDim;
+  const unsigned pool_rows = static_cast<unsigned>(min(p.pool_tokens, static_cast<int64_t>(INT_MAX)));
+  // loader side: thread t stages 16-byte chunk t%16 of keys 2 (t/16) and 2 (t/16) + 1
+  const int ld_key = 2 * (tid >> 4), ld_chunk = tid & 15;
+  const int ld_pk0 = ld_key * 16 + (ld_chunk ^ (4 * ((ld_key >> 3) & 3) + (ld_key & 3)));
+  const int ld_pk1 = (ld_key + 1) * 16 + (ld_chunk ^ (4 * (((ld_key + 1) >> 3) & 3) + ((ld_key + 1) & 3)));
+  const int ld_pv0 = ld_key * kVRow + ld_chunk;
+  const int ld_pv1 = (ld_key + 1) * kVRow + ld_chunk;
+  // compute side: K A-operand positions (tile t, k-step s) and V^T read
+  // addresses (16-dim tile dt, half h) of this lane
+  int pk[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int key = 8 * (col >> 2) + 4 * t + (col & 3);
+    const int sw = 4 * ((key >> 3) & 3) + (key & 3);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) pk[t][s] = key * 16 + ((4 * s + quad) ^ sw);
+  }
+  // V^T: lane j = col of group quad reads key 8 quad + 4 h + (j >> 2), dims
+  // 16 dt + 4 (j & 3) .. + 3: element offset pv[h] + 16 dt of the V tile
+  int pv[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) pv[h] = (8 * quad + 4 * h + (col >> 2)) * (kVRow * 8) + 4 * (col & 3);
+
+  for (int task = blockIdx.x; task < total_tasks; task += gridDim.x) {
+    __syncthreads();  // the previous task's waves are done with the tiles
+    const int blk = task / (Hkv * nchunks);
+    const int rem = task - blk * Hkv * nchunks;
+    const int hkv = rem / nchunks;
+    const int hg0 = kHeadsPerTask * (rem - hkv * nchunks) + HPW * wave;  // first head of this wave in the group
+    int lo = 0, hi = B - 1;  // request of this row block: largest b with s_boff[b] <= blk
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_boff[mid] <= blk) lo = mid;
+      else hi = mid - 1;
+    }
+    const int b = lo;
+    const int len = p.qo_indptr[b + 1] - p.qo_indptr[b];
+    const int kvlen = p.kv_indptr[b + 1] - p.kv_indptr[b];
+    const int64_t kv_begin = p.kv_indptr[b];
+    const int r_local = kRows * (blk - s_boff[b]);
+    const int nrows = min(kRows, len - r_local);
+    const int pos0 = kvlen - len + r_local;
+    const int pos_last = pos0 + nrows - 1;
+    const bool row_ok = col < nrows;
+    const int pos = pos0 + col;  // this lane's row position
+    const int64_t grow = static_cast<int64_t>(p.qo_indptr[b]) + r_local + (row_ok ? col : 0);
+    const int w_lo = p.window_left < 0 ? 0 : max(pos - p.window_left, 0);  // this row's keys [w_lo, pos]
+    const int seg_lo = p.window_left < 0 ? 0 : max(pos0 - p.window_left, 0);
+    const int seg_hi = pos_last + 1;
+
+    // Q rows of the wave's heads (B operands): lane (quad, col) holds
+    // Q[row col][8 (4s + quad) .. +8]; rows of absent heads are zero
+    uint4 qreg[HPW][4];
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) {
+      const bool hv = hg0 + i < G;
+      const int h = hkv * G + (hv ? hg0 + i : 0);
+      const uint16_t* qp = p.q + (grow * Hq + h) * kHeadDim;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        uint4 w = *reinterpret_cast<const uint4*>(qp + 8 * (4 * s + quad));
+        if (!row_ok || !hv) w = make_uint4(0, 0, 0, 0);
+        qreg[i][s] = w;
+      }
+    }
+    const int nheads = __builtin_amdgcn_readfirstlane(max(0, min(HPW, G - hg0)));  // heads this wave computes
+
+    float m[HPW], l[HPW];
+    f32x4_t acc[HPW][8];
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) {
+      m[i] = kNegBig;
+      l[i] = 0.0f;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) acc[i][dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+
+    const uint16_t* kbase = p.k + static_cast<int64_t>(hkv) * kHeadDim + ld_chunk * 8;
+    const uint16_t* vbase = p.v + static_cast<int64_t>(hkv) * kHeadDim + ld_chunk * 8;
+    const int nblk = seg_hi > seg_lo ? ceil_div(seg_hi - seg_lo, kBlk) : 0;
+    // pool row of the loader's key ld_key + t of block i (-1: masked)
+    auto row_of = [&](int i, int t) -> int {
+      const int key = seg_lo + i * kBlk + ld_key + t;
+      const int raw = p.kv_indices[kv_begin + min(key, kvlen - 1)];
+      return (key < seg_hi && static_cast<unsigned>(raw) < pool_rows) ? raw : -1;
+    };
+    auto ld = [&](const uint16_t* base, int r) -> uint4 {
+      return *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(max(r, 0)) * kv_stride);
+    };
+    // the loader's K/V chunks of the block in flight (rc0/rc1: their rows)
+    int rc0 = -1, rc1 = -1, rn0 = -1, rn1 = -1;
+    uint4 kq0 = make_uint4(0, 0, 0, 0), kq1 = kq0, vq0 = kq0, vq1 = kq0;
+    if (nblk > 0) {
+      rc0 = row_of(0, 0);
+      rc1 = row_of(0, 1);
+      kq0 = ld(kbase, rc0);
+      kq1 = ld(kbase, rc1);
+      vq0 = ld(vbase, rc0);
+      vq1 = ld(vbase, rc1);
+      if (nblk > 1) {
+        rn0 = row_of(1, 0);
+        rn1 = row_of(1, 1);
+      }
+    }
+    for (int i = 0; i < nblk; ++i) {
+      const int buf = i & 1;
+      // stage block i: K and V rows (V of masked keys zeroed), key validity bits
+      {
+        s_k[buf][ld_pk0] = kq0;
+        s_k[buf][ld_pk1] = kq1;
+        s_v[buf][ld_pv0] = rc0 >= 0 ? vq0 : make_uint4(0, 0, 0, 0);
+        s_v[buf][ld_pv1] = rc1 >= 0 ? vq1 : make_uint4(0, 0, 0, 0);
+        const uint64_t b0 = __ballot(rc0 >= 0), b1 = __ballot(rc1 >= 0);
+        if (lane == 0) {
+          // lanes 16 r hold keys 8 wave + 2 r and 8 wave + 2 r + 1
+          uint32_t bits = 0;
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            bits |= static_cast<uint32_t>(((b0 >> (16 * r)) & 1) | (((b1 >> (16 * r)) & 1) << 1)) << (2 * r);
+          s_okw[buf][wave] = bits;
+        }
+      }
+      __syncthreads();  // block i visible; every wave is done with block i - 2 (same buffer)
+      // block i + 1 in flight while block i is computed
+      if (i + 1 < nblk) {
+        rc0 = rn0;
+        rc1 = rn1;
+        kq0 = ld(kbase, rc0);
+        kq1 = ld(kbase, rc1);
+        vq0 = ld(vbase, rc0);
+        vq1 = ld(vbase, rc1);
+        if (i + 2 < nblk) {
+          rn0 = row_of(i + 2, 0);
+          rn1 = row_of(i + 2, 1);
+        }
+      }
+      if (nheads == 0) continue;
+      const int base = seg_lo + i * kBlk;
+
+      // K A operands of both score tiles (row m = 4a + i <-> key 8a + 4t + i)
+      uint4 ka[2][4];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) ka[t][s] = s_k[buf][pk[t][s]];
+      // mask of the lane's keys 8 quad + e: a pool row, and inside [w_lo, pos]
+      uint32_t kmask = s_okw[buf][quad];
+      {
+        const int k0 = base + 8 * quad;
+        const int lo_e = min(max(w_lo - k0, 0), 8), hi_e = min(max(pos + 1 - k0, 0), 8);
+        kmask &= ((1u << hi_e) - 1u) & ~((1u << lo_e) - 1u);
+        if (!row_ok) kmask = 0;
+      }
+      // blocks inside every row's window with every key present need no masks
+      const bool full = __builtin_amdgcn_read_exec() == ~0ull && !__any(kmask != 0xffu);
+      bf16x8_t pb[HPW];
+#pragma unroll
+      for (int h = 0; h < HPW; ++h) {
+        if (h >= nheads) break;
+        // raw scores (the softmax scale is applied inside exp2: m[h] is a raw
+        // score, p = 2^(q_scale (s - m)))
+        float sv[8];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          f32x4_t c4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[t][s]), as_bf16x8(qreg[h][s]), c4, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sv[4 * t + r] = c4[r];
+        }
+        if (!full) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sv[e] = ((kmask >> e) & 1) ? sv[e] : -INFINITY;
+        }
+        float bmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        // lazy move of the reference point: p <= 2^8 stays exact in fp32
+        if (__any(bmax * p.q_scale > m[h] * p.q_scale + 8.0f)) {
+          const float m_new = fmaxf(m[h], bmax);
+          const float alpha = fast_exp2((m[h] - m_new) * p.q_scale);
+          m[h] = m_new;
+          l[h] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) acc[h][dt] *= alpha;
+        }
+        const float mo = -m[h] * p.q_scale;
+        float psum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float pe = fast_exp2(fmaf(sv[e], p.q_scale, mo));
+          psum += pe;
+          pb[h][e] = static_cast<__bf16>(pe);
+        }
+        l[h] += psum;
+      }
+      // O^T += V^T P^T
+      const uint16_t* vtile = reinterpret_cast<const uint16_t*>(&s_v[buf][0]);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        bf16x4_t part[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) part[hh] = lds_read_tr16(vtile + pv[hh] + 16 * dt);
+        const bf16x8_t va = __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+        for (int h = 0; h < HPW; ++h)
+          if (h < nheads) acc[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[h], acc[h][dt], 0, 0, 0);
+      }
+    }
+    if (nheads == 0 || !row_ok) continue;
+#pragma unroll
+    for (int h = 0; h < HPW; ++h) {
+      if (h >= nheads) break;
+      float lt = l[h] + __shfl_xor(l[h], 16);
+      lt += __shfl_xor(lt, 32);
+      const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+      const int hq = hkv * G + hg0 + h;
+      uint16_t* op = p.out + (grow * Hq + hq) * kHeadDim + 4 * quad;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        uint2 w;
+        w.x = f32_to_bf16(acc[h][dt][0] * inv) | (static_cast<uint32_t>(f32_to_bf16(acc[h][dt][1] * inv)) << 16);
+        w.y = f32_to_bf16(acc[h][dt][2] * inv) | (static_cast<uint32_t>(f32_to_bf16(acc[h][dt][3] * inv)) << 16);
+        *reinterpret_cast<uint2*>(op + 16 * dt) = w;
+      }
+      if (quad == 0) p.out_lse[grow * Hq + hq] = lt > 0.0f ? (m[h] * p.q_scale + fast_log2(lt)) * kLn2 : -INFINITY;
     }
   }
 }
@@ -589,8 +871,15 @@ extern "C" int mac_prefill_window_attention_bf16(const MacWindowAttentionArgs* a
   p.window_left = a->window_left;
   p.q_scale = static_cast<float>(a->sm_scale * 1.4426950408889634);
   const int64_t blocks = (a->total_q + kRows - 1) / kRows + a->B;
-  hipLaunchKernelGGL(window_kernel<false>, dim3(grid_for(4 * blocks * a->Hkv * ceil_div(a->Hq / a->Hkv, 4), reinterpret_cast<const void*>(&window_kernel<false>))), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), p);
+  const int G = a->Hq / a->Hkv;
+  const void* kern = G <= 4 ? reinterpret_cast<const void*>(&window_plain_kernel<1>)
+                            : reinterpret_cast<const void*>(&window_plain_kernel<2>);
+  const int heads_per_task = G <= 4 ? 4 : 8;
+  const int grid = grid_for(4 * blocks * a->Hkv * ceil_div(G, heads_per_task), kern);
+  if (G <= 4)
+    hipLaunchKernelGGL(window_plain_kernel<1>, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), p);
+  else
+    hipLaunchKernelGGL(window_plain_kernel<2>, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), p);
   HIP_OK(hipGetLastError());
   return MAC_OK;
 }
@@ -646,7 +935,7 @@ extern "C" int mac_prefill_rectify_update_cache_bf16(const MacRectifyArgs* a, vo
   const int64_t kept = std::min<int64_t>(a->total_q, static_cast<int64_t>(a->B) * a->M);
   const int64_t blocks = (kept + kRows - 1) / kRows + a->B;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(window_kernel<true>, dim3(grid_for(4 * blocks * a->Hkv * ceil_div(a->Hq / a->Hkv, 4), reinterpret_cast<const void*>(&window_kernel<true>))), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(rectify_kernel, dim3(grid_for(4 * blocks * a->Hkv * ceil_div(a->Hq / a->Hkv, 4), reinterpret_cast<const void*>(&rectify_kernel))), dim3(256), 0, s, p);
   HIP_OK(hipGetLastError());
   if (!p.rl_by_batch) {
     hipLaunchKernelGGL(bump_kernel, dim3((a->B + 255) / 256), dim3(256), 0, s, a->request_length, a->req_ids,
