@@ -181,3 +181,30 @@ def test_bench_mode_override(bench_mode, ext):
                                       bench=bench)
     torch.cuda.synchronize()
     _check_against_oracle(c, dev, out, out_lse, ws, res, what=f"bench{bench_mode}")
+
+
+def _ragged_many(batch, seed):
+    rng = np.random.default_rng(seed)
+    kv_lens = [int(x) for x in rng.integers(20, 120, size=batch)]
+    return syn.random_case(batch=batch, hq=32, hkv=8, kv_lens=kv_lens, capacity=16, semantic_pos_ahead=32,
+                           front_sink_tokens=4, hit_rate=0.5, match_lag=8, seed=seed)
+
+
+def test_largest_plannable_batch(ext):
+    """N * Hkv = 4096 groups, the most one launch plans (the attention
+    kernel's task table in LDS is sized by it): every request against the
+    oracle."""
+    c = _ragged_many(512, 61)
+    print("largest plannable batch: N=512 Hq=32 Hkv=8", flush=True)
+    res = oracle_run(c)
+    dev = syn.to_device(torch, c)
+    out, out_lse, ws = syn.run_decode(torch, ext, dev, c, max_context=160, tile_tokens=32)
+    torch.cuda.synchronize()
+    _check_against_oracle(c, dev, out, out_lse, ws, res, what="N=512 Hkv=8")
+
+
+def test_more_groups_than_one_launch_plans_is_refused(ext):
+    c = _ragged_many(513, 62)
+    dev = syn.to_device(torch, c)
+    with pytest.raises(RuntimeError, match="groups one launch can plan"):
+        syn.run_decode(torch, ext, dev, c, max_context=160, tile_tokens=32)
