@@ -211,6 +211,7 @@ __device__ __forceinline__ uint4 load_stream16(const uint16_t* ptr) {
 // reduces the tiles (kMode 2) instead of scanning.  kMode 0 scans and decides
 // in one workgroup per group.
 constexpr int kSplitSlots = 256;
+constexpr int kLsePrefetchSlots = 64;
 
 template <int G, int kMode>
 __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
@@ -239,6 +240,20 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
   __shared__ float s_d[kWaves][kMaxGroup];
   __shared__ int s_p[kWaves][kMaxGroup];
   __shared__ int s_s[kWaves][kMaxGroup];
+  __shared__ float s_lse[kMaxGroup][kLsePrefetchSlots];  // lse of every slot (small rings)
+
+  // Every load of the scan is independent of the readiness gate and of the
+  // other loads (a request id outside [0, R) reads request 0's rows, and the
+  // results are masked), so the kernel waits for one round of loads, not a
+  // chain.  For rings of at most kLsePrefetchSlots slots the entries' lse
+  // are fetched in the same round, so the decision reads them from LDS.
+  const bool req_ok = req >= 0 && req < p.s.R;
+  const int64_t cache_req = static_cast<int64_t>(req_ok ? req : 0) * M;
+  const bool lse_in_lds = kMode == 0 && M <= kLsePrefetchSlots;
+  if (lse_in_lds && wave == 0 && lane < M) {
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) s_lse[hh][lane] = p.lse_cache[(cache_req + lane) * Hq + hkv * G + hh];
+  }
 
   float best_d[kPasses];
   int best_p[kPasses], best_s[kPasses];
@@ -260,8 +275,7 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
   const int per_split = ceil_div(M, p.splits);
   const int s_lo = kMode == 1 ? static_cast<int>(blockIdx.y) * per_split : 0;
   const int s_hi = kMode == 1 ? min(M, s_lo + per_split) : M;
-  if (kMode != 2 && eligible) {
-    const int64_t cache_req = static_cast<int64_t>(req) * M;
+  if (kMode != 2) {
     for (int s0 = s_lo + wave; s0 < s_hi; s0 += kWaves * kSlotBatch) {
       // every pass's loads of the batch are in flight before any reduction
       uint4 w[kPasses][kSlotBatch];
@@ -271,19 +285,16 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
       for (int u = 0; u < kSlotBatch; ++u) {
         const int slot = s0 + u * kWaves;
         pos[u] = ring_slot_to_pos(P, M, slot);
-        in_window[u] = slot < s_hi && pos[u] >= cand_begin && pos[u] < cand_end;
+        in_window[u] = eligible && slot < s_hi && pos[u] >= cand_begin && pos[u] < cand_end;
       }
 #pragma unroll
       for (int ps = 0; ps < kPasses; ++ps) {
-        const int hl = row + 4 * ps;
+        const int hl = min(row + 4 * ps, G - 1);
 #pragma unroll
         for (int u = 0; u < kSlotBatch; ++u) {
-          w[ps][u] = make_uint4(0, 0, 0, 0);
-          if (in_window[u] && hl < G) {
-            const int64_t off =
-                ((cache_req + s0 + u * kWaves) * Hq + hkv * G + hl) * kHeadDim + c * 8;
-            w[ps][u] = load_stream16(p.query_cache + off);  // ring rows are read once per step
-          }
+          const int slot = min(s0 + u * kWaves, s_hi - 1);  // past the range: re-reads its last row
+          const int64_t off = ((cache_req + slot) * Hq + hkv * G + hl) * kHeadDim + c * 8;
+          w[ps][u] = load_stream16(p.query_cache + off);  // ring rows are read once per step
         }
       }
 #pragma unroll
@@ -441,7 +452,7 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
   // DECODE:1315-1328 validity of a hit head for MAC reuse
   bool valid = false;
   if (head_lane && hit && mslot >= 0) {
-    const float pl = p.lse_cache[(static_cast<int64_t>(req) * M + mslot) * Hq + hq];
+    const float pl = lse_in_lds ? s_lse[h][mslot] : p.lse_cache[(static_cast<int64_t>(req) * M + mslot) * Hq + hq];
     const int clen = new_end - prefix_end;
     valid = isfinite(pl) && clen >= 0 && clen <= M;
   }
