@@ -67,6 +67,8 @@ def parse_args():
     ap.add_argument("--ref-shape-hits", default="0,0.5,0.8,0.9,1.0",
                     help="hit ratios measured at the reference's published benchmark shape "
                          "(ring 2048, past_len 126976); empty to skip")
+    ap.add_argument("--aux-only", action="store_true",
+                    help="run only the prefill-rectification and decode-RoPE legs (prints their JSON)")
     ap.add_argument("--no-aux", action="store_true",
                     help="skip the prefill-rectification and decode-RoPE measurements")
     return ap.parse_args()
@@ -371,6 +373,11 @@ def main():
                                    "so --gpus must be 1 (multi-GPU sharding is design-only)"}))
         sys.exit(2)
     import torch
+
+    if args.aux_only:
+        assert torch.cuda.is_available(), "bench.py needs a HIP device"
+        print(json.dumps({"aux": measure_aux(torch)}), flush=True)
+        return
 
     from mac_attention import synthetic as syn
     from mac_attention.integrations.sglang.bridge import load_mac_persistent_decode_extension
