@@ -47,6 +47,17 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+// gfx950 transposing LDS read (ds_read_b64_tr_b16).  Every lane passes the
+// address of four consecutive 16-bit elements; in each group of 16 lanes,
+// lane i receives element (i & 3) of the vectors of lanes 4e + (i >> 2),
+// e = 0..3.  With lane j pointing at row r0 + (j >> 2), columns c0 + 4 (j & 3)
+// of a row-major tile, lane i gets column c0 + i of rows r0 .. r0 + 3: the
+// transposed 4 x 16 block, as an MFMA operand wants it.
+__device__ __forceinline__ bf16x4_t lds_read_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_t*)(p));
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 

@@ -994,21 +994,30 @@ __global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
 //    from HBM, whose layout splits lines across instructions.  The block
 //    after the current one is always in flight in registers; its
 //    req_to_token entries are loaded one block earlier still.
-//  * The rows are staged in two 8 KiB per-wave LDS tiles.  In the K tile,
-//    16-byte chunk c of token t sits at position c ^ (t & 15), so the MFMA
-//    A-operand reads of 16 tokens hit 16 different bank groups; in the V tile
-//    at c ^ 2*((t >> 2) & 3), so the column gathers of 4 token groups do.
+//  * The rows are staged in two 8 KiB per-wave LDS tiles, token-major.  In
+//    the K tile, 16-byte chunk c of token t sits at position c ^ k_swz(t)
+//    (see below), so the 16 tokens one A-operand read touches hit 16
+//    different bank groups; in the V tile at c ^ 2 (t & 7), which does the
+//    same for the transposing reads.
 //  * S^T[t][g] = sum_d K[t][d] Q[g][d] and O^T[d][g] += sum_t V[t][d] P[g][t]
-//    both run on v_mfma_f32_16x16x32_bf16.  The lane holding head g = l%16
-//    keeps that head's softmax state, its scores (already the B operand of
-//    the PV product after conversion to bf16, by the choice of token order on
-//    the k axis) and its 32 O^T accumulators, so the online-softmax rescale is
+//    both run on v_mfma_f32_16x16x32_bf16.  MFMA row 4a + i of score tile t
+//    is token 8a + 4t + i, so the lane holding head g = l%16 ends with the
+//    scores of tokens 8q .. 8q + 7 (q = l/16): after conversion to bf16 they
+//    are the B operand of the PV product as they stand, and its A operand
+//    V^T[16 dt + g][8q .. 8q + 7] is two ds_read_b64_tr_b16 (gfx950's
+//    transposing LDS read) of the V tile.  The lane keeps its head's softmax
+//    state and 32 O^T accumulators, so the online-softmax rescale is
 //    lane-local.  Heads g >= G are zero padding rows of the 16-wide MFMA.
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& w) { return __builtin_bit_cast(bf16x8_t, w); }
+
+// K tile: 16-byte chunk c of token t at position c ^ k_swz(t) of its row.
+// The S^T tiles read tokens 8a + 4t + i (a, i < 4) in one instruction; this
+// swizzle puts the 16 of them on 16 different chunk positions.
+__device__ __forceinline__ int k_swz(int t) { return 4 * ((t >> 3) & 3) + (t & 3); }
 
 template <int G>
 __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnParams p) {
@@ -1128,8 +1137,8 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
         w.y &= keep;
         w.z &= keep;
         w.w &= keep;
-        s_k[wave][tok * 16 + (col ^ (tok & 15))] = kr[i];
-        s_v[wave][tok * 16 + (col ^ (2 * ((tok >> 2) & 3)))] = w;
+        s_k[wave][tok * 16 + (col ^ k_swz(tok))] = kr[i];
+        s_v[wave][tok * 16 + (col ^ (2 * (tok & 7)))] = w;
       }
       __builtin_amdgcn_sched_barrier(0);
       // the next block's rows go in flight while this block is computed
@@ -1146,10 +1155,10 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
 #pragma unroll
       for (int tile = 0; tile < 2; ++tile) {
         f32x4_t c4 = {0.0f, 0.0f, 0.0f, 0.0f};
-        const int tok = 16 * tile + col;
+        const int tok = 8 * (col >> 2) + 4 * tile + (col & 3);  // MFMA row col of this tile
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-          c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(s_k[wave][tok * 16 + ((4 * s + quad) ^ col)]),
+          c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(s_k[wave][tok * 16 + ((4 * s + quad) ^ k_swz(tok))]),
                                                       as_bf16x8(s_q[col * 16 + 4 * s + quad]), c4, 0, 0, 0);
         st[tile] = c4;
       }
@@ -1161,7 +1170,7 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
       for (int tile = 0; tile < 2; ++tile) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int tok = 16 * tile + 4 * quad + r;
+          const int tok = 8 * quad + 4 * tile + r;
           const bool ok = head_ok && ((vmask >> tok) & 1) && base + tok >= head_begin;
           const float x = ok ? st[tile][r] * p.q_scale : -INFINITY;
           sv[4 * tile + r] = x;
@@ -1192,17 +1201,19 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
         pb[e] = static_cast<__bf16>(pe);
       }
       l += psum;
-      // O^T += V^T P^T: A operand gathered from the V tile
+      // O^T += V^T P^T: the A operand V^T[16 dt + col][tokens 8 quad .. +8]
+      // is two transposing reads of tokens 8 quad + 4 h + (col >> 2), dims
+      // 16 dt + 4 (col & 3) .. +3 (16-byte chunk 2 dt + ((col & 3) >> 1))
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const int chunk_pos = (2 * (dt ^ quad) + (col >> 3));
-        bf16x8_t va;
+        bf16x4_t part[2];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int tok = e < 4 ? 4 * quad + e : 16 + 4 * quad + (e - 4);
-          const uint16_t bits = vtile[(tok * 16 + chunk_pos) * 8 + (col & 7)];
-          va[e] = __builtin_bit_cast(__bf16, bits);
+        for (int h = 0; h < 2; ++h) {
+          const int t = 8 * quad + 4 * h + (col >> 2);
+          const int c = (2 * dt + ((col & 3) >> 1)) ^ (2 * (t & 7));
+          part[h] = lds_read_tr16(vtile + t * 128 + c * 8 + (col & 1) * 4);
         }
+        const bf16x8_t va = __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7);
         acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, acc[dt], 0, 0, 0);
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -487,10 +487,6 @@ __global__ void __launch_bounds__(256) rectify_kernel(WindowParams p) {
 // the mask of its 8 keys with the row's window bounds by shifts.  The running
 // maximum is moved lazily (only when a block exceeds it by 2^8), which leaves
 // the result exact and skips most accumulator rescales.
-typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ bf16x4_t lds_read_tr16(const uint16_t* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_t*)(p));
-}
 
 constexpr int kVRow = 18;  // 16-byte units per staged V row: 256 bytes + 32 of padding
 
