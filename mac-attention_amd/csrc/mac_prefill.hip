@@ -672,11 +672,18 @@ __global__ void __launch_bounds__(256, 2) window_plain_kernel(WindowParams p) {
       const int base = seg_lo + i * kBlk;
 
       // K A operands of both score tiles (row m = 4a + i <-> key 8a + 4t + i)
+      // and V A operands of the eight 16-dim tiles, all issued up front
       uint4 ka[2][4];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int s = 0; s < 4; ++s) ka[t][s] = s_k[buf][pk[t][s]];
+      const uint16_t* vtile = reinterpret_cast<const uint16_t*>(&s_v[buf][0]);
+      bf16x8_t va[8];
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+        va[dt] = __builtin_shufflevector(lds_read_tr16(vtile + pv[0] + 16 * dt), lds_read_tr16(vtile + pv[1] + 16 * dt),
+                                         0, 1, 2, 3, 4, 5, 6, 7);
       // mask of the lane's keys 8 quad + e: a pool row, and inside [w_lo, pos]
       uint32_t kmask = s_okw[buf][quad];
       {
@@ -686,23 +693,32 @@ __global__ void __launch_bounds__(256, 2) window_plain_kernel(WindowParams p) {
         if (!row_ok) kmask = 0;
       }
       // blocks inside every row's window with every key present need no masks
-      const bool full = __builtin_amdgcn_read_exec() == ~0ull && !__any(kmask != 0xffu);
+      const bool full = !__any(kmask != 0xffu);
+      // raw scores of both tiles and every head, the four accumulation chains
+      // interleaved (an absent head has zero Q rows and is never stored)
+      f32x4_t c4[HPW][2];
+#pragma unroll
+      for (int h = 0; h < HPW; ++h)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) c4[h][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int h = 0; h < HPW; ++h)
+            c4[h][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[t][s]), as_bf16x8(qreg[h][s]), c4[h][t],
+                                                              0, 0, 0);
       bf16x8_t pb[HPW];
 #pragma unroll
       for (int h = 0; h < HPW; ++h) {
-        if (h >= nheads) break;
-        // raw scores (the softmax scale is applied inside exp2: m[h] is a raw
-        // score, p = 2^(q_scale (s - m)))
+        // the softmax scale is applied inside exp2: m[h] is a raw score,
+        // p = 2^(q_scale (s - m))
         float sv[8];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          f32x4_t c4 = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int s = 0; s < 4; ++s)
-            c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[t][s]), as_bf16x8(qreg[h][s]), c4, 0, 0, 0);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) sv[4 * t + r] = c4[r];
-        }
+          for (int r = 0; r < 4; ++r) sv[4 * t + r] = c4[h][t][r];
         if (!full) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) sv[e] = ((kmask >> e) & 1) ? sv[e] : -INFINITY;
@@ -730,17 +746,10 @@ __global__ void __launch_bounds__(256, 2) window_plain_kernel(WindowParams p) {
         l[h] += psum;
       }
       // O^T += V^T P^T
-      const uint16_t* vtile = reinterpret_cast<const uint16_t*>(&s_v[buf][0]);
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        bf16x4_t part[2];
+      for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) part[hh] = lds_read_tr16(vtile + pv[hh] + 16 * dt);
-        const bf16x8_t va = __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7);
-#pragma unroll
-        for (int h = 0; h < HPW; ++h)
-          if (h < nheads) acc[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[h], acc[h][dt], 0, 0, 0);
-      }
+        for (int h = 0; h < HPW; ++h) acc[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], pb[h], acc[h][dt], 0, 0, 0);
     }
     if (nheads == 0 || !row_ok) continue;
 #pragma unroll
