@@ -612,29 +612,35 @@ __global__ void __launch_bounds__(256, 2) window_plain_kernel(WindowParams p) {
     const uint16_t* kbase = p.k + static_cast<int64_t>(hkv) * kHeadDim + ld_chunk * 8;
     const uint16_t* vbase = p.v + static_cast<int64_t>(hkv) * kHeadDim + ld_chunk * 8;
     const int nblk = seg_hi > seg_lo ? ceil_div(seg_hi - seg_lo, kBlk) : 0;
-    // pool row of the loader's key ld_key + t of block i (-1: masked)
-    auto row_of = [&](int i, int t) -> int {
+    // The loader's key ld_key + t of block i: its kv_indices entry (the load
+    // only, index clamped into the request) and, checked later, its pool row
+    // (-1: masked).  An index is loaded one block before it is checked, so
+    // the wait for it never includes K/V loads issued after it (the memory
+    // counter retires in order).
+    auto index_of = [&](int i, int t) -> int {
       const int key = seg_lo + i * kBlk + ld_key + t;
-      const int raw = p.kv_indices[kv_begin + min(key, kvlen - 1)];
+      return p.kv_indices[kv_begin + min(key, kvlen - 1)];
+    };
+    auto row_of = [&](int i, int t, int raw) -> int {
+      const int key = seg_lo + i * kBlk + ld_key + t;
       return (key < seg_hi && static_cast<unsigned>(raw) < pool_rows) ? raw : -1;
     };
     auto ld = [&](const uint16_t* base, int r) -> uint4 {
       return *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(max(r, 0)) * kv_stride);
     };
     // the loader's K/V chunks of the block in flight (rc0/rc1: their rows)
-    int rc0 = -1, rc1 = -1, rn0 = -1, rn1 = -1;
+    // and the raw indices of the block after it
+    int rc0 = -1, rc1 = -1, rn0 = 0, rn1 = 0;
     uint4 kq0 = make_uint4(0, 0, 0, 0), kq1 = kq0, vq0 = kq0, vq1 = kq0;
     if (nblk > 0) {
-      rc0 = row_of(0, 0);
-      rc1 = row_of(0, 1);
+      rc0 = row_of(0, 0, index_of(0, 0));
+      rc1 = row_of(0, 1, index_of(0, 1));
       kq0 = ld(kbase, rc0);
       kq1 = ld(kbase, rc1);
       vq0 = ld(vbase, rc0);
       vq1 = ld(vbase, rc1);
-      if (nblk > 1) {
-        rn0 = row_of(1, 0);
-        rn1 = row_of(1, 1);
-      }
+      rn0 = index_of(1, 0);
+      rn1 = index_of(1, 1);
     }
     for (int i = 0; i < nblk; ++i) {
       const int buf = i & 1;
@@ -657,16 +663,14 @@ __global__ void __launch_bounds__(256, 2) window_plain_kernel(WindowParams p) {
       __syncthreads();  // block i visible; every wave is done with block i - 2 (same buffer)
       // block i + 1 in flight while block i is computed
       if (i + 1 < nblk) {
-        rc0 = rn0;
-        rc1 = rn1;
+        rc0 = row_of(i + 1, 0, rn0);
+        rc1 = row_of(i + 1, 1, rn1);
         kq0 = ld(kbase, rc0);
         kq1 = ld(kbase, rc1);
         vq0 = ld(vbase, rc0);
         vq1 = ld(vbase, rc1);
-        if (i + 2 < nblk) {
-          rn0 = row_of(i + 2, 0);
-          rn1 = row_of(i + 2, 1);
-        }
+        rn0 = index_of(i + 2, 0);  // clamped: harmless past the last block
+        rn1 = index_of(i + 2, 1);
       }
       if (nheads == 0) continue;
       const int base = seg_lo + i * kBlk;
