@@ -299,28 +299,32 @@ __global__ void __launch_bounds__(256) rectify_kernel(WindowParams p) {
       const int r_lo = seg == 0 ? 0 : w_lo;  // this row's bounds in the segment
       const int r_hi = seg == 0 ? s_hi : pos + 1;
       const int nblk = seg_hi > seg_lo ? ceil_div(seg_hi - seg_lo, kBlk) : 0;
-      // rows of the loader's two keys of block i (-1: masked)
-      auto rows_of = [&](int i, int (&r)[2]) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int key = seg_lo + i * kBlk + ld_key + 16 * t;
-          const int raw = p.kv_indices[kv_begin + min(key, kvlen - 1)];
-          r[t] = (key < seg_hi && static_cast<unsigned>(raw) < pool_rows) ? raw : -1;
-        }
+      // kv_indices entry of the loader's key t of block i (clamped: always a
+      // valid address) and the pool row it names (-1: masked).  The entries
+      // of block i + 2 are loaded after block i + 1's K/V and checked only an
+      // iteration later: checking them at once would wait on those K/V loads.
+      auto index_of = [&](int i, int t) -> int {
+        const int key = seg_lo + i * kBlk + ld_key + 16 * t;
+        return p.kv_indices[kv_begin + min(key, kvlen - 1)];
       };
-      uint4 kq[2], vq[2];  // the loader's K/V chunks of the block in flight
-      auto issue = [&](const int (&r)[2]) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          kq[t] = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(max(r[t], 0)) * kv_stride);
-          vq[t] = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(max(r[t], 0)) * kv_stride);
-        }
+      auto row_of = [&](int i, int t, int raw) -> int {
+        const int key = seg_lo + i * kBlk + ld_key + 16 * t;
+        return (key < seg_hi && static_cast<unsigned>(raw) < pool_rows) ? raw : -1;
       };
-      int rc[2], rn[2];
+      uint4 kq0, kq1, vq0, vq1;  // the loader's K/V chunks of the block in flight
+      auto issue = [&](int r0, int r1) {
+        kq0 = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(max(r0, 0)) * kv_stride);
+        vq0 = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(max(r0, 0)) * kv_stride);
+        kq1 = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(max(r1, 0)) * kv_stride);
+        vq1 = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(max(r1, 0)) * kv_stride);
+      };
+      int rc0 = -1, rc1 = -1, rn0 = 0, rn1 = 0;
       if (nblk > 0) {
-        rows_of(0, rc);
-        issue(rc);
-        if (nblk > 1) rows_of(1, rn);
+        rc0 = row_of(0, 0, index_of(0, 0));
+        rc1 = row_of(0, 1, index_of(0, 1));
+        issue(rc0, rc1);
+        rn0 = index_of(1, 0);
+        rn1 = index_of(1, 1);
       }
       for (int i = 0; i < nblk; ++i) {
         const int buf = i & 1;
@@ -328,19 +332,21 @@ __global__ void __launch_bounds__(256) rectify_kernel(WindowParams p) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           const int tok = ld_key + 16 * t;
-          uint4 w = vq[t];
-          if (rc[t] < 0) w = make_uint4(0, 0, 0, 0);
-          s_k[buf][tok * 16 + (ld_chunk ^ (tok & 15))] = kq[t];
+          const int rct = t == 0 ? rc0 : rc1;
+          uint4 w = t == 0 ? vq0 : vq1;
+          if (rct < 0) w = make_uint4(0, 0, 0, 0);
+          s_k[buf][tok * 16 + (ld_chunk ^ (tok & 15))] = t == 0 ? kq0 : kq1;
           s_v[buf][tok * 16 + (ld_chunk ^ (2 * ((tok >> 2) & 3)))] = w;
-          if (ld_chunk == 0) s_ok[buf][tok] = rc[t] >= 0 ? 1 : 0;
+          if (ld_chunk == 0) s_ok[buf][tok] = rct >= 0 ? 1 : 0;
         }
         __syncthreads();  // block i visible; every wave is done with block i - 2 (same buffer)
         // block i + 1 in flight while block i is computed
         if (i + 1 < nblk) {
-          rc[0] = rn[0];
-          rc[1] = rn[1];
-          issue(rc);
-          if (i + 2 < nblk) rows_of(i + 2, rn);
+          rc0 = row_of(i + 1, 0, rn0);
+          rc1 = row_of(i + 1, 1, rn1);
+          issue(rc0, rc1);
+          rn0 = index_of(i + 2, 0);  // clamped: harmless past the last block
+          rn1 = index_of(i + 2, 1);
         }
         if (!head_valid) continue;
         const int base = seg_lo + i * kBlk;
