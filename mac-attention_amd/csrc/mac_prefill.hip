@@ -373,8 +373,7 @@ __global__ void __launch_bounds__(256) rectify_kernel(WindowParams p) {
             bmax = fmaxf(bmax, x);
           }
         }
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        bmax = quad_max(bmax);
         if (bmax > m) {  // exact online softmax (per lane: its row's state)
           const float alpha = fast_exp2(m - bmax);
           m = bmax;
@@ -415,8 +414,7 @@ __global__ void __launch_bounds__(256) rectify_kernel(WindowParams p) {
     }
     if (!head_valid) continue;
 
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    l = quad_sum(l);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     const float lse_w = l > 0.0f ? (m + fast_log2(l)) * kLn2 : -INFINITY;
     if (!row_ok) continue;
@@ -734,8 +732,7 @@ __global__ void __launch_bounds__(256, 2) window_plain_kernel(WindowParams p) {
           for (int e = 0; e < 8; ++e) sv[e] = ((kmask >> e) & 1) ? sv[e] : -INFINITY;
         }
         float bmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        bmax = quad_max(bmax);
         // lazy move of the reference point: p <= 2^8 stays exact in fp32
         if (__any(bmax * p.q_scale > m[h] * p.q_scale + 8.0f)) {
           const float m_new = fmaxf(m[h], bmax);
@@ -765,8 +762,7 @@ __global__ void __launch_bounds__(256, 2) window_plain_kernel(WindowParams p) {
 #pragma unroll
     for (int h = 0; h < HPW; ++h) {
       if (h >= nheads) break;
-      float lt = l[h] + __shfl_xor(l[h], 16);
-      lt += __shfl_xor(lt, 32);
+      const float lt = quad_sum(l[h]);
       const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
       const int hq = hkv * G + hg0 + h;
       uint16_t* op = p.out + (grow * Hq + hq) * kHeadDim + 4 * quad;
