@@ -10,21 +10,21 @@
 //
 //  * downdate_kernel: the reference's downdate op on its own (any head_dim,
 //    f32/bf16/f16 lse), for callers that keep the reference's three calls.
-//  * window_plain_kernel: causal sliding-window attention over a ragged
-//    batch with a page-size-1 KV pool (the windowed FlashInfer pass).
-//  * rectify_kernel: the fused form.  Only the rows the ring keeps (the last
-//    min(len, M) of each request) are computed; for them the window state
-//    never leaves registers: it is downdated from the full state and stored
-//    straight into the ring with the pre-RoPE query, followed by the
+//  * window_kernel<HPW, false>: causal sliding-window attention over a
+//    ragged batch with a page-size-1 KV pool (the windowed FlashInfer pass).
+//  * window_kernel<HPW, true>: the fused form.  Only the rows the ring keeps
+//    (the last min(len, M) of each request) are computed; for them the window
+//    state never leaves registers: it is downdated from the full state and
+//    stored straight into the ring with the pre-RoPE query, followed by the
 //    request_length bump (bump_kernel).
 //
-// Both run S^T[key][row] = K Q^T and O^T[d][row] += V^T P^T on
+// Both forms run S^T[key][row] = K Q^T and O^T[d][row] += V^T P^T on
 // v_mfma_f32_16x16x32_bf16 as the decode kernel does, with 16 query rows in
 // place of the GQA heads: the lane holding row l%16 keeps that row's softmax
 // state and 32 O^T accumulators per head.  A workgroup takes 16 rows of one
 // request and several query heads of one KV head; its four waves share
-// double-buffered LDS K/V tiles of 32 keys.  The layouts of each kernel are
-// described above it.
+// double-buffered LDS K/V tiles of 32 keys.  The layouts are described above
+// window_kernel.
 
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
@@ -191,284 +191,11 @@ __device__ __forceinline__ int request_rows(const WindowParams& p, int b) {
   return ok ? len - first_row<kRectify>(len, p.M) : 0;
 }
 
-__global__ void __launch_bounds__(256) rectify_kernel(WindowParams p) {
-  __shared__ int s_boff[kMaxB + 1];  // row-block offsets per request
-  __shared__ int s_part[256];
-  __shared__ uint4 s_k[2][kBlk * 16];  // double-buffered K / V tiles of 32 keys, shared by the four waves
-  __shared__ uint4 s_v[2][kBlk * 16];
-  __shared__ int s_ok[2][kBlk];        // key has a pool row
-
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lane = tid & 63;
-  const int quad = lane >> 4;
-  const int col = lane & 15;
-
-  // ---- plan: s_boff[b] = sum over b' < b of ceil(rows(b') / 16) ----
-  const int B = p.B;
-  const int per = ceil_div(B, 256);
-  {
-    int sum = 0;
-    for (int b = tid * per; b < min(B, (tid + 1) * per); ++b) {
-      const int rows = request_rows<true>(p, b);
-      sum += ceil_div(rows, kRows);
-    }
-    s_part[tid] = sum;
-    __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {  // inclusive Hillis-Steele scan
-      const int x = tid >= off ? s_part[tid - off] : 0;
-      __syncthreads();
-      s_part[tid] += x;
-      __syncthreads();
-    }
-    int acc = tid > 0 ? s_part[tid - 1] : 0;
-    for (int b = tid * per; b < min(B, (tid + 1) * per); ++b) {
-      s_boff[b] = acc;
-      const int rows = request_rows<true>(p, b);
-      acc += ceil_div(rows, kRows);
-    }
-    if (tid == 255) s_boff[B] = s_part[255];
-    __syncthreads();
-  }
-  const int Hq = p.Hq, Hkv = p.Hkv;
-  const int G = Hq / Hkv;
-  const int nquads = ceil_div(G, 4);  // workgroups per (row block, KV head): 4 query heads each
-  const int total_tasks = s_boff[B] * Hkv * nquads;
-  const int64_t kv_stride = static_cast<int64_t>(Hkv) * kHeadDim;
-  const unsigned pool_rows = static_cast<unsigned>(min(p.pool_tokens, static_cast<int64_t>(INT_MAX)));
-  // loader side: thread t stages 16-byte chunk t%16 of keys t/16 and t/16 + 16
-  const int ld_key = tid >> 4, ld_chunk = tid & 15;
-
-  for (int task = blockIdx.x; task < total_tasks; task += gridDim.x) {
-    __syncthreads();  // the previous task's waves are done with the tiles
-    const int blk = task / (Hkv * nquads);
-    const int rem = task - blk * Hkv * nquads;
-    const int hkv = rem / nquads;
-    const int hg = 4 * (rem - hkv * nquads) + wave;  // head within the group
-    const bool head_valid = hg < G;                   // wave-uniform
-    const int h = hkv * G + (head_valid ? hg : 0);
-    // request of this row block: largest b with s_boff[b] <= blk
-    int lo = 0, hi = B - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_boff[mid] <= blk) lo = mid;
-      else hi = mid - 1;
-    }
-    const int b = lo;
-    const int len = p.qo_indptr[b + 1] - p.qo_indptr[b];
-    const int kvlen = p.kv_indptr[b + 1] - p.kv_indptr[b];
-    const int64_t kv_begin = p.kv_indptr[b];
-    const int r_local = first_row<true>(len, p.M) + kRows * (blk - s_boff[b]);
-    const int nrows = min(kRows, len - r_local);
-    const int pos0 = kvlen - len + r_local;
-    const int pos_last = pos0 + nrows - 1;
-    const bool row_ok = col < nrows;
-    const int pos = pos0 + col;  // this lane's row position
-    const int64_t grow = static_cast<int64_t>(p.qo_indptr[b]) + r_local + (row_ok ? col : 0);
-
-    // window bounds of this lane's row and of the workgroup's key range
-    const int w_lo = max(pos + 1 - p.S, 0);
-    const int w_lo0 = max(pos0 + 1 - p.S, 0);
-    const bool sink = p.sink_mode == 1 && p.F > 0;
-    const int s_hi = sink ? min(p.F, max(pos + 1 - p.S, 0)) : 0;             // this row's sink end
-    const int s_hi_last = sink ? min(p.F, max(pos_last + 1 - p.S, 0)) : 0;  // the workgroup's
-
-    // Q row (B operand): lane (quad, col) holds Q[row col][8*(4s+quad) .. +8]
-    uint4 qreg[4];
-    {
-      const uint16_t* qp = p.q + (grow * Hq + h) * kHeadDim;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        uint4 w = *reinterpret_cast<const uint4*>(qp + 8 * (4 * s + quad));
-        if (!row_ok || !head_valid) w = make_uint4(0, 0, 0, 0);
-        qreg[s] = w;
-      }
-    }
-
-    float m = kNegBig, l = 0.0f;
-    f32x4_t acc[8];
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-    const uint16_t* kbase = p.k + static_cast<int64_t>(hkv) * kHeadDim + ld_chunk * 8;
-    const uint16_t* vbase = p.v + static_cast<int64_t>(hkv) * kHeadDim + ld_chunk * 8;
-    // segment 0: the front sink (fused mode, sink_mode 1); segment 1: the window
-    for (int seg = sink ? 0 : 1; seg < 2; ++seg) {
-      const int seg_lo = seg == 0 ? 0 : w_lo0;
-      const int seg_hi = seg == 0 ? s_hi_last : pos_last + 1;
-      const int r_lo = seg == 0 ? 0 : w_lo;  // this row's bounds in the segment
-      const int r_hi = seg == 0 ? s_hi : pos + 1;
-      const int nblk = seg_hi > seg_lo ? ceil_div(seg_hi - seg_lo, kBlk) : 0;
-      // kv_indices entry of the loader's key t of block i (clamped: always a
-      // valid address) and the pool row it names (-1: masked).  The entries
-      // of block i + 2 are loaded after block i + 1's K/V and checked only an
-      // iteration later: checking them at once would wait on those K/V loads.
-      auto index_of = [&](int i, int t) -> int {
-        const int key = seg_lo + i * kBlk + ld_key + 16 * t;
-        return p.kv_indices[kv_begin + min(key, kvlen - 1)];
-      };
-      auto row_of = [&](int i, int t, int raw) -> int {
-        const int key = seg_lo + i * kBlk + ld_key + 16 * t;
-        return (key < seg_hi && static_cast<unsigned>(raw) < pool_rows) ? raw : -1;
-      };
-      uint4 kq0, kq1, vq0, vq1;  // the loader's K/V chunks of the block in flight
-      auto issue = [&](int r0, int r1) {
-        kq0 = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(max(r0, 0)) * kv_stride);
-        vq0 = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(max(r0, 0)) * kv_stride);
-        kq1 = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(max(r1, 0)) * kv_stride);
-        vq1 = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(max(r1, 0)) * kv_stride);
-      };
-      int rc0 = -1, rc1 = -1, rn0 = 0, rn1 = 0;
-      if (nblk > 0) {
-        rc0 = row_of(0, 0, index_of(0, 0));
-        rc1 = row_of(0, 1, index_of(0, 1));
-        issue(rc0, rc1);
-        rn0 = index_of(1, 0);
-        rn1 = index_of(1, 1);
-      }
-      for (int i = 0; i < nblk; ++i) {
-        const int buf = i & 1;
-        // stage block i (V of masked keys zeroed) and its key validity
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int tok = ld_key + 16 * t;
-          const int rct = t == 0 ? rc0 : rc1;
-          uint4 w = t == 0 ? vq0 : vq1;
-          if (rct < 0) w = make_uint4(0, 0, 0, 0);
-          s_k[buf][tok * 16 + (ld_chunk ^ (tok & 15))] = t == 0 ? kq0 : kq1;
-          s_v[buf][tok * 16 + (ld_chunk ^ (2 * ((tok >> 2) & 3)))] = w;
-          if (ld_chunk == 0) s_ok[buf][tok] = rct >= 0 ? 1 : 0;
-        }
-        __syncthreads();  // block i visible; every wave is done with block i - 2 (same buffer)
-        // block i + 1 in flight while block i is computed
-        if (i + 1 < nblk) {
-          rc0 = row_of(i + 1, 0, rn0);
-          rc1 = row_of(i + 1, 1, rn1);
-          issue(rc0, rc1);
-          rn0 = index_of(i + 2, 0);  // clamped: harmless past the last block
-          rn1 = index_of(i + 2, 1);
-        }
-        if (!head_valid) continue;
-        const int base = seg_lo + i * kBlk;
-        const uint16_t* vtile = reinterpret_cast<const uint16_t*>(&s_v[buf][0]);
-
-        // S^T = K Q^T; lane (quad, col): row col, keys 16 t + 4 quad + r
-        float sv[8];
-        float bmax = kNegBig;
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          f32x4_t c4 = {0.0f, 0.0f, 0.0f, 0.0f};
-          const int tok = 16 * t + col;
-#pragma unroll
-          for (int s = 0; s < 4; ++s)
-            c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(s_k[buf][tok * 16 + ((4 * s + quad) ^ col)]),
-                                                        as_bf16x8(qreg[s]), c4, 0, 0, 0);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int kk = 16 * t + 4 * quad + r;
-            const int key = base + kk;
-            const bool ok = row_ok && s_ok[buf][kk] != 0 && key >= r_lo && key < r_hi;
-            const float x = ok ? c4[r] * p.q_scale : -INFINITY;
-            sv[4 * t + r] = x;
-            bmax = fmaxf(bmax, x);
-          }
-        }
-        bmax = quad_max(bmax);
-        if (bmax > m) {  // exact online softmax (per lane: its row's state)
-          const float alpha = fast_exp2(m - bmax);
-          m = bmax;
-          l *= alpha;
-#pragma unroll
-          for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
-        }
-        // P as the B operand.  The fused form also feeds the bf16 rounding
-        // residual of P through a second MFMA (P = hi + lo, ~16 significant
-        // bits): the downdate divides the window's contribution by the
-        // prefix's share of the softmax mass, which amplifies any error of
-        // the window state.
-        bf16x8_t pb, pl;
-        float psum = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float pe = fast_exp2(sv[e] - m);
-          psum += pe;
-          pb[e] = static_cast<__bf16>(pe);
-          pl[e] = static_cast<__bf16>(pe - static_cast<float>(pb[e]));
-        }
-        l += psum;
-        // O^T += V^T P^T; k index e of the lane <-> key (e < 4 ? 4q+e : 16+4q+e-4)
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-          const int chunk_pos = 2 * (dt ^ quad) + (col >> 3);
-          bf16x8_t va;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int tok = e < 4 ? 4 * quad + e : 16 + 4 * quad + (e - 4);
-            va[e] = __builtin_bit_cast(__bf16, vtile[(tok * 16 + chunk_pos) * 8 + (col & 7)]);
-          }
-          acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, acc[dt], 0, 0, 0);
-          acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl, acc[dt], 0, 0, 0);
-        }
-      }
-      __syncthreads();  // the segment's last tiles are read before the next segment stages into them
-    }
-    if (!head_valid) continue;
-
-    l = quad_sum(l);
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    const float lse_w = l > 0.0f ? (m + fast_log2(l)) * kLn2 : -INFINITY;
-    if (!row_ok) continue;
-
-    // ---- fused: downdate the full state, store the ring row ----
-    const int req = p.req_ids[b];
-    if (req < 0 || req >= p.R) continue;
-    int before = p.rl_by_batch ? p.request_length[b] : p.request_length[req];
-    if (before < 0) before = 0;
-    const int local = r_local + col;  // row index within the request
-    const int slot = static_cast<int>((static_cast<int64_t>(before) + local) % p.M);
-    const int64_t drow = static_cast<int64_t>(req) * p.M + slot;
-    const int e_end = pos + 1 - p.S;
-    const bool empty = e_end <= (sink ? p.F : 0);
-    Downdate c;
-    if (empty) {
-      c.lse = -INFINITY;
-      c.t = 0.0f;
-      c.scale = 0.0f;
-    } else {
-      c = downdate_control(p.lse_full[grow * Hq + h], lse_w);
-    }
-    const uint16_t* of = p.o_full + (grow * Hq + h) * kHeadDim + 4 * quad;
-    uint16_t* ap = p.attn_cache + (drow * Hq + h) * kHeadDim + 4 * quad;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const uint2 f = *reinterpret_cast<const uint2*>(of + 16 * dt);
-      float r[4];
-      const float fo[4] = {bf16_lo(f.x), bf16_hi(f.x), bf16_lo(f.y), bf16_hi(f.y)};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) r[i] = empty ? 0.0f : (fo[i] - c.t * (acc[dt][i] * inv)) * c.scale;
-      uint2 w;
-      w.x = f32_to_bf16(r[0]) | (static_cast<uint32_t>(f32_to_bf16(r[1])) << 16);
-      w.y = f32_to_bf16(r[2]) | (static_cast<uint32_t>(f32_to_bf16(r[3])) << 16);
-      *reinterpret_cast<uint2*>(ap + 16 * dt) = w;
-    }
-    if (quad == 0) p.lse_cache[drow * Hq + h] = (p.sink_mode == 0 && p.F > 0) ? -INFINITY : c.lse;
-    // pre-RoPE query row and the NaN marker of the unknown post-RoPE row (PREFILL:251-262)
-    const uint16_t* sq = p.src_q + (grow * Hq + h) * kHeadDim;
-    uint16_t* dq = p.q_cache + (drow * Hq + h) * kHeadDim;
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-      *reinterpret_cast<uint4*>(dq + 8 * (4 * s + quad)) = *reinterpret_cast<const uint4*>(sq + 8 * (4 * s + quad));
-    if (p.q_post_cache != nullptr) {
-      uint16_t* pq = p.q_post_cache + (drow * Hq + h) * kHeadDim;
-      const uint4 nan4 = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) *reinterpret_cast<uint4*>(pq + 8 * (4 * s + quad)) = nan4;
-    }
-  }
-}
-
-// Plain sliding-window attention (the windowed FlashInfer pass) for GQA
-// groups of any size.  A workgroup takes 16 consecutive query rows of one
+// Sliding-window attention for GQA groups of any size: the windowed
+// FlashInfer pass (kRectify false) or the fused rectification of the rows
+// the ring keeps (kRectify true: a window of S keys, optionally the front
+// sink [0, min(F, E)) as a second key segment, P fed to the PV product as
+// bf16 hi + lo, and the downdate and ring write as epilogue).  A workgroup takes 16 consecutive query rows of one
 // request and 4 * HPW query heads of one KV head (HPW heads per wave), so
 // every 32-key K/V tile it stages in LDS serves 16 rows x 4 HPW heads.  Per
 // wave and block:
@@ -494,8 +221,8 @@ __global__ void __launch_bounds__(256) rectify_kernel(WindowParams p) {
 
 constexpr int kVRow = 18;  // 16-byte units per staged V row: 256 bytes + 32 of padding
 
-template <int HPW>
-__global__ void __launch_bounds__(256, 2) window_plain_kernel(WindowParams p) {
+template <int HPW, bool kRectify>
+__global__ void __launch_bounds__(256, 2) window_kernel(WindowParams p) {
   __shared__ int s_boff[kMaxB + 1];
   __shared__ int s_part[256];
   __shared__ uint4 s_k[2][kBlk * 16];  // K rows of a 32-key block (swizzled)
@@ -513,7 +240,7 @@ __global__ void __launch_bounds__(256, 2) window_plain_kernel(WindowParams p) {
   const int per = ceil_div(B, 256);
   {
     int sum = 0;
-    for (int b = tid * per; b < min(B, (tid + 1) * per); ++b) sum += ceil_div(request_rows<false>(p, b), kRows);
+    for (int b = tid * per; b < min(B, (tid + 1) * per); ++b) sum += ceil_div(request_rows<kRectify>(p, b), kRows);
     s_part[tid] = sum;
     __syncthreads();
     for (int off = 1; off < 256; off <<= 1) {  // inclusive Hillis-Steele scan
@@ -525,7 +252,7 @@ __global__ void __launch_bounds__(256, 2) window_plain_kernel(WindowParams p) {
     int acc = tid > 0 ? s_part[tid - 1] : 0;
     for (int b = tid * per; b < min(B, (tid + 1) * per); ++b) {
       s_boff[b] = acc;
-      acc += ceil_div(request_rows<false>(p, b), kRows);
+      acc += ceil_div(request_rows<kRectify>(p, b), kRows);
     }
     if (tid == 255) s_boff[B] = s_part[255];
     __syncthreads();
@@ -537,6 +264,9 @@ __global__ void __launch_bounds__(256, 2) window_plain_kernel(WindowParams p) {
   const int total_tasks = s_boff[B] * Hkv * nchunks;
   const int64_t kv_stride = static_cast<int64_t>(Hkv) * kHeadDim;
   const unsigned pool_rows = static_cast<unsigned>(min(p.pool_tokens, static_cast<int64_t>(INT_MAX)));
+  // keys [pos - wl, pos] form a row's window (wl < 0: [0, pos])
+  const int wl = kRectify ? p.S - 1 : p.window_left;
+  const bool sink = kRectify && p.sink_mode == 1 && p.F > 0;  // the front sink [0, min(F, E)) as well
   // loader side: thread t stages 16-byte chunk t%16 of keys 2 (t/16) and 2 (t/16) + 1
   const int ld_key = 2 * (tid >> 4), ld_chunk = tid & 15;
   const int ld_pk0 = ld_key * 16 + (ld_chunk ^ (4 * ((ld_key >> 3) & 3) + (ld_key & 3)));
@@ -575,16 +305,15 @@ __global__ void __launch_bounds__(256, 2) window_plain_kernel(WindowParams p) {
     const int len = p.qo_indptr[b + 1] - p.qo_indptr[b];
     const int kvlen = p.kv_indptr[b + 1] - p.kv_indptr[b];
     const int64_t kv_begin = p.kv_indptr[b];
-    const int r_local = kRows * (blk - s_boff[b]);
+    const int r_local = first_row<kRectify>(len, p.M) + kRows * (blk - s_boff[b]);
     const int nrows = min(kRows, len - r_local);
     const int pos0 = kvlen - len + r_local;
     const int pos_last = pos0 + nrows - 1;
     const bool row_ok = col < nrows;
     const int pos = pos0 + col;  // this lane's row position
     const int64_t grow = static_cast<int64_t>(p.qo_indptr[b]) + r_local + (row_ok ? col : 0);
-    const int w_lo = p.window_left < 0 ? 0 : max(pos - p.window_left, 0);  // this row's keys [w_lo, pos]
-    const int seg_lo = p.window_left < 0 ? 0 : max(pos0 - p.window_left, 0);
-    const int seg_hi = pos_last + 1;
+    const int w_lo = wl < 0 ? 0 : max(pos - wl, 0);  // this row's window [w_lo, pos]
+    const int nheads = __builtin_amdgcn_readfirstlane(max(0, min(HPW, G - hg0)));  // heads this wave computes
 
     // Q rows of the wave's heads (B operands): lane (quad, col) holds
     // Q[row col][8 (4s + quad) .. +8]; rows of absent heads are zero
@@ -601,7 +330,6 @@ __global__ void __launch_bounds__(256, 2) window_plain_kernel(WindowParams p) {
         qreg[i][s] = w;
       }
     }
-    const int nheads = __builtin_amdgcn_readfirstlane(max(0, min(HPW, G - hg0)));  // heads this wave computes
 
     float m[HPW], l[HPW];
     f32x4_t acc[HPW][8];
@@ -615,165 +343,240 @@ __global__ void __launch_bounds__(256, 2) window_plain_kernel(WindowParams p) {
 
     const uint16_t* kbase = p.k + static_cast<int64_t>(hkv) * kHeadDim + ld_chunk * 8;
     const uint16_t* vbase = p.v + static_cast<int64_t>(hkv) * kHeadDim + ld_chunk * 8;
-    const int nblk = seg_hi > seg_lo ? ceil_div(seg_hi - seg_lo, kBlk) : 0;
-    // The loader's key ld_key + t of block i: its kv_indices entry (the load
-    // only, index clamped into the request) and, checked later, its pool row
-    // (-1: masked).  An index is loaded one block before it is checked, so
-    // the wait for it never includes K/V loads issued after it (the memory
-    // counter retires in order).
-    auto index_of = [&](int i, int t) -> int {
-      const int key = seg_lo + i * kBlk + ld_key + t;
-      return p.kv_indices[kv_begin + min(key, kvlen - 1)];
-    };
-    auto row_of = [&](int i, int t, int raw) -> int {
-      const int key = seg_lo + i * kBlk + ld_key + t;
-      return (key < seg_hi && static_cast<unsigned>(raw) < pool_rows) ? raw : -1;
-    };
-    auto ld = [&](const uint16_t* base, int r) -> uint4 {
-      return *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(max(r, 0)) * kv_stride);
-    };
-    // the loader's K/V chunks of the block in flight (rc0/rc1: their rows)
-    // and the raw indices of the block after it
-    int rc0 = -1, rc1 = -1, rn0 = 0, rn1 = 0;
-    uint4 kq0 = make_uint4(0, 0, 0, 0), kq1 = kq0, vq0 = kq0, vq1 = kq0;
-    if (nblk > 0) {
-      rc0 = row_of(0, 0, index_of(0, 0));
-      rc1 = row_of(0, 1, index_of(0, 1));
-      kq0 = ld(kbase, rc0);
-      kq1 = ld(kbase, rc1);
-      vq0 = ld(vbase, rc0);
-      vq1 = ld(vbase, rc1);
-      rn0 = index_of(1, 0);
-      rn1 = index_of(1, 1);
-    }
-    for (int i = 0; i < nblk; ++i) {
-      const int buf = i & 1;
-      // stage block i: K and V rows (V of masked keys zeroed), key validity bits
-      {
-        s_k[buf][ld_pk0] = kq0;
-        s_k[buf][ld_pk1] = kq1;
-        s_v[buf][ld_pv0] = rc0 >= 0 ? vq0 : make_uint4(0, 0, 0, 0);
-        s_v[buf][ld_pv1] = rc1 >= 0 ? vq1 : make_uint4(0, 0, 0, 0);
-        const uint64_t b0 = __ballot(rc0 >= 0), b1 = __ballot(rc1 >= 0);
-        if (lane == 0) {
-          // lanes 16 r hold keys 8 wave + 2 r and 8 wave + 2 r + 1
-          uint32_t bits = 0;
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            bits |= static_cast<uint32_t>(((b0 >> (16 * r)) & 1) | (((b1 >> (16 * r)) & 1) << 1)) << (2 * r);
-          s_okw[buf][wave] = bits;
-        }
-      }
-      __syncthreads();  // block i visible; every wave is done with block i - 2 (same buffer)
-      // block i + 1 in flight while block i is computed
-      if (i + 1 < nblk) {
-        rc0 = row_of(i + 1, 0, rn0);
-        rc1 = row_of(i + 1, 1, rn1);
+    // segment 0: the front sink [0, min(F, w_lo)) of each row (fused form,
+    // sink_mode 1); segment 1: the window [w_lo, pos]
+    for (int seg = sink ? 0 : 1; seg < 2; ++seg) {
+      const int seg_lo = seg == 0 ? 0 : (wl < 0 ? 0 : max(pos0 - wl, 0));
+      const int seg_hi = seg == 0 ? min(p.F, max(pos_last - wl, 0)) : pos_last + 1;
+      const int r_lo = seg == 0 ? 0 : w_lo;  // this row's keys in the segment: [r_lo, r_hi)
+      const int r_hi = seg == 0 ? min(p.F, w_lo) : pos + 1;
+      const int nblk = seg_hi > seg_lo ? ceil_div(seg_hi - seg_lo, kBlk) : 0;
+      // The loader's key ld_key + t of block i: its kv_indices entry (the load
+      // only, index clamped into the request) and, checked later, its pool row
+      // (-1: masked).  An index is loaded one block before it is checked, so
+      // the wait for it never includes K/V loads issued after it (the memory
+      // counter retires in order).
+      auto index_of = [&](int i, int t) -> int {
+        const int key = seg_lo + i * kBlk + ld_key + t;
+        return p.kv_indices[kv_begin + min(key, kvlen - 1)];
+      };
+      auto row_of = [&](int i, int t, int raw) -> int {
+        const int key = seg_lo + i * kBlk + ld_key + t;
+        return (key < seg_hi && static_cast<unsigned>(raw) < pool_rows) ? raw : -1;
+      };
+      auto ld = [&](const uint16_t* base, int r) -> uint4 {
+        return *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(max(r, 0)) * kv_stride);
+      };
+      // the loader's K/V chunks of the block in flight (rc0/rc1: their rows)
+      // and the raw indices of the block after it
+      int rc0 = -1, rc1 = -1, rn0 = 0, rn1 = 0;
+      uint4 kq0 = make_uint4(0, 0, 0, 0), kq1 = kq0, vq0 = kq0, vq1 = kq0;
+      if (nblk > 0) {
+        rc0 = row_of(0, 0, index_of(0, 0));
+        rc1 = row_of(0, 1, index_of(0, 1));
         kq0 = ld(kbase, rc0);
         kq1 = ld(kbase, rc1);
         vq0 = ld(vbase, rc0);
         vq1 = ld(vbase, rc1);
-        rn0 = index_of(i + 2, 0);  // clamped: harmless past the last block
-        rn1 = index_of(i + 2, 1);
+        rn0 = index_of(1, 0);
+        rn1 = index_of(1, 1);
       }
-      if (nheads == 0) continue;
-      const int base = seg_lo + i * kBlk;
+      for (int i = 0; i < nblk; ++i) {
+        const int buf = i & 1;
+        // stage block i: K and V rows (V of masked keys zeroed), key validity bits
+        {
+          s_k[buf][ld_pk0] = kq0;
+          s_k[buf][ld_pk1] = kq1;
+          s_v[buf][ld_pv0] = rc0 >= 0 ? vq0 : make_uint4(0, 0, 0, 0);
+          s_v[buf][ld_pv1] = rc1 >= 0 ? vq1 : make_uint4(0, 0, 0, 0);
+          const uint64_t b0 = __ballot(rc0 >= 0), b1 = __ballot(rc1 >= 0);
+          if (lane == 0) {
+            // lanes 16 r hold keys 8 wave + 2 r and 8 wave + 2 r + 1
+            uint32_t bits = 0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              bits |= static_cast<uint32_t>(((b0 >> (16 * r)) & 1) | (((b1 >> (16 * r)) & 1) << 1)) << (2 * r);
+            s_okw[buf][wave] = bits;
+          }
+        }
+        __syncthreads();  // block i visible; every wave is done with block i - 2 (same buffer)
+        // block i + 1 in flight while block i is computed
+        if (i + 1 < nblk) {
+          rc0 = row_of(i + 1, 0, rn0);
+          rc1 = row_of(i + 1, 1, rn1);
+          kq0 = ld(kbase, rc0);
+          kq1 = ld(kbase, rc1);
+          vq0 = ld(vbase, rc0);
+          vq1 = ld(vbase, rc1);
+          rn0 = index_of(i + 2, 0);  // clamped: harmless past the last block
+          rn1 = index_of(i + 2, 1);
+        }
+        if (nheads == 0) continue;
+        const int base = seg_lo + i * kBlk;
 
-      // K A operands of both score tiles (row m = 4a + i <-> key 8a + 4t + i)
-      // and V A operands of the eight 16-dim tiles, all issued up front
-      uint4 ka[2][4];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int s = 0; s < 4; ++s) ka[t][s] = s_k[buf][pk[t][s]];
-      const uint16_t* vtile = reinterpret_cast<const uint16_t*>(&s_v[buf][0]);
-      bf16x8_t va[8];
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-        va[dt] = __builtin_shufflevector(lds_read_tr16(vtile + pv[0] + 16 * dt), lds_read_tr16(vtile + pv[1] + 16 * dt),
-                                         0, 1, 2, 3, 4, 5, 6, 7);
-      // mask of the lane's keys 8 quad + e: a pool row, and inside [w_lo, pos]
-      uint32_t kmask = s_okw[buf][quad];
-      {
-        const int k0 = base + 8 * quad;
-        const int lo_e = min(max(w_lo - k0, 0), 8), hi_e = min(max(pos + 1 - k0, 0), 8);
-        kmask &= ((1u << hi_e) - 1u) & ~((1u << lo_e) - 1u);
-        if (!row_ok) kmask = 0;
-      }
-      // blocks inside every row's window with every key present need no masks
-      const bool full = !__any(kmask != 0xffu);
-      // raw scores of both tiles and every head, the four accumulation chains
-      // interleaved (an absent head has zero Q rows and is never stored)
-      f32x4_t c4[HPW][2];
-#pragma unroll
-      for (int h = 0; h < HPW; ++h)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) c4[h][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
+        // K A operands of both score tiles (row m = 4a + i <-> key 8a + 4t + i)
+        // and V A operands of the eight 16-dim tiles, all issued up front
+        uint4 ka[2][4];
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int h = 0; h < HPW; ++h)
-            c4[h][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[t][s]), as_bf16x8(qreg[h][s]), c4[h][t],
-                                                              0, 0, 0);
-      bf16x8_t pb[HPW];
+          for (int s = 0; s < 4; ++s) ka[t][s] = s_k[buf][pk[t][s]];
+        const uint16_t* vtile = reinterpret_cast<const uint16_t*>(&s_v[buf][0]);
+        bf16x8_t va[8];
 #pragma unroll
-      for (int h = 0; h < HPW; ++h) {
-        // the softmax scale is applied inside exp2: m[h] is a raw score,
-        // p = 2^(q_scale (s - m))
-        float sv[8];
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) sv[4 * t + r] = c4[h][t][r];
-        if (!full) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) sv[e] = ((kmask >> e) & 1) ? sv[e] : -INFINITY;
+        for (int dt = 0; dt < 8; ++dt)
+          va[dt] = __builtin_shufflevector(lds_read_tr16(vtile + pv[0] + 16 * dt), lds_read_tr16(vtile + pv[1] + 16 * dt),
+                                           0, 1, 2, 3, 4, 5, 6, 7);
+        // mask of the lane's keys 8 quad + e: a pool row, and inside [r_lo, r_hi)
+        uint32_t kmask = s_okw[buf][quad];
+        {
+          const int k0 = base + 8 * quad;
+          const int lo_e = min(max(r_lo - k0, 0), 8), hi_e = min(max(r_hi - k0, 0), 8);
+          kmask &= ((1u << hi_e) - 1u) & ~((1u << lo_e) - 1u);
+          if (!row_ok) kmask = 0;
         }
-        float bmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-        bmax = quad_max(bmax);
-        // lazy move of the reference point: p <= 2^8 stays exact in fp32
-        if (__any(bmax * p.q_scale > m[h] * p.q_scale + 8.0f)) {
-          const float m_new = fmaxf(m[h], bmax);
-          const float alpha = fast_exp2((m[h] - m_new) * p.q_scale);
-          m[h] = m_new;
-          l[h] *= alpha;
+        // blocks inside every row's range with every key present need no masks
+        const bool full = !__any(kmask != 0xffu);
+        // raw scores of both tiles and every head, the four accumulation chains
+        // interleaved (an absent head has zero Q rows and is never stored)
+        f32x4_t c4[HPW][2];
 #pragma unroll
-          for (int dt = 0; dt < 8; ++dt) acc[h][dt] *= alpha;
-        }
-        const float mo = -m[h] * p.q_scale;
-        float psum = 0.0f;
+        for (int h = 0; h < HPW; ++h)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float pe = fast_exp2(fmaf(sv[e], p.q_scale, mo));
-          psum += pe;
-          pb[h][e] = static_cast<__bf16>(pe);
+          for (int t = 0; t < 2; ++t) c4[h][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int h = 0; h < HPW; ++h)
+              c4[h][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[t][s]), as_bf16x8(qreg[h][s]), c4[h][t],
+                                                                0, 0, 0);
+        bf16x8_t pb[HPW], pl[HPW];
+#pragma unroll
+        for (int h = 0; h < HPW; ++h) {
+          // the softmax scale is applied inside exp2: m[h] is a raw score,
+          // p = 2^(q_scale (s - m))
+          float sv[8];
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sv[4 * t + r] = c4[h][t][r];
+          if (!full) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sv[e] = ((kmask >> e) & 1) ? sv[e] : -INFINITY;
+          }
+          float bmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+          bmax = quad_max(bmax);
+          // lazy move of the reference point: p <= 2^8 stays exact in fp32
+          if (__any(bmax * p.q_scale > m[h] * p.q_scale + 8.0f)) {
+            const float m_new = fmaxf(m[h], bmax);
+            const float alpha = fast_exp2((m[h] - m_new) * p.q_scale);
+            m[h] = m_new;
+            l[h] *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) acc[h][dt] *= alpha;
+          }
+          const float mo = -m[h] * p.q_scale;
+          float psum = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float pe = fast_exp2(fmaf(sv[e], p.q_scale, mo));
+            psum += pe;
+            pb[h][e] = static_cast<__bf16>(pe);
+            // The fused form also feeds the bf16 rounding residual of P
+            // through a second MFMA (P = hi + lo, ~16 significant bits): the
+            // downdate divides the window's contribution by the prefix's
+            // share of the softmax mass, which amplifies any error of the
+            // window state.
+            if (kRectify) pl[h][e] = static_cast<__bf16>(pe - static_cast<float>(pb[h][e]));
+          }
+          l[h] += psum;
         }
-        l[h] += psum;
+        // O^T += V^T P^T
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+          for (int h = 0; h < HPW; ++h) {
+            acc[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], pb[h], acc[h][dt], 0, 0, 0);
+            if (kRectify) acc[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], pl[h], acc[h][dt], 0, 0, 0);
+          }
       }
-      // O^T += V^T P^T
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-        for (int h = 0; h < HPW; ++h) acc[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], pb[h], acc[h][dt], 0, 0, 0);
+      if (seg == 0) __syncthreads();  // the sink's last tiles are read before the window stages into them
     }
     if (nheads == 0 || !row_ok) continue;
+
+    if (!kRectify) {
 #pragma unroll
-    for (int h = 0; h < HPW; ++h) {
-      if (h >= nheads) break;
-      const float lt = quad_sum(l[h]);
+      for (int h = 0; h < HPW; ++h) {
+        if (h >= nheads) break;
+        const float lt = quad_sum(l[h]);
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        const int hq = hkv * G + hg0 + h;
+        uint16_t* op = p.out + (grow * Hq + hq) * kHeadDim + 4 * quad;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          uint2 w;
+          w.x = f32_to_bf16(acc[h][dt][0] * inv) | (static_cast<uint32_t>(f32_to_bf16(acc[h][dt][1] * inv)) << 16);
+          w.y = f32_to_bf16(acc[h][dt][2] * inv) | (static_cast<uint32_t>(f32_to_bf16(acc[h][dt][3] * inv)) << 16);
+          *reinterpret_cast<uint2*>(op + 16 * dt) = w;
+        }
+        if (quad == 0) p.out_lse[grow * Hq + hq] = lt > 0.0f ? (m[h] * p.q_scale + fast_log2(lt)) * kLn2 : -INFINITY;
+      }
+      continue;
+    }
+
+    // ---- fused: downdate the full state, store the ring row ----
+    const int req = p.req_ids[b];
+    if (req < 0 || req >= p.R) continue;
+    int before = p.rl_by_batch ? p.request_length[b] : p.request_length[req];
+    if (before < 0) before = 0;
+    const int local = r_local + col;  // row index within the request
+    const int slot = static_cast<int>((static_cast<int64_t>(before) + local) % p.M);
+    const int64_t drow = static_cast<int64_t>(req) * p.M + slot;
+    const bool empty = pos + 1 - p.S <= (sink ? p.F : 0);  // nothing left after the downdate
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh) {
+      if (hh >= nheads) break;
+      const int h = hkv * G + hg0 + hh;
+      const float lt = quad_sum(l[hh]);
       const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-      const int hq = hkv * G + hg0 + h;
-      uint16_t* op = p.out + (grow * Hq + hq) * kHeadDim + 4 * quad;
+      const float lse_w = lt > 0.0f ? (m[hh] * p.q_scale + fast_log2(lt)) * kLn2 : -INFINITY;
+      Downdate c;
+      if (empty) {
+        c.lse = -INFINITY;
+        c.t = 0.0f;
+        c.scale = 0.0f;
+      } else {
+        c = downdate_control(p.lse_full[grow * Hq + h], lse_w);
+      }
+      const uint16_t* of = p.o_full + (grow * Hq + h) * kHeadDim + 4 * quad;
+      uint16_t* ap = p.attn_cache + (drow * Hq + h) * kHeadDim + 4 * quad;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
+        const uint2 f = *reinterpret_cast<const uint2*>(of + 16 * dt);
+        float r[4];
+        const float fo[4] = {bf16_lo(f.x), bf16_hi(f.x), bf16_lo(f.y), bf16_hi(f.y)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = empty ? 0.0f : (fo[i] - c.t * (acc[hh][dt][i] * inv)) * c.scale;
         uint2 w;
-        w.x = f32_to_bf16(acc[h][dt][0] * inv) | (static_cast<uint32_t>(f32_to_bf16(acc[h][dt][1] * inv)) << 16);
-        w.y = f32_to_bf16(acc[h][dt][2] * inv) | (static_cast<uint32_t>(f32_to_bf16(acc[h][dt][3] * inv)) << 16);
-        *reinterpret_cast<uint2*>(op + 16 * dt) = w;
+        w.x = f32_to_bf16(r[0]) | (static_cast<uint32_t>(f32_to_bf16(r[1])) << 16);
+        w.y = f32_to_bf16(r[2]) | (static_cast<uint32_t>(f32_to_bf16(r[3])) << 16);
+        *reinterpret_cast<uint2*>(ap + 16 * dt) = w;
       }
-      if (quad == 0) p.out_lse[grow * Hq + hq] = lt > 0.0f ? (m[h] * p.q_scale + fast_log2(lt)) * kLn2 : -INFINITY;
+      if (quad == 0) p.lse_cache[drow * Hq + h] = (p.sink_mode == 0 && p.F > 0) ? -INFINITY : c.lse;
+      // pre-RoPE query row and the NaN marker of the unknown post-RoPE row (PREFILL:251-262)
+      const uint16_t* sq = p.src_q + (grow * Hq + h) * kHeadDim;
+      uint16_t* dq = p.q_cache + (drow * Hq + h) * kHeadDim;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        *reinterpret_cast<uint4*>(dq + 8 * (4 * s + quad)) = *reinterpret_cast<const uint4*>(sq + 8 * (4 * s + quad));
+      if (p.q_post_cache != nullptr) {
+        uint16_t* pq = p.q_post_cache + (drow * Hq + h) * kHeadDim;
+        const uint4 nan4 = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) *reinterpret_cast<uint4*>(pq + 8 * (4 * s + quad)) = nan4;
+      }
     }
   }
 }
@@ -803,6 +606,22 @@ int grid_for(int64_t tasks, const void* kernel) {
   }
   const int64_t wgs = (tasks + 3) / 4;
   return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(wgs, static_cast<int64_t>(cus) * per_cu)));
+}
+
+// Launches the window kernel over `blocks` (a bound on the 16-row blocks of
+// the batch): two query heads per wave when the GQA group has more than four.
+template <bool kRectify>
+void launch_window(const WindowParams& p, int64_t blocks, hipStream_t stream) {
+  const int G = p.Hq / p.Hkv;
+  if (G <= 4) {
+    const void* kern = reinterpret_cast<const void*>(&window_kernel<1, kRectify>);
+    hipLaunchKernelGGL((window_kernel<1, kRectify>), dim3(grid_for(4 * blocks * p.Hkv * ceil_div(G, 4), kern)), dim3(256),
+                       0, stream, p);
+  } else {
+    const void* kern = reinterpret_cast<const void*>(&window_kernel<2, kRectify>);
+    hipLaunchKernelGGL((window_kernel<2, kRectify>), dim3(grid_for(4 * blocks * p.Hkv * ceil_div(G, 8), kern)), dim3(256),
+                       0, stream, p);
+  }
 }
 
 }  // namespace
@@ -882,15 +701,7 @@ extern "C" int mac_prefill_window_attention_bf16(const MacWindowAttentionArgs* a
   p.window_left = a->window_left;
   p.q_scale = static_cast<float>(a->sm_scale * 1.4426950408889634);
   const int64_t blocks = (a->total_q + kRows - 1) / kRows + a->B;
-  const int G = a->Hq / a->Hkv;
-  const void* kern = G <= 4 ? reinterpret_cast<const void*>(&window_plain_kernel<1>)
-                            : reinterpret_cast<const void*>(&window_plain_kernel<2>);
-  const int heads_per_task = G <= 4 ? 4 : 8;
-  const int grid = grid_for(4 * blocks * a->Hkv * ceil_div(G, heads_per_task), kern);
-  if (G <= 4)
-    hipLaunchKernelGGL(window_plain_kernel<1>, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), p);
-  else
-    hipLaunchKernelGGL(window_plain_kernel<2>, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), p);
+  launch_window<false>(p, blocks, static_cast<hipStream_t>(stream));
   HIP_OK(hipGetLastError());
   return MAC_OK;
 }
@@ -946,7 +757,7 @@ extern "C" int mac_prefill_rectify_update_cache_bf16(const MacRectifyArgs* a, vo
   const int64_t kept = std::min<int64_t>(a->total_q, static_cast<int64_t>(a->B) * a->M);
   const int64_t blocks = (kept + kRows - 1) / kRows + a->B;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(rectify_kernel, dim3(grid_for(4 * blocks * a->Hkv * ceil_div(a->Hq / a->Hkv, 4), reinterpret_cast<const void*>(&rectify_kernel))), dim3(256), 0, s, p);
+  launch_window<true>(p, blocks, s);
   HIP_OK(hipGetLastError());
   if (!p.rl_by_batch) {
     hipLaunchKernelGGL(bump_kernel, dim3((a->B + 255) / 256), dim3(256), 0, s, a->request_length, a->req_ids,
