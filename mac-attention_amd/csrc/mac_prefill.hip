@@ -223,7 +223,12 @@ constexpr int kVRow = 18;  // 16-byte units per staged V row: 256 bytes + 32 of 
 
 template <int HPW, bool kRectify>
 __global__ void __launch_bounds__(256, 2) window_kernel(WindowParams p) {
-  __shared__ int s_boff[kMaxB + 1];
+  // dynamic: s_boff[B + 1] row-block offsets, s_qo[B + 1] / s_kv[B + 1] the
+  // request offsets (copies of qo_indptr / kv_indptr)
+  extern __shared__ int s_dyn[];
+  int* s_boff = s_dyn;
+  int* s_qo = s_dyn + (p.B + 1);
+  int* s_kv = s_dyn + 2 * (p.B + 1);
   __shared__ int s_part[256];
   __shared__ uint4 s_k[2][kBlk * 16];  // K rows of a 32-key block (swizzled)
   __shared__ uint4 s_v[2][kBlk * kVRow];  // V rows of the block (padded rows)
@@ -240,7 +245,15 @@ __global__ void __launch_bounds__(256, 2) window_kernel(WindowParams p) {
   const int per = ceil_div(B, 256);
   {
     int sum = 0;
-    for (int b = tid * per; b < min(B, (tid + 1) * per); ++b) sum += ceil_div(request_rows<kRectify>(p, b), kRows);
+    for (int b = tid * per; b < min(B, (tid + 1) * per); ++b) {
+      const int n = ceil_div(request_rows<kRectify>(p, b), kRows);
+      s_boff[b] = n;  // the count until the prefix replaces it below
+      sum += n;
+    }
+    for (int b = tid; b <= B; b += 256) {
+      s_qo[b] = p.qo_indptr[b];
+      s_kv[b] = p.kv_indptr[b];
+    }
     s_part[tid] = sum;
     __syncthreads();
     for (int off = 1; off < 256; off <<= 1) {  // inclusive Hillis-Steele scan
@@ -251,8 +264,9 @@ __global__ void __launch_bounds__(256, 2) window_kernel(WindowParams p) {
     }
     int acc = tid > 0 ? s_part[tid - 1] : 0;
     for (int b = tid * per; b < min(B, (tid + 1) * per); ++b) {
+      const int n = s_boff[b];
       s_boff[b] = acc;
-      acc += ceil_div(request_rows<kRectify>(p, b), kRows);
+      acc += n;
     }
     if (tid == 255) s_boff[B] = s_part[255];
     __syncthreads();
@@ -302,17 +316,28 @@ __global__ void __launch_bounds__(256, 2) window_kernel(WindowParams p) {
       else hi = mid - 1;
     }
     const int b = lo;
-    const int len = p.qo_indptr[b + 1] - p.qo_indptr[b];
-    const int kvlen = p.kv_indptr[b + 1] - p.kv_indptr[b];
-    const int64_t kv_begin = p.kv_indptr[b];
+    const int len = s_qo[b + 1] - s_qo[b];
+    const int kvlen = s_kv[b + 1] - s_kv[b];
+    const int64_t kv_begin = s_kv[b];
     const int r_local = first_row<kRectify>(len, p.M) + kRows * (blk - s_boff[b]);
     const int nrows = min(kRows, len - r_local);
     const int pos0 = kvlen - len + r_local;
     const int pos_last = pos0 + nrows - 1;
     const bool row_ok = col < nrows;
     const int pos = pos0 + col;  // this lane's row position
-    const int64_t grow = static_cast<int64_t>(p.qo_indptr[b]) + r_local + (row_ok ? col : 0);
+    const int64_t grow = static_cast<int64_t>(s_qo[b]) + r_local + (row_ok ? col : 0);
     const int w_lo = wl < 0 ? 0 : max(pos - wl, 0);  // this row's window [w_lo, pos]
+    // fused form: the epilogue's inputs that do not depend on the attention,
+    // loaded now so that their latency hides behind it
+    int req = 0, before = 0;
+    float lse_full[HPW];
+    if (kRectify) {
+      req = p.req_ids[b];
+      const bool req_ok = req >= 0 && req < p.R;
+      before = p.rl_by_batch ? p.request_length[b] : p.request_length[req_ok ? req : 0];
+#pragma unroll
+      for (int i = 0; i < HPW; ++i) lse_full[i] = p.lse_full[grow * Hq + hkv * G + min(hg0 + i, G - 1)];
+    }
     const int nheads = __builtin_amdgcn_readfirstlane(max(0, min(HPW, G - hg0)));  // heads this wave computes
 
     // Q rows of the wave's heads (B operands): lane (quad, col) holds
@@ -527,9 +552,7 @@ __global__ void __launch_bounds__(256, 2) window_kernel(WindowParams p) {
     }
 
     // ---- fused: downdate the full state, store the ring row ----
-    const int req = p.req_ids[b];
     if (req < 0 || req >= p.R) continue;
-    int before = p.rl_by_batch ? p.request_length[b] : p.request_length[req];
     if (before < 0) before = 0;
     const int local = r_local + col;  // row index within the request
     const int slot = static_cast<int>((static_cast<int64_t>(before) + local) % p.M);
@@ -548,7 +571,7 @@ __global__ void __launch_bounds__(256, 2) window_kernel(WindowParams p) {
         c.t = 0.0f;
         c.scale = 0.0f;
       } else {
-        c = downdate_control(p.lse_full[grow * Hq + h], lse_w);
+        c = downdate_control(lse_full[hh], lse_w);
       }
       const uint16_t* of = p.o_full + (grow * Hq + h) * kHeadDim + 4 * quad;
       uint16_t* ap = p.attn_cache + (drow * Hq + h) * kHeadDim + 4 * quad;
@@ -596,13 +619,13 @@ __global__ void bump_kernel(int32_t* request_length, const int32_t* req_ids, con
 // Workgroups for `tasks` wave-sized units of work (4 per workgroup), at most
 // as many as are resident at once (`kernel`'s occupancy on every CU), since
 // the kernels loop over their tasks.
-int grid_for(int64_t tasks, const void* kernel) {
+int grid_for(int64_t tasks, const void* kernel, size_t dyn_lds = 0) {
   int dev = 0, cus = 256, per_cu = 2;
   if (hipGetDevice(&dev) == hipSuccess) {
     int v = 0;
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
     int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, 256, 0) == hipSuccess && occ > 0) per_cu = occ;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, 256, dyn_lds) == hipSuccess && occ > 0) per_cu = occ;
   }
   const int64_t wgs = (tasks + 3) / 4;
   return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(wgs, static_cast<int64_t>(cus) * per_cu)));
@@ -613,14 +636,15 @@ int grid_for(int64_t tasks, const void* kernel) {
 template <bool kRectify>
 void launch_window(const WindowParams& p, int64_t blocks, hipStream_t stream) {
   const int G = p.Hq / p.Hkv;
+  const size_t lds = 3 * sizeof(int) * (static_cast<size_t>(p.B) + 1);
   if (G <= 4) {
     const void* kern = reinterpret_cast<const void*>(&window_kernel<1, kRectify>);
-    hipLaunchKernelGGL((window_kernel<1, kRectify>), dim3(grid_for(4 * blocks * p.Hkv * ceil_div(G, 4), kern)), dim3(256),
-                       0, stream, p);
+    hipLaunchKernelGGL((window_kernel<1, kRectify>), dim3(grid_for(4 * blocks * p.Hkv * ceil_div(G, 4), kern, lds)),
+                       dim3(256), lds, stream, p);
   } else {
     const void* kern = reinterpret_cast<const void*>(&window_kernel<2, kRectify>);
-    hipLaunchKernelGGL((window_kernel<2, kRectify>), dim3(grid_for(4 * blocks * p.Hkv * ceil_div(G, 8), kern)), dim3(256),
-                       0, stream, p);
+    hipLaunchKernelGGL((window_kernel<2, kRectify>), dim3(grid_for(4 * blocks * p.Hkv * ceil_div(G, 8), kern, lds)),
+                       dim3(256), lds, stream, p);
   }
 }
 

@@ -129,6 +129,26 @@ def test_window_attention_matches_oracle(rect_ext, window_left, hq, hkv):
     np.testing.assert_allclose(lse.cpu().numpy(), el, atol=2e-4, rtol=1e-5)
 
 
+def test_window_attention_many_requests(rect_ext):
+    """4096 requests (the planner's maximum; its per-request tables then take
+    49 KB of LDS), most of them a few rows long, some empty, one long."""
+    rng = np.random.default_rng(12)
+    qo = rng.integers(0, 4, 4096)
+    qo[7] = 300
+    kv = qo + rng.integers(0, 6, 4096)
+    case = syn.prefill_case(qo_lens=qo.tolist(), kv_lens=kv.tolist(), hq=8, hkv=2, seed=12)
+    d = _dev_case(case)
+    out, lse = rect_ext.window_attention_return_lse(d["q"], d["k"], d["v"], d["qo"], d["kv"], d["idx"],
+                                                    40, case.sm_scale)
+    torch.cuda.synchronize()
+    eo, el = orc.window_attention(_bf(case.q), _bf(case.k), _bf(case.v), case.qo_indptr,
+                                  case.kv_indptr, case.kv_indices, window_left=40,
+                                  sm_scale=case.sm_scale)
+    got = bits(_host_bits(out))
+    assert rel_l2(got, bits(eo)) < 1e-2
+    np.testing.assert_allclose(lse.cpu().numpy(), el, atol=2e-4, rtol=1e-5)
+
+
 # ---------------------------------------------------------- rectify ----
 
 
