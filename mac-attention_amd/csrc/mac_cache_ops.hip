@@ -3,8 +3,8 @@
 //  * prefill_update_cache: copies the last min(len, M) prefill rows of each
 //    batch row (pre-RoPE q, prefix attention output, lse) into the request's
 //    ring at (L_before + start + i) % M and bumps request_length
-//    (PREFILL:201-269).  One workgroup per batch row: all its copies read the
-//    same L_before, and the bump happens after the copies were addressed.
+//    (PREFILL:201-269).  One workgroup per kept row; the bump is a second
+//    launch, so every copy of a batch row reads the same L_before.
 //  * mark / invalidate / update_request_state: per-request readiness and
 //    length metadata (PREFILL:271-320).
 
@@ -39,52 +39,82 @@ struct PrefillParams {
   int by_batch;
 };
 
-// Copies `elems` bf16 values; 16-byte vectors when the row allows it.
-__device__ __forceinline__ void copy_row_bf16(uint16_t* dst, const uint16_t* src, int64_t elems,
-                                              bool vec16) {
-  if (vec16) {
-    const int64_t n16 = elems / 8;
-    uint4* d = reinterpret_cast<uint4*>(dst);
-    const uint4* s = reinterpret_cast<const uint4*>(src);
-    for (int64_t i = threadIdx.x; i < n16; i += blockDim.x) d[i] = s[i];
+// Validity of batch row b and its kept rows [start, ni) (PREFILL:201-230):
+// false when it has nothing to copy or names a request or source range
+// outside the buffers.
+__device__ __forceinline__ bool prefill_row(const PrefillParams& p, int b, int& req, int& ni, int& start) {
+  req = p.req_ids[b];
+  ni = p.lens[b];
+  const int off = p.offsets[b];
+  start = ni > p.M ? ni - p.M : 0;
+  return ni > 0 && p.M > 0 && req >= 0 && req < p.R && off >= 0 && off + ni <= p.src_rows;
+}
+
+// Kept row i of batch row b: copies source row
+// offsets[b] + start + i (q and attention output: H * D bf16 each, lse: H
+// floats) to ring slot (L_before + start + i) % M.  Every load of a round is
+// issued before its stores.
+__device__ __forceinline__ void copy_prefill_row(const PrefillParams& p, int b, int i) {
+  int req, ni, start;
+  if (!prefill_row(p, b, req, ni, start) || i >= ni - start) return;
+  int before = p.by_batch ? p.request_length[b] : p.request_length[req];
+  if (before < 0) before = 0;
+  const int dst = static_cast<int>((static_cast<int64_t>(before) + start + i) % p.M);
+  const int64_t drow = static_cast<int64_t>(req) * p.M + dst;
+  const int64_t srow = static_cast<int64_t>(p.offsets[b]) + start + i;
+  const int64_t row = static_cast<int64_t>(p.H) * p.D;
+  const int tid = threadIdx.x;
+  if (row % 8 == 0) {
+    const int64_t n16 = row / 8;
+    const uint4* sq = reinterpret_cast<const uint4*>(p.src_q + srow * row);
+    const uint4* sa = reinterpret_cast<const uint4*>(p.src_attn + srow * row);
+    uint4* dq = reinterpret_cast<uint4*>(p.q_cache + drow * row);
+    uint4* da = reinterpret_cast<uint4*>(p.attn_cache + drow * row);
+    for (int64_t e = tid; e < n16; e += 2 * kThreads) {
+      const bool two = e + kThreads < n16;
+      const uint4 q0 = sq[e], a0 = sa[e];
+      uint4 q1 = q0, a1 = a0;
+      if (two) {
+        q1 = sq[e + kThreads];
+        a1 = sa[e + kThreads];
+      }
+      dq[e] = q0;
+      da[e] = a0;
+      if (two) {
+        dq[e + kThreads] = q1;
+        da[e + kThreads] = a1;
+      }
+    }
   } else {
-    for (int64_t i = threadIdx.x; i < elems; i += blockDim.x) dst[i] = src[i];
+    for (int64_t e = tid; e < row; e += kThreads) {
+      const uint16_t q = p.src_q[srow * row + e], a = p.src_attn[srow * row + e];
+      p.q_cache[drow * row + e] = q;
+      p.attn_cache[drow * row + e] = a;
+    }
+  }
+  for (int h = tid; h < p.H; h += kThreads) p.lse_cache[drow * p.H + h] = p.src_lse[srow * p.H + h];
+  if (p.q_post_cache != nullptr) {
+    // bf16 quiet NaN marks rows whose post-RoPE query is unknown (PREFILL:251-262)
+    uint16_t* qp = p.q_post_cache + drow * row;
+    for (int64_t e = tid; e < row; e += kThreads) qp[e] = 0x7fc0;
   }
 }
 
+// One workgroup per (kept row, batch row).  request_length is bumped
+// afterwards by bump_length_kernel, so every workgroup of a batch row reads
+// the same L_before.
 __global__ void __launch_bounds__(kThreads) prefill_update_cache_kernel(PrefillParams p) {
-  const int b = blockIdx.x;
-  const int req = p.req_ids[b];
-  const int ni = p.lens[b];
-  if (ni <= 0 || p.M <= 0) return;
-  if (req < 0 || req >= p.R) return;
-  const int start = ni > p.M ? ni - p.M : 0;
-  const int keep = ni - start;
-  const int base_off = p.offsets[b];
-  if (base_off < 0 || base_off + ni > p.src_rows) return;
-  int before = p.by_batch ? p.request_length[b] : p.request_length[req];
-  if (before < 0) before = 0;
-  __syncthreads();  // every thread has read request_length before the bump below
+  const int i = blockIdx.x;
+  for (int b = blockIdx.y; b < p.B; b += gridDim.y) copy_prefill_row(p, b, i);
+}
 
-  const int64_t row = static_cast<int64_t>(p.H) * p.D;
-  const bool vec16 = (row % 8) == 0;
-  const int base_dest = static_cast<int>((static_cast<int64_t>(before) + start) % p.M);
-  for (int i = 0; i < keep; ++i) {
-    int dst = base_dest + i;
-    if (dst >= p.M) dst -= p.M;
-    const int64_t drow = static_cast<int64_t>(req) * p.M + dst;
-    const int64_t srow = static_cast<int64_t>(base_off) + start + i;
-    copy_row_bf16(p.q_cache + drow * row, p.src_q + srow * row, row, vec16);
-    copy_row_bf16(p.attn_cache + drow * row, p.src_attn + srow * row, row, vec16);
-    for (int h = threadIdx.x; h < p.H; h += blockDim.x)
-      p.lse_cache[drow * p.H + h] = p.src_lse[srow * p.H + h];
-    if (p.q_post_cache != nullptr) {
-      // bf16 quiet NaN marks rows whose post-RoPE query is unknown (PREFILL:251-262)
-      uint16_t* qp = p.q_post_cache + drow * row;
-      for (int64_t e = threadIdx.x; e < row; e += blockDim.x) qp[e] = 0x7fc0;
-    }
-  }
-  if (!p.by_batch && threadIdx.x == 0) atomicAdd(&p.request_length[req], ni);
+// request_length[req] += lens[b] for the valid batch rows (indexed-by-request
+// form only), after every copy has read the old length.
+__global__ void bump_length_kernel(PrefillParams p) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= p.B) return;
+  int req, ni, start;
+  if (prefill_row(p, b, req, ni, start)) atomicAdd(&p.request_length[req], ni);
 }
 
 __global__ void mark_ready_kernel(uint8_t* ready, int64_t* cache_epoch, const int64_t* request_epoch,
@@ -169,9 +199,13 @@ extern "C" int mac_prefill_update_cache(void* q_cache, void* attn_cache, float* 
   p.B = B;
   p.src_rows = src_rows;
   p.by_batch = request_length_len == B ? 1 : 0;
-  hipLaunchKernelGGL(prefill_update_cache_kernel, dim3(B), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), p);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(prefill_update_cache_kernel, dim3(capacity, B < 65535 ? B : 65535), dim3(kThreads), 0, st, p);
   HIP_OK(hipGetLastError());
+  if (!p.by_batch) {
+    hipLaunchKernelGGL(bump_length_kernel, dim3((B + kThreads - 1) / kThreads), dim3(kThreads), 0, st, p);
+    HIP_OK(hipGetLastError());
+  }
   return MAC_OK;
 }
 
