@@ -271,6 +271,7 @@ def measure_aux(torch):
       prefill_rectify -- the fused op (kept rows only) against the reference's
                          three calls on the GPU (window attention of every row,
                          downdate of every row, mac_prefill_update_cache);
+      prefill_update_cache -- the ring write of the last M rows of every chunk;
       decode_rope     -- fused RoPE + q preserve + KV write for a 64-token decode
                          batch (GQA-4, rotary_dim 128, NeoX)."""
     from mac_attention.integrations.sglang import bridge
@@ -318,6 +319,11 @@ def measure_aux(torch):
 
     fused_us = _time_us(torch, fused, 20)
     comp_us = _time_us(torch, composed, 5)
+    # mac_prefill_update_cache alone (the last M rows of every chunk into the
+    # ring): q and attention rows (2 * Hq * D bf16) + lse read and written per row
+    upd_us = _time_us(torch, lambda: cache.mac_prefill_update_cache(qc, ac, lc, rl[:B], req, src_q, wo, wl, qo, lens,
+                                                                    M, hq, D, empty), 20)
+    upd_bytes = 2 * B * M * hq * (2 * 2 * D + 4)
     # algorithmic bytes of the fused op: per (request, kv head) the K/V rows
     # of the window of the kept rows (M + S - 1 tokens), per kept row and
     # head q_post, src_q, o_full (256 B each) + lse_full read, ring q and o
@@ -328,7 +334,11 @@ def measure_aux(torch):
         "workload": f"B={B} requests x {chunk}-token chunk, GQA-8 (Hq={hq}, Hkv={hkv}), S={S}, ring={M}",
         "fused_us": round(fused_us, 2), "reference_three_calls_us": round(comp_us, 2),
         "speedup": round(comp_us / fused_us, 1), "fused_algorithmic_bytes": fused_bytes,
-        "fused_gbs": round(fused_bytes / fused_us / 1e3, 1)}}
+        "fused_gbs": round(fused_bytes / fused_us / 1e3, 1)},
+        "prefill_update_cache": {
+            "workload": f"B={B} batch rows x {chunk} source rows, ring={M}, Hq={hq}",
+            "us": round(upd_us, 2), "algorithmic_bytes": upd_bytes,
+            "gbs": round(upd_bytes / upd_us / 1e3, 1)}}
     del k, v, q, src_q, o_full, wo
     torch.cuda.empty_cache()
 
