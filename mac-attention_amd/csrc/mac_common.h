@@ -58,6 +58,19 @@ __device__ __forceinline__ bf16x4_t lds_read_tr16(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_t*)(p));
 }
 
+// Maximum of finite or infinite floats (no NaN operands) with the plain
+// v_max3_f32: fmaxf makes the compiler quiet every operand first (an extra
+// v_max per operand) because it cannot rule out signalling NaNs in MFMA
+// results.
+__device__ __forceinline__ float max3_nonan(float a, float b, float c) {
+  float r;
+  asm volatile("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float max8_nonan(const float (&x)[8]) {
+  return max3_nonan(max3_nonan(x[0], x[1], x[2]), max3_nonan(x[3], x[4], x[5]), max3_nonan(x[6], x[7], x[7]));
+}
+
 // Max and sum over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (one column of
 // an MFMA result tile) with gfx950's row-swapping VALU permutes: no LDS
 // round trip, so no wait on the wave's outstanding LDS reads.

@@ -412,8 +412,9 @@ __global__ void __launch_bounds__(256, 2) window_kernel(WindowParams p) {
         {
           s_k[buf][ld_pk0] = kq0;
           s_k[buf][ld_pk1] = kq1;
-          s_v[buf][ld_pv0] = rc0 >= 0 ? vq0 : make_uint4(0, 0, 0, 0);
-          s_v[buf][ld_pv1] = rc1 >= 0 ? vq1 : make_uint4(0, 0, 0, 0);
+          const uint32_t z0 = rc0 >= 0 ? 0xffffffffu : 0u, z1 = rc1 >= 0 ? 0xffffffffu : 0u;
+          s_v[buf][ld_pv0] = make_uint4(vq0.x & z0, vq0.y & z0, vq0.z & z0, vq0.w & z0);
+          s_v[buf][ld_pv1] = make_uint4(vq1.x & z1, vq1.y & z1, vq1.z & z1, vq1.w & z1);
           const uint64_t b0 = __ballot(rc0 >= 0), b1 = __ballot(rc1 >= 0);
           if (lane == 0) {
             // lanes 16 r hold keys 8 wave + 2 r and 8 wave + 2 r + 1
@@ -477,6 +478,14 @@ __global__ void __launch_bounds__(256, 2) window_kernel(WindowParams p) {
             for (int h = 0; h < HPW; ++h)
               c4[h][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[t][s]), as_bf16x8(qreg[h][s]), c4[h][t],
                                                                 0, 0, 0);
+        if (!full) {  // masked keys -> -inf, the lane's eight bits decoded once for all heads
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const bool keep = (kmask >> e) & 1;
+#pragma unroll
+            for (int h = 0; h < HPW; ++h) c4[h][e >> 2][e & 3] = keep ? c4[h][e >> 2][e & 3] : -INFINITY;
+          }
+        }
         bf16x8_t pb[HPW], pl[HPW];
 #pragma unroll
         for (int h = 0; h < HPW; ++h) {
@@ -487,11 +496,7 @@ __global__ void __launch_bounds__(256, 2) window_kernel(WindowParams p) {
           for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) sv[4 * t + r] = c4[h][t][r];
-          if (!full) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) sv[e] = ((kmask >> e) & 1) ? sv[e] : -INFINITY;
-          }
-          float bmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+          float bmax = max8_nonan(sv);
           bmax = quad_max(bmax);
           // lazy move of the reference point: p <= 2^8 stays exact in fp32
           if (__any(bmax * p.q_scale > m[h] * p.q_scale + 8.0f)) {
