@@ -121,6 +121,39 @@ class Step:
             acc = [a + b for a, b in zip(acc, t)]
         return [a / runs for a in acc]
 
+    def scan_bytes(self, past):
+        """Ring-scan bytes.  Rings scanned by the range-split launch (3+
+        ranges of 256 slots) are probed: the first 128 B of every slot in the
+        candidate window, the other 128 B only where the first half's squared
+        distance does not exceed the threshold (+ the kernel's slack), unless
+        MAC_PERSISTENT_MATCH_EARLY_EXIT=0; smaller rings are read in full."""
+        import os
+
+        import numpy as np
+
+        torch = self.torch
+        tiles = -(-self.ring // 32)
+        splits = max(1, min(tiles, -(-self.ring // 256)))
+        probe = splits >= 3 and os.environ.get("MAC_PERSISTENT_MATCH_EARLY_EXIT", "1").strip() != "0"
+        slots = [int(min(self.ring, int(p))) for p in past]
+        if not probe:
+            return int(self.hq * sum(slots)) * 2 * D
+        thr = float(np.float32(2.0 * D * (1.0 - 0.45) ** 2))
+        thr_prune = thr + abs(thr) * 1e-4 + 1e-4
+        evaluated = 0
+        q = self.dev["q_pre"][: self.batch, :, :64].float()
+        req = self.dev["req_ids"][: self.batch].tolist()
+        for n in range(self.batch):
+            m = slots[n]
+            if m == 0:
+                continue
+            first = int(past[n]) - m  # candidate window [P - m, P): slots (P - m .. P - 1) % M
+            idx = torch.arange(first, first + m, device=q.device) % self.ring
+            ring = self.dev["query_cache"][req[n], idx, :, :64].float()
+            d = ((ring - q[n].unsqueeze(0)) ** 2).sum(-1)
+            evaluated += int((d <= thr_prune).sum())
+        return (self.hq * sum(slots) + evaluated) * D
+
     def bytes(self):
         """Algorithmic HBM bytes of one step from the decisions it made."""
         import numpy as np
@@ -137,13 +170,14 @@ class Step:
         kv = int(tokens.sum()) * 2 * 2 * D
         r2t = int(tokens.max(axis=1).sum()) * 4
         ready = not self.exact
-        scan = int(self.hq * np.minimum(self.ring, past).sum()) * 2 * D if ready else 0
+        full_rows = int(self.hq * np.minimum(self.ring, past).sum()) * 2 * D if ready else 0
+        scan = self.scan_bytes(past) if ready else 0
         cached = int(hit.sum()) * (2 * D + 4)
         heads = self.batch * self.hq
         small = heads * (2 * D + 2 * D + 2 * D + 4) + (heads * (2 * D + 2 * D + 2 * D + 4) if ready else 0)
         attn = kv + r2t + heads * 2 * D
         return dict(total=kv + r2t + scan + cached + small, attention_kernel=attn, kv=kv,
-                    ring_scan=scan, hit_heads=int(hit.sum()), heads=heads,
+                    ring_scan=scan, ring_scan_full_rows=full_rows, hit_heads=int(hit.sum()), heads=heads,
                     nonhit_groups=int((mode != 0).sum()), groups=int(mode.size))
 
 
@@ -185,6 +219,7 @@ def measure(torch, step: Step, warmup, steps, phase_runs):
         us_per_step=round(ms * 1e3, 2), wall_us_per_step=round(wall * 1e3, 2),
         phase_us=[round(p * 1e3, 2) for p in phases],
         algorithmic_bytes=b["total"], attention_kernel_bytes=b["attention_kernel"],
+        ring_scan_bytes=b["ring_scan"], ring_scan_full_row_bytes=b["ring_scan_full_rows"],
         achieved_gbs=round(b["total"] / (ms * 1e-3) / 1e9, 1),
         frac_of_peak=round(b["total"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         attention_kernel_gbs=round(b["attention_kernel"] / (phases[1] * 1e-3) / 1e9, 1),

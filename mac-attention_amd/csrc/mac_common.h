@@ -47,6 +47,14 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
+// Sum over the 8 lanes of a DPP half-row; every lane of it receives the total.
+__device__ __forceinline__ float row8_sum(float x) {
+  x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp<0x141>(x);  // row_half_mirror
+  return x;
+}
+
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 // gfx950 transposing LDS read (ds_read_b64_tr_b16).  Every lane passes the
 // address of four consecutive 16-bit elements; in each group of 16 lanes,

@@ -91,6 +91,7 @@ struct DecideParams {
   int32_t* group_mode;
   int32_t* task_counter;  // zeroed here for span_attention's dynamic fetch
   int splits;             // slot ranges of the ring scan (1: scan inside match_decide)
+  int probe;              // range scan: skip the second half of rows whose first half already exceeds thr_dist
   int S, F, gen_min_limit, lookback_right, candidate_mode;
   float thr_dist;
   int mixed_group_fallback;
@@ -212,6 +213,7 @@ __device__ __forceinline__ uint4 load_stream16(const uint16_t* ptr) {
 // in one workgroup per group.
 constexpr int kSplitSlots = 256;
 constexpr int kLsePrefetchSlots = 64;
+constexpr int kProbeSlots = 4;  // probe scan: slot pairs per lane batch and pass
 
 template <int G, int kMode>
 __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
@@ -275,7 +277,107 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
   const int per_split = ceil_div(M, p.splits);
   const int s_lo = kMode == 1 ? static_cast<int>(blockIdx.y) * per_split : 0;
   const int s_hi = kMode == 1 ? min(M, s_lo + per_split) : M;
-  if (kMode != 2) {
+  if (kMode == 1 && p.probe != 0) {
+    // Probe scan (the reference's default, DECODE:1001-1075).  The squared
+    // distance over dims [0, 64) is a lower bound of the full one, so a slot
+    // whose probe exceeds thr_dist (plus a relative slack of 1e-4, far above
+    // the rounding of a 128-term fp32 sum) cannot be a hit and its second
+    // half-row is not fetched; every other slot gets its full distance.
+    // Hit decisions are those of the full scan; only the best distance of a
+    // head without a hit may differ.  Lane (row, c) takes slot 2u + (c >> 3)
+    // of the batch and 16-byte chunk (c & 7) of its first half, then chunk
+    // 8 + (c & 7) -- or, for a pruned slot, its first chunk again, a cache hit
+    // instead of HBM traffic (no divergent loads).
+    constexpr int kProbeBatch = kProbeSlots / kPasses;  // slot pairs per lane batch
+    const int half = c >> 3, cc = c & 7;
+    float qa[kPasses][8], qb[kPasses][8];
+#pragma unroll
+    for (int ps = 0; ps < kPasses; ++ps) {
+      const int hl = min(row + 4 * ps, G - 1);
+      const uint16_t* qp = p.q_pre + (static_cast<int64_t>(n) * Hq + hkv * G + hl) * kHeadDim + cc * 8;
+      unpack8(*reinterpret_cast<const uint4*>(qp), qa[ps]);
+      unpack8(*reinterpret_cast<const uint4*>(qp + 64), qb[ps]);
+    }
+    const float thr_prune = p.thr_dist + fabsf(p.thr_dist) * 1e-4f + 1e-4f;
+    for (int s0 = s_lo + wave; s0 < s_hi; s0 += kWaves * 2 * kProbeBatch) {
+      int pos[kProbeBatch], slot[kProbeBatch];
+      bool in_window[kProbeBatch];
+#pragma unroll
+      for (int u = 0; u < kProbeBatch; ++u) {
+        slot[u] = s0 + (2 * u + half) * kWaves;
+        pos[u] = ring_slot_to_pos(P, M, slot[u]);
+        in_window[u] = eligible && slot[u] < s_hi && pos[u] >= cand_begin && pos[u] < cand_end;
+      }
+      uint4 w[kPasses][kProbeBatch];
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps) {
+        const int hl = min(row + 4 * ps, G - 1);
+#pragma unroll
+        for (int u = 0; u < kProbeBatch; ++u) {
+          const int64_t off = ((cache_req + min(slot[u], s_hi - 1)) * Hq + hkv * G + hl) * kHeadDim + cc * 8;
+          w[ps][u] = *reinterpret_cast<const uint4*>(p.query_cache + off);
+        }
+      }
+      float acc[kPasses][kProbeBatch];
+      bool eval[kPasses][kProbeBatch];
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps)
+#pragma unroll
+        for (int u = 0; u < kProbeBatch; ++u) {
+          float cf[8];
+          unpack8(w[ps][u], cf);
+          float a = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float df = qa[ps][i] - cf[i];
+            a = fmaf(df, df, a);
+          }
+          acc[ps][u] = a;
+          eval[ps][u] = in_window[u] && row + 4 * ps < G && row8_sum(a) <= thr_prune;
+        }
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps) {
+        const int hl = min(row + 4 * ps, G - 1);
+#pragma unroll
+        for (int u = 0; u < kProbeBatch; ++u) {
+          const int64_t off = ((cache_req + min(slot[u], s_hi - 1)) * Hq + hkv * G + hl) * kHeadDim + cc * 8 +
+                              (eval[ps][u] ? 64 : 0);
+          w[ps][u] = load_stream16(p.query_cache + off);
+        }
+      }
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps)
+#pragma unroll
+        for (int u = 0; u < kProbeBatch; ++u) {
+          float cf[8];
+          unpack8(w[ps][u], cf);
+          float b = acc[ps][u];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float df = qb[ps][i] - cf[i];
+            b = fmaf(df, df, b);
+          }
+          const float d = row8_sum(b);
+          if (eval[ps][u] && better_pair(d, pos[u], best_d[ps], best_p[ps])) {
+            best_d[ps] = d;
+            best_p[ps] = pos[u];
+            best_s[ps] = slot[u];
+          }
+        }
+    }
+    // the two half-rows of lanes tracked different slots: lane c takes the
+    // better of its own and lane c ^ 8's
+#pragma unroll
+    for (int ps = 0; ps < kPasses; ++ps) {
+      const float od = __shfl_xor(best_d[ps], 8);
+      const int op = __shfl_xor(best_p[ps], 8), os = __shfl_xor(best_s[ps], 8);
+      if (better_pair(od, op, best_d[ps], best_p[ps])) {
+        best_d[ps] = od;
+        best_p[ps] = op;
+        best_s[ps] = os;
+      }
+    }
+  } else if (kMode != 2) {
     for (int s0 = s_lo + wave; s0 < s_hi; s0 += kWaves * kSlotBatch) {
       // every pass's loads of the batch are in flight before any reduction
       uint4 w[kPasses][kSlotBatch];
@@ -1431,6 +1533,16 @@ int min_chunk() {
   return v;
 }
 
+// MAC_PERSISTENT_MATCH_EARLY_EXIT (the reference's knob, DECODE:5202; read
+// once, default on): probe-pruned ring scan for rings split over ranges.
+int match_probe() {
+  static const int v = [] {
+    const char* e = std::getenv("MAC_PERSISTENT_MATCH_EARLY_EXIT");
+    return (e != nullptr && std::atoi(e) == 0) ? 0 : 1;
+  }();
+  return v;
+}
+
 int attn_impl() {
   static const int impl = [] {
     const char* e = std::getenv("MAC_AMD_ATTN_IMPL");
@@ -1632,6 +1744,7 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   // rings of more than two ranges of kSplitSlots slots are scanned by a
   // separate (group, range) launch, one match tile per range
   dp.splits = std::max(1, std::min(a->max_match_tiles, ceil_div(M, kSplitSlots)));
+  dp.probe = match_probe();
   if (dp.splits < 3) dp.splits = 1;
   dp.S = a->semantic_pos_ahead;
   dp.F = a->front_sink_tokens > 0 ? a->front_sink_tokens : 0;

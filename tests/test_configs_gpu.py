@@ -272,6 +272,52 @@ def test_config4_ragged_serving_mix(ext, cache_ext):
     _check_subset(dev, out2, out_lse2, ws2, sub2, res2, check2, "config4 step2")
 
 
+def _row_with_distance(target):
+    """A bf16 row (as float32) whose squared norm lies within 2e-4 of
+    `target`, all but at most 2e-4 of it in the probed dims [0, 64)."""
+    def bf(x):
+        return float(syn.from_bits(syn.to_bits(np.array([x], np.float32)))[0])
+    r = np.zeros(128, np.float32)
+    a = bf(math.sqrt(0.95 * target / 56.0))
+    r[:56] = a
+    rest = target - 56.0 * a * a
+    for i in range(56, 128):  # the rest greedily with ever smaller values, probed dims first
+        if rest <= 2e-4:
+            break
+        v = bf(math.sqrt(rest))
+        while v * v > rest + 1e-4:  # step down one bf16 ulp at a time
+            v = float(syn.from_bits(syn.to_bits(np.array([v], np.float32)) - 1)[0])
+        r[i] = v
+        rest -= v * v
+    d = float(np.sum(r.astype(np.float64) ** 2))
+    assert abs(d - target) < 2e-4 and d - float(np.sum(r[:64].astype(np.float64) ** 2)) < 2e-4
+    return r
+
+
+def test_probe_scan_keeps_threshold_neighbours(ext):
+    """The range-split ring scan skips the second half-row of a slot whose
+    first-half distance exceeds the threshold.  Entries whose distance sits
+    just below or just above the threshold, almost all of it in the probed
+    dims (the worst case for a lower-bound prune), keep the full scan's
+    decisions: hit at thr (1 - 5e-5) and thr (1 - 1e-3), miss at thr
+    (1 + 5e-5) and 1.01 thr."""
+    b, m, ctx, S = 2, 1024, 5000, 256
+    dev = syn.device_ragged_case(torch, kv_lens=[ctx + 1] * b, hq=32, hkv=8, capacity=m, seed=77)
+    thr = float(np.float32(2.0 * 128 * (1.0 - 0.45) ** 2))
+    pos = ctx - 100
+    slot = pos % m
+    for h, f in enumerate((1 - 5e-5, 1 + 5e-5, 1 - 1e-3, 1.01)):
+        dev["q_pre"][0, h] = 0
+        dev["query_cache"][0, slot, h] = torch.from_numpy(_row_with_distance(thr * f)).to(torch.bfloat16)
+        dev["lse_cache"][0, slot, h] = 5.0
+    sub = host_subset(torch, dev, [0], semantic_pos_ahead=S)
+    res = oracle_run(sub)
+    assert res.head["hit"][0, :4].tolist() == [1, 0, 1, 0]
+    out, out_lse, ws = _run(ext, dev, S=S, F=0, max_context=8192)
+    torch.cuda.synchronize()
+    _check_subset(dev, out, out_lse, ws, sub, res, [0], "probe threshold neighbours")
+
+
 # ------------------------------------------------------------ hipGraph ----
 
 
