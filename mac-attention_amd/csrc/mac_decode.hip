@@ -287,7 +287,8 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
     // head without a hit may differ.  Lane (row, c) takes slot 2u + (c >> 3)
     // of the batch and 16-byte chunk (c & 7) of its first half, then chunk
     // 8 + (c & 7) -- or, for a pruned slot, its first chunk again, a cache hit
-    // instead of HBM traffic (no divergent loads).
+    // instead of HBM traffic (no divergent loads); a batch the whole wave
+    // pruned skips the second round.
     constexpr int kProbeBatch = kProbeSlots / kPasses;  // slot pairs per lane batch
     const int half = c >> 3, cc = c & 7;
     float qa[kPasses][8], qb[kPasses][8];
@@ -335,6 +336,12 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
           acc[ps][u] = a;
           eval[ps][u] = in_window[u] && row + 4 * ps < G && row8_sum(a) <= thr_prune;
         }
+      bool any_eval = false;
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps)
+#pragma unroll
+        for (int u = 0; u < kProbeBatch; ++u) any_eval |= eval[ps][u];
+      if (!__any(any_eval)) continue;  // the whole batch pruned (the common case): no second half-rows
 #pragma unroll
       for (int ps = 0; ps < kPasses; ++ps) {
         const int hl = min(row + 4 * ps, G - 1);
