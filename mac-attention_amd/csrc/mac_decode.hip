@@ -1352,13 +1352,12 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
 // ============================================================ 3. merge ====
 
 // One workgroup per (group, query head); lane l of every wave owns dims
-// 2l, 2l+1.  The partials of a range are split over the four waves (wave w
-// takes j = j0 + w, j0 + w + 4, ..., eight loads in flight at a time), and the
-// four wave states are combined through LDS, so a full-fallback group with
-// hundreds of partials is merged in a fraction of the serial latency.
-// Order per head (DECODE:4280-4685): state <- cached entry (hit heads) (+)
-// band partials -> ring row (ready requests only) -> (+) sink and tail
-// partials -> out / out_lse.  An empty partial (lse = -inf) has weight 0,
+// 2l, 2l+1.  The partials are split over the four waves (eight loads in
+// flight at a time) and loaded in one pass, so a full-fallback group with
+// hundreds of partials is merged in a fraction of the serial latency; the
+// four wave states are combined through LDS.  Per head (DECODE:4280-4685):
+// ring state = cached entry (hit heads) (+) band partials -> ring row (ready
+// requests only); out / out_lse = ring state (+) sink and tail partials.  An empty partial (lse = -inf) has weight 0,
 // the reference's skip rule (DECODE:866-890).
 struct MergeState {
   float lse;   // natural log; -inf = empty
@@ -1410,8 +1409,8 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
   const int n_band = ceil_div(new_end - band_begin, chunk);
   const int n_tail = ceil_div(kv_len - new_end, chunk);
 
-  __shared__ float s_o[kWaves][kHeadDim];
-  __shared__ float s_l[kWaves];
+  __shared__ float s_o[2][kWaves][kHeadDim];
+  __shared__ float s_l[2][kWaves];
 
   auto load_partial = [&](int j, float& lse2, float& o0, float& o1) {
     const int64_t slot = static_cast<int64_t>(g) * p.cap + j;
@@ -1427,9 +1426,27 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
       o1 = v.y;
     }
   };
-  // this wave's share of partials [j0, j1), batched
-  auto merge_range = [&](MergeState& st, int j0, int j1) {
-    for (int jb = j0 + wave; jb < j1; jb += kWaves * kBatch) {
+
+  // One pass over all partials of the group (wave w takes j = w, w + 4, ...,
+  // eight loads in flight at a time): band partials into `ring` (on top of
+  // the cached entry), sink and tail partials into `rest`.
+  MergeState ring{-INFINITY, {0.0f, 0.0f}}, rest{-INFINITY, {0.0f, 0.0f}};
+  const int mslot = p.head_match_slot[ho];
+  if (wave == 0 && p.head_hit[ho] != 0 && mslot >= 0 && req >= 0 && req < p.s.R) {
+    const int64_t rowi = (static_cast<int64_t>(req) * M + mslot) * Hq + hq;
+    const float pl = p.lse_cache[rowi];
+    if (isfinite(pl)) {
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(p.attn_cache + rowi * kHeadDim + d0);
+      ring.lse = pl;
+      ring.o[0] = bf16_lo(w);
+      ring.o[1] = bf16_hi(w);
+    }
+  }
+  // this wave's partials of [j0, j1) into `st`, eight loads in flight; wave
+  // (first + k) % 4 takes j0 + k, so that consecutive ranges continue the
+  // rotation instead of all starting on wave 0
+  auto merge_range = [&](MergeState& st, int j0, int j1, int first) {
+    for (int jb = j0 + ((wave - first) & (kWaves - 1)); jb < j1; jb += kWaves * kBatch) {
       float pl[kBatch], p0[kBatch], p1[kBatch];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
@@ -1441,58 +1458,45 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
       for (int u = 0; u < kBatch; ++u) merge_into(st, pl[u], p0[u], p1[u]);
     }
   };
-  // combines the four wave states; the result is returned to every wave
-  auto combine = [&](MergeState& st) {
-    __syncthreads();
-    s_o[wave][d0] = st.o[0];
-    s_o[wave][d0 + 1] = st.o[1];
-    if (lane == 0) s_l[wave] = st.lse;
-    __syncthreads();
-    MergeState r{-INFINITY, {0.0f, 0.0f}};
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) merge_into(r, s_l[w], s_o[w][d0], s_o[w][d0 + 1]);
-    st = r;
-  };
-
-  MergeState st{-INFINITY, {0.0f, 0.0f}};
-  const int mslot = p.head_match_slot[ho];
-  if (wave == 0 && p.head_hit[ho] != 0 && mslot >= 0 && req >= 0 && req < p.s.R) {
-    const int64_t rowi = (static_cast<int64_t>(req) * M + mslot) * Hq + hq;
-    const float pl = p.lse_cache[rowi];
-    if (isfinite(pl)) {
-      const uint32_t w = *reinterpret_cast<const uint32_t*>(p.attn_cache + rowi * kHeadDim + d0);
-      st.lse = pl;
-      st.o[0] = bf16_lo(w);
-      st.o[1] = bf16_hi(w);
-    }
+  merge_range(ring, n_sink, n_sink + n_band, 0);
+  merge_range(rest, n_sink + n_band, n_sink + n_band + n_tail, n_band);
+  merge_range(rest, 0, n_sink, n_band + n_tail);
+  // the four waves' states, combined by wave 0 (which also read the entry:
+  // the entry read precedes the ring write below in the same lanes)
+  s_o[0][wave][d0] = ring.o[0];
+  s_o[0][wave][d0 + 1] = ring.o[1];
+  s_o[1][wave][d0] = rest.o[0];
+  s_o[1][wave][d0 + 1] = rest.o[1];
+  if (lane == 0) {
+    s_l[0][wave] = ring.lse;
+    s_l[1][wave] = rest.lse;
   }
-  merge_range(st, n_sink, n_sink + n_band);
-  combine(st);  // also orders every entry read before the ring write below
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    merge_into(ring, s_l[0][w], s_o[0][w][d0], s_o[0][w][d0 + 1]);
+    merge_into(rest, s_l[1][w], s_o[1][w][d0], s_o[1][w][d0 + 1]);
+  }
 
-  if (ready && P >= 0 && wave == 0) {  // (a negative past_len has no ring slot)
+  if (ready && P >= 0) {  // ring row at past_len % M (a negative past_len has no ring slot)
     const int64_t rowi = (static_cast<int64_t>(req) * M + dest) * Hq + hq;
-    const bool valid = isfinite(st.lse);
+    const bool valid = isfinite(ring.lse);
     *reinterpret_cast<uint32_t*>(p.query_cache + rowi * kHeadDim + d0) =
         *reinterpret_cast<const uint32_t*>(p.q_pre + ho * kHeadDim + d0);
-    const uint32_t packed = valid ? (static_cast<uint32_t>(f32_to_bf16(st.o[0])) |
-                                     (static_cast<uint32_t>(f32_to_bf16(st.o[1])) << 16))
+    const uint32_t packed = valid ? (static_cast<uint32_t>(f32_to_bf16(ring.o[0])) |
+                                     (static_cast<uint32_t>(f32_to_bf16(ring.o[1])) << 16))
                                   : 0u;
     *reinterpret_cast<uint32_t*>(p.attn_cache + rowi * kHeadDim + d0) = packed;
-    if (lane == 0) p.lse_cache[rowi] = valid ? st.lse : -INFINITY;
+    if (lane == 0) p.lse_cache[rowi] = valid ? ring.lse : -INFINITY;
   }
-
-  if (wave != 0) st = MergeState{-INFINITY, {0.0f, 0.0f}};
-  merge_range(st, 0, n_sink);
-  merge_range(st, n_sink + n_band, n_sink + n_band + n_tail);
-  combine(st);
-  if (wave == 0) {
-    const bool valid = isfinite(st.lse);
-    const uint32_t packed = valid ? (static_cast<uint32_t>(f32_to_bf16(st.o[0])) |
-                                     (static_cast<uint32_t>(f32_to_bf16(st.o[1])) << 16))
-                                  : 0u;
-    *reinterpret_cast<uint32_t*>(p.out + ho * kHeadDim + d0) = packed;
-    if (p.out_lse != nullptr && lane == 0) p.out_lse[ho] = valid ? st.lse : -INFINITY;
-  }
+  merge_into(ring, rest.lse, rest.o[0], rest.o[1]);
+  const bool valid = isfinite(ring.lse);
+  const uint32_t packed = valid ? (static_cast<uint32_t>(f32_to_bf16(ring.o[0])) |
+                                   (static_cast<uint32_t>(f32_to_bf16(ring.o[1])) << 16))
+                                : 0u;
+  *reinterpret_cast<uint32_t*>(p.out + ho * kHeadDim + d0) = packed;
+  if (p.out_lse != nullptr && lane == 0) p.out_lse[ho] = valid ? ring.lse : -INFINITY;
 }
 
 // ============================================================ host side ====

@@ -229,7 +229,7 @@ __global__ void __launch_bounds__(256, 2) window_kernel(WindowParams p) {
   int* s_boff = s_dyn;
   int* s_qo = s_dyn + (p.B + 1);
   int* s_kv = s_dyn + 2 * (p.B + 1);
-  __shared__ int s_part[256];
+  __shared__ int s_part[kWaves];
   __shared__ uint4 s_k[2][kBlk * 16];  // K rows of a 32-key block (swizzled)
   __shared__ uint4 s_v[2][kBlk * kVRow];  // V rows of the block (padded rows)
   __shared__ uint32_t s_okw[2][kWaves];  // per wave: bits of its 8 keys that have a pool row
@@ -254,21 +254,28 @@ __global__ void __launch_bounds__(256, 2) window_kernel(WindowParams p) {
       s_qo[b] = p.qo_indptr[b];
       s_kv[b] = p.kv_indptr[b];
     }
-    s_part[tid] = sum;
-    __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {  // inclusive Hillis-Steele scan
-      const int x = tid >= off ? s_part[tid - off] : 0;
-      __syncthreads();
-      s_part[tid] += x;
-      __syncthreads();
+    // exclusive scan of the per-thread sums: inclusive within each wave by
+    // lane shifts, then the four wave totals through LDS (one barrier)
+    int x = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(x, off);
+      if (lane >= off) x += y;
     }
-    int acc = tid > 0 ? s_part[tid - 1] : 0;
+    if (lane == 63) s_part[wave] = x;
+    __syncthreads();
+    int acc = x - sum, total = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      if (w < wave) acc += s_part[w];
+      total += s_part[w];
+    }
     for (int b = tid * per; b < min(B, (tid + 1) * per); ++b) {
       const int n = s_boff[b];
       s_boff[b] = acc;
       acc += n;
     }
-    if (tid == 255) s_boff[B] = s_part[255];
+    if (tid == 0) s_boff[B] = total;
     __syncthreads();
   }
   const int Hq = p.Hq, Hkv = p.Hkv;
