@@ -273,6 +273,67 @@ def cpu_baseline(args, hit):
                 sample_head_hits=int(res.head["hit"].sum()))
 
 
+def aux_cpu_baselines():
+    """The CPU oracle (one thread) on the aux legs' workloads.  The fused
+    rectification and the ring write only touch the last M = 32 rows of each
+    chunk (and, for the rectification, the S - 1 keys before them), so a
+    sample of all 64 requests with 288-row chunks does exactly the per-request
+    work of the 8192-row chunks; the RoPE leg runs at full size."""
+    import numpy as np
+
+    from oracle import oracle as orc
+
+    rng = np.random.default_rng(3)
+    # random bf16 bits (the top half of random float32s: timing data only)
+    bf = lambda *shape: (rng.standard_normal(shape, dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)  # noqa: E731
+    B, chunk, hq, hkv, S, M = 64, 288, 32, 4, 256, 32
+    rows = B * chunk
+    qo = np.arange(0, rows + 1, chunk, dtype=np.int32)
+    idx = rng.permutation(rows).astype(np.int32)
+    q_post, src_q, o_full = bf(rows, hq, D), bf(rows, hq, D), bf(rows, hq, D)
+    lse_full = rng.standard_normal((rows, hq), dtype=np.float32) + 8.0
+    k, v = bf(rows, hkv, D), bf(rows, hkv, D)
+    qc = np.zeros((B + 1, M, hq, D), np.uint16)
+    ac, lc = np.zeros_like(qc), np.zeros((B + 1, M, hq), np.float32)
+    rl = np.zeros(B + 1, np.int32)
+    req = np.arange(B, dtype=np.int32)
+    t0 = time.perf_counter()
+    orc.rectify_update_cache(q_post, src_q, o_full, lse_full, k, v, qo, qo, idx, qc, ac, lc, rl, req,
+                             semantic_pos_ahead=S, front_sink_tokens=0, sink_mode=0,
+                             sm_scale=1.0 / math.sqrt(D))
+    rect_s = time.perf_counter() - t0
+    out = {"prefill_rectify": dict(
+        value=round(rect_s * 1e6, 1), unit="us", cores=1, kind="port",
+        sample=f"all {B} requests with {chunk}-row chunks (the kept {M} rows and their {S}-key windows "
+               f"are the whole work of an 8192-row chunk), single-threaded C oracle")}
+    rl2 = np.zeros(B, np.int32)
+    src_l = rng.standard_normal((rows, hq), dtype=np.float32)
+    lens = np.full(B, chunk, np.int32)
+    t0 = time.perf_counter()
+    orc.prefill_update_cache(qc, ac, lc, rl2, req, src_q, o_full, src_l, qo, lens, M, hq, D)
+    upd_s = time.perf_counter() - t0
+    out["prefill_update_cache"] = dict(
+        value=round(upd_s * 1e6, 1), unit="us", cores=1, kind="port",
+        sample=f"all {B} batch rows with {chunk}-row chunks (the last {M} rows are copied either way), "
+               f"single-threaded C oracle")
+    n, hq4, hkv4, pool = 64, 32, 8, 1 << 16
+    qkv = bf(n, (hq4 + 2 * hkv4) * D)
+    q4, k4, v4 = qkv[:, :hq4 * D], qkv[:, hq4 * D:(hq4 + hkv4) * D], qkv[:, (hq4 + hkv4) * D:]
+    q_pre = np.zeros((n, hq4, D), np.uint16)
+    kb, vb = np.zeros((pool, hkv4, D), np.uint16), np.zeros((pool, hkv4, D), np.uint16)
+    inv = 1.0 / (10000.0 ** (np.arange(0, D, 2, dtype=np.float64) / D))
+    ang = np.arange(131072, dtype=np.float64)[:, None] * inv[None, :]
+    cs = np.concatenate([np.cos(ang), np.sin(ang)], axis=1).astype(np.float32)
+    pos = rng.integers(0, 131072, n).astype(np.int64)
+    locs = rng.permutation(pool)[:n].astype(np.int64)
+    t0 = time.perf_counter()
+    orc.rope_preserve(q4, k4, v4, q_pre, kb, vb, cs, pos, locs, head_dim=D, is_neox=True)
+    rope_s = time.perf_counter() - t0
+    out["decode_rope"] = dict(value=round(rope_s * 1e6, 1), unit="us", cores=1, kind="port",
+                              sample=f"full size ({n} tokens), single-threaded C oracle")
+    return out
+
+
 # The reference's published MAC decode-step times on H100 80GB (CUDA-graph
 # replay, B=64, past_len 126976, ring 2048, S=256, F=0, synthetic_head):
 # results/cuda_graph_hit_curves/gqa4.csv:156-169 and gqa8.csv:156-169.
@@ -500,6 +561,10 @@ def main():
         log("[bench] timing the CPU oracle sample")
         cpu = cpu_baseline(args, args.hit)
         log(f"[bench] cpu {cpu}")
+        if aux is not None:
+            for name, base in aux_cpu_baselines().items():
+                aux[name]["cpu_baseline"] = base
+            log(f"[bench] aux with CPU baselines {aux}")
 
     ms = headline["us_per_step"] / 1e3
     attn_us = headline["phase_us"][1]
