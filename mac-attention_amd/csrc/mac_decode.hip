@@ -1286,8 +1286,7 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
           bmax = fmaxf(bmax, x);
         }
       }
-      bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-      bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+      bmax = quad_max(bmax);
       // Lazy rescale: the reference point m only moves when the block max
       // exceeds it by more than kRescaleSlack (log2 units), so most blocks
       // skip the 32-accumulator rescale; p <= 2^kRescaleSlack stays exact in
@@ -1330,8 +1329,7 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
     }
 
     // ---- wave result -> LDS (over the K tiles), then combine the four waves ----
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    l = quad_sum(l);
     __syncthreads();  // every wave is done with its K tile
     if (head_ok) {
 #pragma unroll

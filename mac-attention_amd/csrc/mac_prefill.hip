@@ -570,6 +570,30 @@ __global__ void __launch_bounds__(256, 2) window_kernel(WindowParams p) {
     const int slot = static_cast<int>((static_cast<int64_t>(before) + local) % p.M);
     const int64_t drow = static_cast<int64_t>(req) * p.M + slot;
     const bool empty = pos + 1 - p.S <= (sink ? p.F : 0);  // nothing left after the downdate
+    // every load of the epilogue (the full state's o and the pre-RoPE query
+    // of the wave's heads) is issued before its math: one round of latency,
+    // not two per head
+    uint32_t fow[HPW][16], sqw[HPW][16];
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh) {
+      const int h = hkv * G + min(hg0 + hh, G - 1);
+      const uint16_t* of = p.o_full + (grow * Hq + h) * kHeadDim + 4 * quad;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const uint2 f = *reinterpret_cast<const uint2*>(of + 16 * dt);
+        fow[hh][2 * dt] = f.x;
+        fow[hh][2 * dt + 1] = f.y;
+      }
+      const uint16_t* sq = p.src_q + (grow * Hq + h) * kHeadDim;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint4 w = *reinterpret_cast<const uint4*>(sq + 8 * (4 * s + quad));
+        sqw[hh][4 * s] = w.x;
+        sqw[hh][4 * s + 1] = w.y;
+        sqw[hh][4 * s + 2] = w.z;
+        sqw[hh][4 * s + 3] = w.w;
+      }
+    }
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) {
       if (hh >= nheads) break;
@@ -585,13 +609,12 @@ __global__ void __launch_bounds__(256, 2) window_kernel(WindowParams p) {
       } else {
         c = downdate_control(lse_full[hh], lse_w);
       }
-      const uint16_t* of = p.o_full + (grow * Hq + h) * kHeadDim + 4 * quad;
       uint16_t* ap = p.attn_cache + (drow * Hq + h) * kHeadDim + 4 * quad;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const uint2 f = *reinterpret_cast<const uint2*>(of + 16 * dt);
         float r[4];
-        const float fo[4] = {bf16_lo(f.x), bf16_hi(f.x), bf16_lo(f.y), bf16_hi(f.y)};
+        const uint32_t fx = fow[hh][2 * dt], fy = fow[hh][2 * dt + 1];
+        const float fo[4] = {bf16_lo(fx), bf16_hi(fx), bf16_lo(fy), bf16_hi(fy)};
 #pragma unroll
         for (int i = 0; i < 4; ++i) r[i] = empty ? 0.0f : (fo[i] - c.t * (acc[hh][dt][i] * inv)) * c.scale;
         uint2 w;
@@ -601,11 +624,11 @@ __global__ void __launch_bounds__(256, 2) window_kernel(WindowParams p) {
       }
       if (quad == 0) p.lse_cache[drow * Hq + h] = (p.sink_mode == 0 && p.F > 0) ? -INFINITY : c.lse;
       // pre-RoPE query row and the NaN marker of the unknown post-RoPE row (PREFILL:251-262)
-      const uint16_t* sq = p.src_q + (grow * Hq + h) * kHeadDim;
       uint16_t* dq = p.q_cache + (drow * Hq + h) * kHeadDim;
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        *reinterpret_cast<uint4*>(dq + 8 * (4 * s + quad)) = *reinterpret_cast<const uint4*>(sq + 8 * (4 * s + quad));
+        *reinterpret_cast<uint4*>(dq + 8 * (4 * s + quad)) =
+            make_uint4(sqw[hh][4 * s], sqw[hh][4 * s + 1], sqw[hh][4 * s + 2], sqw[hh][4 * s + 3]);
       if (p.q_post_cache != nullptr) {
         uint16_t* pq = p.q_post_cache + (drow * Hq + h) * kHeadDim;
         const uint4 nan4 = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
