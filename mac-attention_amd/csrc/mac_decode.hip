@@ -286,9 +286,10 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
     // Hit decisions are those of the full scan; only the best distance of a
     // head without a hit may differ.  Lane (row, c) takes slot 2u + (c >> 3)
     // of the batch and 16-byte chunk (c & 7) of its first half, then chunk
-    // 8 + (c & 7) -- or, for a pruned slot, its first chunk again, a cache hit
-    // instead of HBM traffic (no divergent loads); a batch the whole wave
-    // pruned skips the second round.
+    // 8 + (c & 7) -- or, for a pruned slot, a chunk of its head's query row,
+    // a cache hit instead of HBM traffic (no divergent loads); a batch the
+    // whole wave pruned skips the second round.  Ring rows are read once per
+    // step, with the non-temporal policy.
     constexpr int kProbeBatch = kProbeSlots / kPasses;  // slot pairs per lane batch
     const int half = c >> 3, cc = c & 7;
     float qa[kPasses][8], qb[kPasses][8];
@@ -316,7 +317,7 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
 #pragma unroll
         for (int u = 0; u < kProbeBatch; ++u) {
           const int64_t off = ((cache_req + min(slot[u], s_hi - 1)) * Hq + hkv * G + hl) * kHeadDim + cc * 8;
-          w[ps][u] = *reinterpret_cast<const uint4*>(p.query_cache + off);
+          w[ps][u] = load_stream16(p.query_cache + off);  // read once: no cache pollution
         }
       }
       float acc[kPasses][kProbeBatch];
@@ -347,9 +348,12 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
         const int hl = min(row + 4 * ps, G - 1);
 #pragma unroll
         for (int u = 0; u < kProbeBatch; ++u) {
-          const int64_t off = ((cache_req + min(slot[u], s_hi - 1)) * Hq + hkv * G + hl) * kHeadDim + cc * 8 +
-                              (eval[ps][u] ? 64 : 0);
-          w[ps][u] = load_stream16(p.query_cache + off);
+          // a pruned slot's lanes read their head's query row instead (hot in
+          // the cache: every workgroup of the group reads it); the value is unused
+          const uint16_t* src =
+              eval[ps][u] ? p.query_cache + ((cache_req + min(slot[u], s_hi - 1)) * Hq + hkv * G + hl) * kHeadDim + 64 + cc * 8
+                          : p.q_pre + (static_cast<int64_t>(n) * Hq + hkv * G + hl) * kHeadDim + cc * 8;
+          w[ps][u] = load_stream16(src);
         }
       }
 #pragma unroll
