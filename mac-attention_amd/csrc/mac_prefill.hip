@@ -42,6 +42,8 @@ int fail(int code, const char* fmt, ...);
 
 namespace {
 
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
 using namespace mac;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -104,36 +106,61 @@ __global__ void __launch_bounds__(256) downdate_kernel(const uint16_t* __restric
                                                        const void* __restrict__ lse1, int dt1,
                                                        uint16_t* __restrict__ out2, void* __restrict__ lse2,
                                                        int dt2, int64_t rows, int D) {
+  // Each 16-lane group takes kR rows at a time (rows g, g + 16, ... of the
+  // workgroup's slab) with every load issued before the math; the rows are
+  // read once, so o1 and o2 move with the non-temporal policy.
+  constexpr int kR = 4;
   const int sub = threadIdx.x & 15;
-  for (int64_t row = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4); row < rows;
-       row += static_cast<int64_t>(gridDim.x) * 16) {
-    const float l1 = load_lse(lse1, dt1, row);
-    const float l2 = load_lse(lse2, dt2, row);
-    const Downdate c = downdate_control(l1, l2);
-    const uint16_t* a = out1 + row * D;
-    uint16_t* b = out2 + row * D;
+  const int64_t step = static_cast<int64_t>(gridDim.x) * 16 * kR;
+  for (int64_t row0 = static_cast<int64_t>(blockIdx.x) * 16 * kR + (threadIdx.x >> 4); row0 < rows; row0 += step) {
+    Downdate c[kR];
+#pragma unroll
+    for (int k = 0; k < kR; ++k) {
+      const int64_t row = min(row0 + 16 * k, rows - 1);
+      c[k] = downdate_control(load_lse(lse1, dt1, row), load_lse(lse2, dt2, row));
+    }
     if ((D & 7) == 0) {
       for (int e = sub * 8; e < D; e += 128) {
-        const uint4 wa = *reinterpret_cast<const uint4*>(a + e);
-        const uint4 wb = *reinterpret_cast<const uint4*>(b + e);
-        float fa[8], fb[8];
-        unpack8(wa, fa);
-        unpack8(wb, fb);
-        uint16_t r[8];
+        uint4 wa[kR], wb[kR];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) r[i] = f32_to_bf16((fa[i] - c.t * fb[i]) * c.scale);
-        uint4 w;
-        w.x = r[0] | (static_cast<uint32_t>(r[1]) << 16);
-        w.y = r[2] | (static_cast<uint32_t>(r[3]) << 16);
-        w.z = r[4] | (static_cast<uint32_t>(r[5]) << 16);
-        w.w = r[6] | (static_cast<uint32_t>(r[7]) << 16);
-        *reinterpret_cast<uint4*>(b + e) = w;
+        for (int k = 0; k < kR; ++k) {
+          const int64_t row = min(row0 + 16 * k, rows - 1);
+          wa[k] = __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(out1 + row * D + e)));
+          wb[k] = __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(out2 + row * D + e)));
+        }
+#pragma unroll
+        for (int k = 0; k < kR; ++k) {
+          if (row0 + 16 * k >= rows) break;
+          float fa[8], fb[8];
+          unpack8(wa[k], fa);
+          unpack8(wb[k], fb);
+          uint16_t r[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) r[i] = f32_to_bf16((fa[i] - c[k].t * fb[i]) * c[k].scale);
+          u32x4_t w;
+          w[0] = r[0] | (static_cast<uint32_t>(r[1]) << 16);
+          w[1] = r[2] | (static_cast<uint32_t>(r[3]) << 16);
+          w[2] = r[4] | (static_cast<uint32_t>(r[5]) << 16);
+          w[3] = r[6] | (static_cast<uint32_t>(r[7]) << 16);
+          __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t*>(out2 + (row0 + 16 * k) * D + e));
+        }
       }
     } else {
-      for (int e = sub; e < D; e += 16)
-        b[e] = f32_to_bf16((bf16_to_f32(a[e]) - c.t * bf16_to_f32(b[e])) * c.scale);
+#pragma unroll
+      for (int k = 0; k < kR; ++k) {
+        const int64_t row = row0 + 16 * k;
+        if (row >= rows) break;
+        const uint16_t* a = out1 + row * D;
+        uint16_t* b = out2 + row * D;
+        for (int e = sub; e < D; e += 16)
+          b[e] = f32_to_bf16((bf16_to_f32(a[e]) - c[k].t * bf16_to_f32(b[e])) * c[k].scale);
+      }
     }
-    if (sub == 0) store_lse(lse2, dt2, row, c.lse);
+    if (sub == 0) {
+#pragma unroll
+      for (int k = 0; k < kR; ++k)
+        if (row0 + 16 * k < rows) store_lse(lse2, dt2, row0 + 16 * k, c[k].lse);
+    }
   }
 }
 
@@ -708,7 +735,7 @@ extern "C" int mac_update_then_downdate_bf16_inplace(const void* out1, const voi
   if ((head_dim & 7) == 0)
     REQUIRE((reinterpret_cast<uintptr_t>(out1) & 15) == 0 && (reinterpret_cast<uintptr_t>(out2) & 15) == 0,
             "out tensors must be 16-byte aligned");
-  const int64_t wgs = std::min<int64_t>((rows + 15) / 16, 65536);
+  const int64_t wgs = std::min<int64_t>((rows + 63) / 64, 65536);
   hipLaunchKernelGGL(downdate_kernel, dim3(static_cast<unsigned>(wgs)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(out1), lse1, lse1_dtype,
                      static_cast<uint16_t*>(out2), lse2, lse2_dtype, rows, head_dim);
