@@ -273,6 +273,40 @@ def cpu_baseline(args, hit):
                 sample_head_hits=int(res.head["hit"].sum()))
 
 
+def stream_read_peak(torch):
+    """The rate a plain streaming read of 8 GiB reaches on this GPU
+    (mac_bench_stream_read: non-temporal 16-byte loads, eight in flight per
+    lane), the best of grids of 0.75 and 1 workgroups per CU (larger grids
+    measured slower), as context for the kernels' fractions of the 8 TB/s
+    nameplate."""
+    import ctypes
+
+    from mac_attention.integrations.sglang import bridge
+
+    lib = bridge.load_library()
+    nbytes = 8 << 30
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    src = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").fill_(1)
+    sink = torch.empty(cus, dtype=torch.int32, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    best = None
+    for grid in (cus * 3 // 4, cus):
+        def run():
+            rc = lib.mac_bench_stream_read(ctypes.c_void_p(src.data_ptr()), ctypes.c_int64(nbytes),
+                                           ctypes.c_void_p(sink.data_ptr()), ctypes.c_int32(grid), stream)
+            if rc != 0:
+                raise RuntimeError(lib.mac_last_error().decode())
+
+        us = _time_us(torch, run, 10)
+        if best is None or us < best[0]:
+            best = (us, grid)
+    del src, sink
+    torch.cuda.empty_cache()
+    gbs = nbytes / best[0] / 1e3
+    return dict(bytes=nbytes, workgroups=best[1], us=round(best[0], 1), gbs=round(gbs, 1),
+                frac_of_peak=round(gbs / HBM_PEAK_GBS, 4))
+
+
 def aux_cpu_baselines():
     """The CPU oracle (one thread) on the aux legs' workloads.  The fused
     rectification and the ring write only touch the last M = 32 rows of each
@@ -550,6 +584,9 @@ def main():
             del dev
             torch.cuda.empty_cache()
 
+    stream_peak = stream_read_peak(torch)
+    log(f"[bench] streaming read {stream_peak}")
+
     aux = None
     if not args.no_aux:
         aux = measure_aux(torch)
@@ -603,6 +640,7 @@ def main():
         "sweep": sweep,
         "reference_shape": ref_shape,
         "aux": aux,
+        "stream_read": stream_peak,
     }
     text = json.dumps(line)
     if args.json_out:

@@ -8,7 +8,7 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
-SOURCES = [os.path.join(HERE, "csrc", f) for f in ("mac_decode.hip", "mac_cache_ops.hip", "mac_prefill.hip", "mac_rope.hip")]
+SOURCES = [os.path.join(HERE, "csrc", f) for f in ("mac_decode.hip", "mac_cache_ops.hip", "mac_prefill.hip", "mac_rope.hip", "mac_bench.hip")]
 OUTPUT = os.path.join(HERE, "libmac_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

@@ -1,0 +1,68 @@
+// mac_bench.hip -- a measurement helper for MI355X (gfx950): the rate a plain
+// streaming read of HBM reaches on this GPU, as context for the decode
+// kernels' fractions of the 8 TB/s nameplate.  Not part of the decode path.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "mac_attention_amd.h"
+
+namespace mac {
+int fail(int code, const char* fmt, ...);
+}  // namespace mac
+
+namespace {
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// Grid-stride read of n16 16-byte words with the non-temporal policy (as the
+// decode kernels stream K/V), eight loads in flight per lane; one XOR per
+// workgroup goes to `sink` so the loads are not dead code.
+__global__ void __launch_bounds__(256) stream_read_kernel(const u32x4_t* __restrict__ src, int64_t n16,
+                                                          uint32_t* __restrict__ sink) {
+  constexpr int kUnroll = 8;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  uint32_t acc = 0;
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  for (; i + (kUnroll - 1) * stride < n16; i += kUnroll * stride) {
+    u32x4_t w[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) w[u] = __builtin_nontemporal_load(src + i + u * stride);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) acc ^= w[u][0] ^ w[u][1] ^ w[u][2] ^ w[u][3];
+  }
+  for (; i < n16; i += stride) {
+    const u32x4_t w = __builtin_nontemporal_load(src + i);
+    acc ^= w[0] ^ w[1] ^ w[2] ^ w[3];
+  }
+  __shared__ uint32_t s_acc[256];
+  s_acc[threadIdx.x] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t x = 0;
+    for (int t = 0; t < 256; ++t) x ^= s_acc[t];
+    sink[blockIdx.x] = x;
+  }
+}
+
+}  // namespace
+
+extern "C" int mac_bench_stream_read(const void* src, int64_t bytes, uint32_t* sink, int32_t sink_len,
+                                     void* stream) {
+  if (src == nullptr || sink == nullptr || bytes < 16 || sink_len <= 0 ||
+      (reinterpret_cast<uintptr_t>(src) & 15) != 0)
+    return mac::fail(MAC_ERR_INVALID_ARGUMENT, "mac_bench_stream_read: invalid arguments");
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+  }
+  const int grid = std::min(sink_len, cus * 8);
+  hipLaunchKernelGGL(stream_read_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const u32x4_t*>(src), bytes / 16, sink);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return mac::fail(MAC_ERR_HIP, "stream_read_kernel: %s", hipGetErrorString(e));
+  return MAC_OK;
+}

@@ -81,6 +81,7 @@ EXPORTED_SYMBOLS = (
     "mac_prefill_window_attention_bf16",
     "mac_prefill_rectify_update_cache_bf16",
     "mac_decode_rope_preserve_q_bf16",
+    "mac_bench_stream_read",
     "mac_last_error",
     "mac_abi_version",
 )
@@ -152,6 +153,8 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i32, _p, _i32, _p, _i32,
         _i64, _i32, _i32, _i32, _i32, _p]
     lib.mac_decode_rope_preserve_q_bf16.restype = ctypes.c_int
+    lib.mac_bench_stream_read.argtypes = [_p, _i64, _p, _i32, _p]
+    lib.mac_bench_stream_read.restype = ctypes.c_int
     if lib.mac_abi_version() != ABI_VERSION:
         raise RuntimeError(
             f"{path} has ABI version {lib.mac_abi_version()}, binding expects {ABI_VERSION}"
