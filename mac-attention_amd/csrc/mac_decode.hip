@@ -128,6 +128,8 @@ struct AttnParams {
   int F;
   int tile_tokens;  // the caller's tile size (task_counts[3] only)
   int tasks_per_wg;  // target tasks per workgroup of the plan
+  int narrow_grid;                // workgroups that take tasks when a step has
+  long long narrow_min_tokens;    // at least this many tokens (the others return)
   int min_chunk;     // smallest chunk of the plan (tokens)
   float q_scale;  // sm_scale * log2(e)
 };
@@ -691,12 +693,11 @@ constexpr int kMaxChunk = 16384;
 // s_off[NG+1 .. 2NG+1] those of the B counts.  Workgroup 0 also publishes the
 // per-group chunk and task counts for merge_write and the task counters.
 __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& total_tasks_out,
-                           int& chunk_out) {
+                           int& chunk_out, int& active_wgs_out) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int NG = p.s.N * p.s.Hkv;
-  const int W = gridDim.x;
   const int per_thread = ceil_div(NG, kBlock);
   const int g_lo = min(tid * per_thread, NG);
   const int g_hi = min(g_lo + per_thread, NG);
@@ -718,6 +719,11 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
     for (int w = 0; w < kWaves; ++w) tok += s_tok[w];
     __syncthreads();
   }
+  // A step with many tokens streams fastest with one workgroup per CU; a
+  // small (latency-bound) one wants every resident workgroup.
+  const int W = tok >= p.narrow_min_tokens ? min(static_cast<int>(gridDim.x), p.narrow_grid)
+                                           : static_cast<int>(gridDim.x);
+  active_wgs_out = W;
   const long long target_tasks = static_cast<long long>(p.tasks_per_wg) * W;
   int chunk = static_cast<int>((tok + target_tasks - 1) / target_tasks);
   chunk = ceil_div(max(chunk, p.min_chunk), 64) * 64;
@@ -931,8 +937,9 @@ __global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
   const int c = lane & 15;
   const int NG = p.s.N * p.s.Hkv;
 
-  int total_tasks = 0, chunk = 0;
-  plan_tasks(p, s_off, s_tmp, total_tasks, chunk);
+  int total_tasks = 0, chunk = 0, active_wgs = 0;
+  plan_tasks(p, s_off, s_tmp, total_tasks, chunk, active_wgs);
+  if (static_cast<int>(blockIdx.x) >= active_wgs) return;
 
   // ---- tasks ----
   const int Hq = p.s.Hq;
@@ -1151,8 +1158,9 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
   const int quad = lane >> 4;  // lane / 16
   const int col = lane & 15;   // lane % 16
   const int NG = p.s.N * p.s.Hkv;
-  int total_tasks = 0, chunk = 0;
-  plan_tasks(p, s_off, s_tmp, total_tasks, chunk);
+  int total_tasks = 0, chunk = 0, active_wgs = 0;
+  plan_tasks(p, s_off, s_tmp, total_tasks, chunk, active_wgs);
+  if (static_cast<int>(blockIdx.x) >= active_wgs) return;
 
   const int Hq = p.s.Hq;
   const int Hkv = p.s.Hkv;
@@ -1556,6 +1564,16 @@ int match_probe() {
   return v;
 }
 
+// Tokens from which a step runs one span-attention workgroup per CU
+// (MAC_AMD_NARROW_TOKENS, read once; default 1M tokens, 512 MB of K/V).
+long long narrow_min_tokens() {
+  static const long long v = [] {
+    const char* e = std::getenv("MAC_AMD_NARROW_TOKENS");
+    return e != nullptr ? std::atoll(e) : (1LL << 20);
+  }();
+  return v;
+}
+
 int attn_impl() {
   static const int impl = [] {
     const char* e = std::getenv("MAC_AMD_ATTN_IMPL");
@@ -1814,6 +1832,8 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   ap.tile_tokens = a->tile_tokens;
   ap.tasks_per_wg = tasks_per_wg();
   ap.min_chunk = min_chunk();
+  ap.narrow_grid = cus;
+  ap.narrow_min_tokens = narrow_min_tokens();
 
   MergeParams mp{};
   mp.s = s;
