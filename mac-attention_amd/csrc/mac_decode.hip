@@ -1565,11 +1565,11 @@ int match_probe() {
 }
 
 // Tokens from which a step runs one span-attention workgroup per CU
-// (MAC_AMD_NARROW_TOKENS, read once; default 1M tokens, 512 MB of K/V).
+// (MAC_AMD_NARROW_TOKENS, read once; default 8M tokens, 4 GB of K/V).
 long long narrow_min_tokens() {
   static const long long v = [] {
     const char* e = std::getenv("MAC_AMD_NARROW_TOKENS");
-    return e != nullptr ? std::atoll(e) : (1LL << 20);
+    return e != nullptr ? std::atoll(e) : (8LL << 20);
   }();
   return v;
 }
@@ -1832,7 +1832,7 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   ap.tile_tokens = a->tile_tokens;
   ap.tasks_per_wg = tasks_per_wg();
   ap.min_chunk = min_chunk();
-  ap.narrow_grid = cus;
+  ap.narrow_grid = impl ? cus : INT_MAX;  // the VALU kernel is instruction-bound: every resident workgroup
   ap.narrow_min_tokens = narrow_min_tokens();
 
   MergeParams mp{};
