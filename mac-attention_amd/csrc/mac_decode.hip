@@ -1096,8 +1096,7 @@ __global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
       }
     }
     __syncthreads();
-    write_partial<G>(p, g, j, s_o, s_ml);
-    __syncthreads();
+    write_partial<G>(p, g, j, s_o, s_ml);  // next_task's barrier closes the task
   }
 }
 
@@ -1139,39 +1138,33 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& w) { return __builtin
 // swizzle puts the 16 of them on 16 different chunk positions.
 __device__ __forceinline__ int k_swz(int t) { return 4 * ((t >> 3) & 3) + (t & 3); }
 
-template <int G>
-__global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnParams p) {
-  constexpr int kBlk = 32;  // tokens per wave block
-  extern __shared__ int s_off[];  // 2 (NG + 1) task offsets (dynamic)
-  __shared__ int s_tmp[kWaves];
-  __shared__ uint4 s_k[kWaves][kBlk * 16];
-  __shared__ uint4 s_v[kWaves][kBlk * 16];
-  __shared__ uint4 s_q[16 * 16];
-  __shared__ float s_ml[kWaves][G][2];
-  // the per-wave o of the task epilogue reuses the K tiles
-  static_assert(sizeof(float) * kWaves * G * kHeadDim <= sizeof(uint4) * kWaves * kBlk * 16, "s_o alias");
-  auto s_o = reinterpret_cast<float (*)[G][kHeadDim]>(&s_k[0][0]);
+constexpr int kMfmaBlk = 32;  // tokens per wave block
 
+// One task of the MFMA kernel: the four waves of the workgroup take its
+// blocks in turn and combine their softmax states through LDS.  (A function
+// of its own, called once per task, so the compiler recomputes the LDS
+// addresses per task instead of holding them across the task loop: the
+// registers go to the block loop, which measured 2% faster for steps of many
+// short tasks.)
+template <int G>
+__device__ __forceinline__ void mfma_task(const AttnParams& p, const TaskInfo& ti,
+                                          uint4 (*s_k)[kMfmaBlk * 16], uint4 (*s_v)[kMfmaBlk * 16],
+                                          uint4* s_q, float (*s_ml)[G][2]) {
+  constexpr int kBlk = kMfmaBlk;
+  // the per-wave o of the task epilogue reuses the K tiles
+  auto s_o = reinterpret_cast<float (*)[G][kHeadDim]>(&s_k[0][0]);
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) control flow
   const int lane = tid & 63;
   const int quad = lane >> 4;  // lane / 16
   const int col = lane & 15;   // lane % 16
-  const int NG = p.s.N * p.s.Hkv;
-  int total_tasks = 0, chunk = 0, active_wgs = 0;
-  plan_tasks(p, s_off, s_tmp, total_tasks, chunk, active_wgs);
-  if (static_cast<int>(blockIdx.x) >= active_wgs) return;
-
   const int Hq = p.s.Hq;
   const int Hkv = p.s.Hkv;
   const int64_t kv_stride = static_cast<int64_t>(Hkv) * kHeadDim;
   const bool head_ok = col < G;
   const uint16_t* vtile = reinterpret_cast<const uint16_t*>(&s_v[wave][0]);
   // load-side token of load i for this lane: 8*quad + i; chunk: col
-
-  __shared__ int s_task;
-  for (int t = next_task(p, s_task); t < total_tasks; t = next_task(p, s_task)) {
-    const TaskInfo ti = decode_task(p, s_off, NG, chunk, t);
+  {
     const int n = ti.n, hkv = ti.hkv, a = ti.a, b = ti.b, P = ti.P;
     const int32_t* r2t = p.req_to_token + static_cast<int64_t>(ti.req_ok ? ti.req : 0) * p.s.r2t_stride;
     const uint16_t* kbase = p.k_buffer + static_cast<int64_t>(hkv) * kHeadDim + col * 8;
@@ -1340,8 +1333,8 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
       __builtin_amdgcn_wave_barrier();
     }
 
-    // ---- wave result -> LDS (over the K tiles), then combine the four waves ----
     l = quad_sum(l);
+    // ---- wave result -> LDS (over the K tiles), then combine the four waves ----
     __syncthreads();  // every wave is done with its K tile
     if (head_ok) {
 #pragma unroll
@@ -1354,9 +1347,28 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
       }
     }
     __syncthreads();
-    write_partial<G>(p, ti.g, ti.j, s_o, s_ml);
-    __syncthreads();
+    write_partial<G>(p, ti.g, ti.j, s_o, s_ml);  // next_task's barrier closes the task
   }
+}
+
+template <int G>
+__global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnParams p) {
+  extern __shared__ int s_off[];  // 2 (NG + 1) task offsets (dynamic)
+  __shared__ int s_tmp[kWaves];
+  __shared__ uint4 s_k[kWaves][kMfmaBlk * 16];
+  __shared__ uint4 s_v[kWaves][kMfmaBlk * 16];
+  __shared__ uint4 s_q[16 * 16];
+  __shared__ float s_ml[kWaves][G][2];
+  static_assert(sizeof(float) * kWaves * G * kHeadDim <= sizeof(uint4) * kWaves * kMfmaBlk * 16, "s_o alias");
+
+  const int NG = p.s.N * p.s.Hkv;
+  int total_tasks = 0, chunk = 0, active_wgs = 0;
+  plan_tasks(p, s_off, s_tmp, total_tasks, chunk, active_wgs);
+  if (static_cast<int>(blockIdx.x) >= active_wgs) return;
+
+  __shared__ int s_task;
+  for (int t = next_task(p, s_task); t < total_tasks; t = next_task(p, s_task))
+    mfma_task<G>(p, decode_task(p, s_off, NG, chunk, t), s_k, s_v, s_q, s_ml);
 }
 
 // ============================================================ 3. merge ====
