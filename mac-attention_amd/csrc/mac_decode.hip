@@ -1453,16 +1453,16 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
   // eight loads in flight at a time): band partials into `ring` (on top of
   // the cached entry), sink and tail partials into `rest`.
   MergeState ring{-INFINITY, {0.0f, 0.0f}}, rest{-INFINITY, {0.0f, 0.0f}};
+  // The cached entry of a hit head (wave 0): its lse and o are loaded
+  // together here and merged after the partials, so the partial loads are
+  // issued without waiting for them.  A non-finite lse is skipped.
+  float entry_lse = -INFINITY;
+  uint32_t entry_o = 0;
   const int mslot = p.head_match_slot[ho];
   if (wave == 0 && p.head_hit[ho] != 0 && mslot >= 0 && req >= 0 && req < p.s.R) {
     const int64_t rowi = (static_cast<int64_t>(req) * M + mslot) * Hq + hq;
-    const float pl = p.lse_cache[rowi];
-    if (isfinite(pl)) {
-      const uint32_t w = *reinterpret_cast<const uint32_t*>(p.attn_cache + rowi * kHeadDim + d0);
-      ring.lse = pl;
-      ring.o[0] = bf16_lo(w);
-      ring.o[1] = bf16_hi(w);
-    }
+    entry_lse = p.lse_cache[rowi];
+    entry_o = *reinterpret_cast<const uint32_t*>(p.attn_cache + rowi * kHeadDim + d0);
   }
   // this wave's partials of [j0, j1) into `st`, eight loads in flight; wave
   // (first + k) % 4 takes j0 + k, so that consecutive ranges continue the
@@ -1483,6 +1483,7 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
   merge_range(ring, n_sink, n_sink + n_band, 0);
   merge_range(rest, n_sink + n_band, n_sink + n_band + n_tail, n_band);
   merge_range(rest, 0, n_sink, n_band + n_tail);
+  merge_into(ring, entry_lse, bf16_lo(entry_o), bf16_hi(entry_o));
   // the four waves' states, combined by wave 0 (which also read the entry:
   // the entry read precedes the ring write below in the same lanes)
   s_o[0][wave][d0] = ring.o[0];
