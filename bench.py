@@ -277,7 +277,8 @@ def stream_read_peak(torch):
     """The rate a plain streaming read of 8 GiB reaches on this GPU
     (mac_bench_stream_read: non-temporal 16-byte loads, eight in flight per
     lane), the best of grids of 0.75 and 1 workgroups per CU (larger grids
-    measured slower), as context for the kernels' fractions of the 8 TB/s
+    measured slower), and that of a plain 2 GiB device copy (4 GiB read and
+    written), as context for the kernels' fractions of the 8 TB/s
     nameplate."""
     import ctypes
 
@@ -300,11 +301,19 @@ def stream_read_peak(torch):
         us = _time_us(torch, run, 10)
         if best is None or us < best[0]:
             best = (us, grid)
-    del src, sink
+    # a plain device-to-device copy (torch's copy kernel), bytes read +
+    # written: the level for kernels that write as much as they read
+    dst = torch.empty(nbytes // 16, dtype=torch.int32, device="cuda")  # 2 GiB
+    half = src[: nbytes // 16]
+    copy_us = _time_us(torch, lambda: dst.copy_(half), 10)
+    del src, sink, dst, half
     torch.cuda.empty_cache()
     gbs = nbytes / best[0] / 1e3
+    copy_gbs = (nbytes // 2) / copy_us / 1e3
     return dict(bytes=nbytes, workgroups=best[1], us=round(best[0], 1), gbs=round(gbs, 1),
-                frac_of_peak=round(gbs / HBM_PEAK_GBS, 4))
+                frac_of_peak=round(gbs / HBM_PEAK_GBS, 4),
+                copy=dict(bytes_read_and_written=nbytes // 2, us=round(copy_us, 1), gbs=round(copy_gbs, 1),
+                          frac_of_peak=round(copy_gbs / HBM_PEAK_GBS, 4)))
 
 
 def aux_cpu_baselines():
