@@ -128,6 +128,8 @@ RANDOM_CASES = [
     (2, 6, 1, [200, 300], 16, 32, 8, 0.6, 15),
     (1, 32, 8, [4097], 16, 256, 0, 1.0, 16),
     (2, 32, 8, [3000, 3001], 32, 256, 128, 0.0, 17),
+    (2, 10, 2, [900, 1500], 16, 64, 8, 0.6, 19),   # G = 5
+    (2, 14, 2, [700, 2100], 32, 128, 0, 0.7, 20),  # G = 7
 ]
 
 

@@ -112,7 +112,7 @@ def _dev_case(case):
 
 
 @pytest.mark.parametrize("window_left", [-1, 0, 5, 255, 1000])
-@pytest.mark.parametrize("hq,hkv", [(8, 2), (8, 8), (16, 2), (6, 2), (32, 2)])
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (8, 8), (16, 2), (6, 2), (32, 2), (10, 2), (14, 2)])
 def test_window_attention_matches_oracle(rect_ext, window_left, hq, hkv):
     case = syn.prefill_case(qo_lens=[1, 17, 300, 0, 64], kv_lens=[1, 40, 700, 9, 64], hq=hq,
                             hkv=hkv, seed=11 + hq + hkv)
