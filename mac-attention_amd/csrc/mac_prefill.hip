@@ -248,8 +248,11 @@ __device__ __forceinline__ int request_rows(const WindowParams& p, int b) {
 
 constexpr int kVRow = 18;  // 16-byte units per staged V row: 256 bytes + 32 of padding
 
+// Residency: the one-head-per-wave window pass fits 168 VGPRs, so it runs
+// three workgroups per CU (more waves per SIMD to overlap the softmax VALU
+// work with the MFMAs: 7% faster at GQA-4); the others need more registers.
 template <int HPW, bool kRectify>
-__global__ void __launch_bounds__(256, 2) window_kernel(WindowParams p) {
+__global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_kernel(WindowParams p) {
   // dynamic: s_boff[B + 1] row-block offsets, s_qo[B + 1] / s_kv[B + 1] the
   // request offsets (copies of qo_indptr / kv_indptr)
   extern __shared__ int s_dyn[];
