@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define MAC_ABI_VERSION 1
+#define MAC_ABI_VERSION 2
 
 #if defined(__GNUC__)
 #define MAC_API __attribute__((visibility("default")))
@@ -63,7 +63,7 @@ enum { MAC_GROUP_MAC_HIT = 0, MAC_GROUP_FULL_FALLBACK = 1, MAC_GROUP_MIXED = 2 }
  * Workspaces (caller-owned, any content on entry):
  *   match_dist f32, match_pos/match_slot i32 [N, Hq, max_match_tiles]
  *   head_* i32 [N, Hq]; group_* i32 [N, Hkv] (leading dimension may exceed N)
- *   complete_task_go/tile i32 [complete_task_len]
+ *   complete_task_go/tile i32 [complete_task_len >= 2 N Hkv + 2]
  *   task_counts i32 [>= 9]
  *   partial_o (f32, or bf16 if partial_o_is_bf16) [>= N, Hkv, max_tiles_context, G, D]
  *   partial_lse f32 [>= N, Hkv, max_tiles_context, G]
@@ -154,6 +154,16 @@ typedef struct MacDecodeArgs {
    * MAC_BENCH_EXACT_QUOTA (DECODE:5334, default 1). */
   int32_t mixed_group_fallback;
   int32_t bench_exact_quota;
+  /* The reference's phase_cycles workspace (DECODE:4751-4929), i64
+   * [phase_cycles_len >= 6] or NULL.  With debug_enabled >= 2 the step
+   * stores s_memrealtime stamps (the 100 MHz device clock, comparable across
+   * kernels and compute units) in [0..5]: [0] the step starts, [1] the ring
+   * scan of the first group is done, [2] every group is decided (the
+   * span-attention kernel starts), [3] its task plan is ready, [4] every
+   * span is attended (the merge kernel starts), [5] the first group's merge
+   * is written.  Otherwise the array is not touched. */
+  int64_t* phase_cycles;
+  int32_t phase_cycles_len;
 } MacDecodeArgs;
 
 /* Replaces mac_persistent_decode_bf16 (DECODE:4962-5524, pybind DECODE:5526-5529).

@@ -97,6 +97,15 @@ __device__ __forceinline__ float quad_sum(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Marks a loaded value as used here: code depending on it cannot be hoisted
+// above this point (the compiler would otherwise unpack a loop-invariant
+// load right after issuing it, and the in-order vmcnt wait for it would also
+// wait for nothing else in flight).
+__device__ __forceinline__ void pin_vgpr(uint4& w) {
+  asm volatile("" : "+v"(w.x), "+v"(w.y), "+v"(w.z), "+v"(w.w));
+}
+__device__ __forceinline__ void pin_vgpr(int& x) { asm volatile("" : "+v"(x)); }
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 

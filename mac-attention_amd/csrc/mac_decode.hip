@@ -98,6 +98,24 @@ struct DecideParams {
   int bench_mode, bench_exact_quota, bench_seed, bench_miss_mask, bench_layer_id;
   float bench_hit_rate, bench_hit_rate_std, bench_skip_ratio, bench_skip_ratio_std;
   float bench_match_lag_mean, bench_match_lag_std;
+  // groups of at most fuse_tokens tokens are finished by match_decide itself
+  // (attention, merge, ring row, out); group_fused[g] tells the later kernels
+  int fuse_tokens;
+  int32_t* group_fused;
+  int32_t* long_groups;  // set to 1 by every group left to span_attention
+  const uint16_t* q_post;
+  const uint16_t* k_buffer;
+  const uint16_t* v_buffer;
+  const int32_t* req_to_token;
+  const void* out_cache_loc;
+  uint16_t* ring_q;  // query_cache (written for finished groups)
+  uint16_t* attn_cache;
+  float* ring_lse;   // lse_cache
+  uint16_t* out;
+  float* out_lse;
+  float q_scale;  // sm_scale * log2(e)
+  int64_t* phase_cycles;  // stamps (debug_enabled >= 2), else NULL
+  int stamp_first;        // this launch records the step's first stamp
 };
 
 struct AttnParams {
@@ -132,6 +150,9 @@ struct AttnParams {
   long long narrow_min_tokens;    // at least this many tokens (the others return)
   int min_chunk;     // smallest chunk of the plan (tokens)
   float q_scale;  // sm_scale * log2(e)
+  const int32_t* group_fused;  // groups match_decide finished (no tasks here)
+  const int32_t* long_groups;  // 0: match_decide finished every group
+  int64_t* phase_cycles;
 };
 
 struct MergeParams {
@@ -159,6 +180,9 @@ struct MergeParams {
   int64_t o_group_stride;
   int cap;
   int F;
+  const int32_t* group_fused;
+  int32_t* long_groups;  // cleared here for the next step
+  int64_t* phase_cycles;
 };
 
 // DECODE:221-230.  A request id outside [0, R) is never ready: its ring rows
@@ -199,6 +223,415 @@ __device__ __forceinline__ uint4 load_stream16(const uint16_t* ptr) {
   return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(ptr)));
 }
 
+
+// ------------------------------------------------- MFMA block stream ----
+//
+// The K/V stream both attention paths share (span_attention for long spans,
+// match_decide for groups it finishes itself).  One 64-lane wave owns a
+// 32-token block at a time (waves take blocks wave, wave+4, ...):
+//
+//  * Loads: each 256-byte K or V row is read by 16 consecutive lanes (lane
+//    l reads 16-byte chunk l%16 of the row of token 8*(l/16) + i in load i),
+//    so every load instruction covers whole 128-byte lines, with the
+//    non-temporal policy (the rows are read once per step).  Measured on
+//    MI355X this streams ~12% faster than loading the MFMA operands straight
+//    from HBM, whose layout splits lines across instructions.  The block
+//    after the current one is always in flight in registers; its
+//    req_to_token entries are loaded one block earlier still.
+//  * The rows are staged in two 8 KiB per-wave LDS tiles, token-major, with
+//    XOR-swizzled 16-byte chunks (k_swz / v_swz below) so that the operand
+//    reads of the MFMAs hit distinct banks.
+//  * S^T[t][g] = sum_d K[t][d] Q[g][d] and O^T[d][g] += sum_t V[t][d] P[g][t]
+//    both run on v_mfma_f32_16x16x32_bf16.  MFMA row 4a + i of score tile t
+//    is token 8a + 4t + i, so the lane holding head g = l%16 ends with the
+//    scores of tokens 8q .. 8q + 7 (q = l/16): after conversion to bf16 they
+//    are the B operand of the PV product as they stand, and its A operand
+//    V^T[16 dt + g][8q .. 8q + 7] is two ds_read_b64_tr_b16 (gfx950's
+//    transposing LDS read) of the V tile.  The lane keeps its head's softmax
+//    state and 32 O^T accumulators, so the online-softmax rescale is
+//    lane-local.  Heads g >= G are zero padding rows of the 16-wide MFMA.
+//  * The Q operand (B of the score MFMAs) is read from LDS into registers
+//    once per stream: read per block, its 16 lanes of a quarter-wave hit one
+//    bank group (the rows are 256 bytes apart).
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& w) { return __builtin_bit_cast(bf16x8_t, w); }
+
+// K tile: 16-byte chunk c of token t at position c ^ k_swz(t) of its row.
+// The S^T tiles read tokens 8a + 4t + i (a, i < 4) in one instruction; this
+// swizzle puts the 16 of them on 16 different chunk positions.
+__device__ __forceinline__ int k_swz(int t) { return 4 * ((t >> 3) & 3) + (t & 3); }
+// V tile: chunk c of token t at c ^ v_swz(t).  One transposing read covers,
+// per 32-lane half, tokens 16h' + 4h + (0..3) and 16h' + 8 + 4h + (0..3)
+// (two quarter-waves) at two chunk bases and two 8-byte halves: with bit 3 of
+// the token in the swizzle the 32 lanes read 32 different 8-byte bank pairs
+// of the 64 banks.
+__device__ __forceinline__ int v_swz(int t) { return 2 * ((t & 3) | ((t >> 1) & 4)); }
+
+constexpr int kMfmaBlk = 32;  // tokens per wave block
+constexpr int kTileU4 = kMfmaBlk * 16;  // uint4 per K or V tile
+
+// Softmax state of one lane: its head's running max m (log2 units) and sum l
+// and the 32 O^T accumulators (dims 16 dt + 4 quad + r).
+struct WaveState {
+  f32x4_t acc[8];
+  float m, l;
+};
+
+__device__ __forceinline__ void state_reset(WaveState& s) {
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) s.acc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  s.m = kNegBig;
+  s.l = 0.0f;
+}
+
+// Per-lane constants of the K/V stream of one (request, KV head).
+struct KvStream {
+  const int32_t* r2t;     // req_to_token row of the request
+  int r2t_last;           // last column that may be read
+  int r2t_cols;           // positions at or past it (other than P) have no row
+  int P;                  // position of the current token (pool row cur_row)
+  int cur_row;            // out_cache_loc of the request, -1 if outside the pool
+  unsigned pool_rows;
+  bool req_ok;
+  const uint16_t* kbase;  // K / V row base of the KV head + this lane's chunk
+  const uint16_t* vbase;
+  int64_t kv_stride;      // elements between consecutive pool rows
+
+  // req_to_token entry of a position (index clamped into the row)
+  __device__ __forceinline__ int raw_row(int pos) const { return r2t[min(max(pos, 0), r2t_last)]; }
+  // Checked pool row of position pos of a range ending at `end`, given its
+  // raw entry: -1 = masked (past the range, outside the pool, or at a
+  // position the req_to_token row does not reach).
+  __device__ __forceinline__ int row_of(int pos, int end, int raw) const {
+    const bool cur = pos == P;
+    const int ph = cur ? cur_row : raw;
+    return (pos < end && req_ok && (cur || pos < r2t_cols) && static_cast<unsigned>(ph) < pool_rows) ? ph : -1;
+  }
+  __device__ __forceinline__ uint4 k_chunk(int row) const {
+    return load_stream16(kbase + static_cast<int64_t>(max(row, 0)) * kv_stride);
+  }
+  __device__ __forceinline__ uint4 v_chunk(int row) const {
+    return load_stream16(vbase + static_cast<int64_t>(max(row, 0)) * kv_stride);
+  }
+};
+
+
+__device__ __forceinline__ KvStream make_stream(const int32_t* req_to_token, int r2t_rows, int r2t_stride,
+                                                int req, int P, int64_t cur_loc, int64_t pool_tokens,
+                                                const uint16_t* k_buffer, const uint16_t* v_buffer,
+                                                int Hkv, int hkv, int col) {
+  KvStream ks;
+  ks.req_ok = req >= 0 && req < r2t_rows;
+  ks.r2t = req_to_token + static_cast<int64_t>(ks.req_ok ? req : 0) * r2t_stride;
+  ks.r2t_last = max(min(P, r2t_stride) - 1, 0);
+  ks.r2t_cols = r2t_stride;
+  ks.P = P;
+  ks.cur_row = (cur_loc >= 0 && cur_loc < pool_tokens) ? static_cast<int>(cur_loc) : -1;
+  ks.pool_rows = static_cast<unsigned>(min(pool_tokens, static_cast<int64_t>(INT_MAX)));
+  ks.kv_stride = static_cast<int64_t>(Hkv) * kHeadDim;
+  ks.kbase = k_buffer + static_cast<int64_t>(hkv) * kHeadDim + col * 8;
+  ks.vbase = v_buffer + static_cast<int64_t>(hkv) * kHeadDim + col * 8;
+  return ks;
+}
+
+// Up to three token ranges, each cut into 32-token blocks from its begin;
+// blocks are numbered across them: [0, first1) range 0, [first1, first2)
+// range 1, [first2, nblk) range 2.  Range 0 applies the per-head start mask
+// (the band of a group whose heads start at different positions).
+struct BlockList {
+  int begin0, end0, first1;
+  int begin1, end1, first2;
+  int begin2, end2, nblk;
+};
+
+__device__ __forceinline__ BlockList one_range(int a, int b) {
+  BlockList bl;
+  const int nb = ceil_div(max(b - a, 0), kMfmaBlk);
+  bl.begin0 = a;
+  bl.end0 = b;
+  bl.first1 = bl.first2 = bl.nblk = nb;
+  bl.begin1 = bl.end1 = bl.begin2 = bl.end2 = b;
+  return bl;
+}
+
+// First position and end of block v (blocks past the last one are empty).
+__device__ __forceinline__ void block_span(const BlockList& bl, int v, int& base, int& end) {
+  if (v < bl.first1) {
+    base = bl.begin0 + v * kMfmaBlk;
+    end = bl.end0;
+  } else if (v < bl.first2) {
+    base = bl.begin1 + (v - bl.first1) * kMfmaBlk;
+    end = bl.end1;
+  } else {
+    base = bl.begin2 + (v - bl.first2) * kMfmaBlk;
+    end = bl.end2;
+  }
+}
+
+// Streams this wave's blocks of `bl` into `st`; qb: this lane's Q operands
+// (k-steps 0..3).  One class (kTwoClass false): range 0 is masked per head
+// from head_begin on (a band piece); ranges 1 and 2 are not.  Two classes:
+// range 2 is the band (masked per head), and its blocks -- the last ones of
+// every wave -- accumulate into `ring`, while ranges 0 and 1 (sink and tail)
+// end in `st`.  pre0/pre1 (when not NULL): the req_to_token entries of the
+// wave's first two blocks, loaded by the caller; used for blocks outside
+// range 2.
+template <int G, bool kTwoClass>
+__device__ __forceinline__ void stream_blocks(const KvStream& ks, const BlockList& bl, int head_begin,
+                                              float q_scale, const bf16x8_t (&qb)[4], uint4* s_kw,
+                                              uint4* s_vw, WaveState& st, WaveState& ring,
+                                              const int* pre0 = nullptr, const int* pre1 = nullptr) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int quad = lane >> 4;
+  const int col = lane & 15;
+  const bool head_ok = col < G;
+  const uint16_t* vtile = reinterpret_cast<const uint16_t*>(s_vw);
+
+  // raw_row() only issues the req_to_token load; phys_ok() checks it one
+  // block later, so waiting for it never drains the K/V loads issued after it.
+  auto raw_row = [&](int pos) -> int { return ks.raw_row(pos); };
+  auto phys_ok = [&](int pos, int end, int raw) -> int { return ks.row_of(pos, end, raw); };
+
+  uint4 kr[8], vr[8];  // rows of tokens 8*quad + i, chunk col (next block)
+  int ph[8];           // checked rows of the block in flight
+  int raw[8];          // raw rows of the block after it
+  auto issue = [&](const int (&rows)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vr[i] = ks.v_chunk(rows[i]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kr[i] = ks.k_chunk(rows[i]);
+  };
+  {
+    int b0, e0, b1, e1;
+    block_span(bl, wave, b0, e0);
+    block_span(bl, wave + kWaves, b1, e1);
+    const bool use0 = pre0 != nullptr && (!kTwoClass || wave < bl.first2);
+    const bool use1 = pre1 != nullptr && (!kTwoClass || wave + kWaves < bl.first2);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ph[i] = phys_ok(b0 + 8 * quad + i, e0, use0 ? pre0[i] : raw_row(b0 + 8 * quad + i));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) raw[i] = use1 ? pre1[i] : raw_row(b1 + 8 * quad + i);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(ph);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  bool switched = false;
+  const int my_blocks = wave < bl.nblk ? ceil_div(bl.nblk - wave, kWaves) : 0;
+  for (int k = 0; k < my_blocks; ++k) {
+    const int v = wave + kWaves * k;
+    if (kTwoClass && !switched && v >= bl.first2) {  // sink and tail done: st -> ring for the band
+      ring = st;
+      state_reset(st);
+      switched = true;
+    }
+    int base, end_unused, b1, e1, b2, e2;
+    block_span(bl, v, base, end_unused);
+    block_span(bl, v + kWaves, b1, e1);
+    block_span(bl, v + 2 * kWaves, b2, e2);
+    const int hb = (kTwoClass ? v >= bl.first2 : v < bl.first1) ? head_begin : 0;
+    int nph[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) nph[i] = phys_ok(b1 + 8 * quad + i, e1, raw[i]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) raw[i] = raw_row(b2 + 8 * quad + i);
+    __builtin_amdgcn_sched_barrier(0);
+    // token validity of this block: bit t set if token t has a row
+    uint32_t vmask = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint64_t bal = __ballot(ph[i] >= 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) vmask |= static_cast<uint32_t>((bal >> (16 * r)) & 1) << (8 * r + i);
+    }
+    // stage K and V rows (V of masked tokens zeroed) into the wave's tiles
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int tok = 8 * quad + i;
+      const uint32_t keep = ph[i] >= 0 ? 0xffffffffu : 0u;
+      uint4 w = vr[i];
+      w.x &= keep;
+      w.y &= keep;
+      w.z &= keep;
+      w.w &= keep;
+      s_kw[tok * 16 + (col ^ k_swz(tok))] = kr[i];
+      s_vw[tok * 16 + (col ^ v_swz(tok))] = w;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the next block's rows go in flight while this block is computed
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ph[i] = nph[i];
+    issue(ph);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // S^T = K Q^T for the block's 32 tokens
+    f32x4_t sc[2];
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile) {
+      f32x4_t c4 = {0.0f, 0.0f, 0.0f, 0.0f};
+      const int tok = 8 * (col >> 2) + 4 * tile + (col & 3);  // MFMA row col of this tile
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(s_kw[tok * 16 + ((4 * s + quad) ^ k_swz(tok))]),
+                                                    qb[s], c4, 0, 0, 0);
+      sc[tile] = c4;
+    }
+
+    // scale, mask, online softmax (lane-local except the block max)
+    float sv[8];
+    float bmax = kNegBig;
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tok = 8 * quad + 4 * tile + r;
+        const bool ok = head_ok && ((vmask >> tok) & 1) && base + tok >= hb;
+        const float x = ok ? sc[tile][r] * q_scale : -INFINITY;
+        sv[4 * tile + r] = x;
+        bmax = fmaxf(bmax, x);
+      }
+    }
+    bmax = quad_max(bmax);
+    // Lazy rescale: the reference point m only moves when the block max
+    // exceeds it by more than kRescaleSlack (log2 units), so most blocks
+    // skip the 32-accumulator rescale; p <= 2^kRescaleSlack stays exact in
+    // fp32 and well inside bf16 range.
+    constexpr float kRescaleSlack = 8.0f;
+    if (__any(bmax > st.m + kRescaleSlack)) {
+      const float m_new = fmaxf(st.m, bmax);
+      const float alpha = fast_exp2(st.m - m_new);
+      st.m = m_new;
+      st.l *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) st.acc[dt] *= alpha;
+    }
+    bf16x8_t pb;
+    float psum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float pe = fast_exp2(sv[e] - st.m);
+      psum += pe;
+      pb[e] = static_cast<__bf16>(pe);
+    }
+    st.l += psum;
+    // O^T += V^T P^T: the A operand V^T[16 dt + col][tokens 8 quad .. +8]
+    // is two transposing reads of tokens 8 quad + 4 h + (col >> 2), dims
+    // 16 dt + 4 (col & 3) .. +3 (16-byte chunk 2 dt + ((col & 3) >> 1))
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      bf16x4_t part[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int t = 8 * quad + 4 * h + (col >> 2);
+        const int c = (2 * dt + ((col & 3) >> 1)) ^ v_swz(t);
+        part[h] = lds_read_tr16(vtile + t * 128 + c * 8 + (col & 1) * 4);
+      }
+      const bf16x8_t va = __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7);
+      st.acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, st.acc[dt], 0, 0, 0);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  }
+  if (kTwoClass) {  // st: band blocks (if any), ring: sink and tail -> swap
+    if (switched) {
+      const WaveState t = st;
+      st = ring;
+      ring = t;
+    } else {
+      state_reset(ring);
+    }
+  }
+  st.l = quad_sum(st.l);
+  if (kTwoClass) ring.l = quad_sum(ring.l);
+}
+
+// This lane's Q operands of the score MFMAs from the 16 x 128 Q tile in LDS
+// (rows g >= G zero): k-step s reads Q[col][8 (4 s + quad) .. + 8].
+__device__ __forceinline__ void load_q_operands(const uint4* s_q, bf16x8_t (&qb)[4]) {
+  const int lane = threadIdx.x & 63;
+  const int quad = lane >> 4, col = lane & 15;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) qb[s] = as_bf16x8(s_q[col * 16 + 4 * s + quad]);
+}
+
+// Stores this lane's part of a wave state into the LDS combine area:
+// so[wave][head][dim] (row pitch kOPitch floats), sml[wave][head] = (m, l).
+constexpr int kOPitch = kHeadDim + 4;  // padded: lanes of different heads hit different banks
+template <int G>
+__device__ __forceinline__ void state_to_lds(const WaveState& st, float* so, float* sml) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int quad = lane >> 4, col = lane & 15;
+  if (col < G) {
+    float* row = so + (wave * G + col) * kOPitch;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) row[16 * dt + 4 * quad + r] = st.acc[dt][r];
+    if (quad == 0) {
+      sml[(wave * G + col) * 2] = st.m;
+      sml[(wave * G + col) * 2 + 1] = st.l;
+    }
+  }
+}
+
+// Normalised (o[d], o[d+1], natural-log lse) of head h from the four wave
+// states in LDS; lse = -inf and o = 0 for an empty state.
+template <int G>
+__device__ __forceinline__ void combine_waves(const float* so, const float* sml, int h, int d, float& o0,
+                                              float& o1, float& lse) {
+  float mm = kNegBig;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, sml[(w * G + h) * 2]);
+  float ll = 0.0f, a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const float sc = fast_exp2(sml[(w * G + h) * 2] - mm);
+    ll += sml[(w * G + h) * 2 + 1] * sc;
+    a0 += so[(w * G + h) * kOPitch + d] * sc;
+    a1 += so[(w * G + h) * kOPitch + d + 1] * sc;
+  }
+  const bool nonempty = ll > 0.0f;
+  const float inv = nonempty ? 1.0f / ll : 0.0f;
+  o0 = a0 * inv;
+  o1 = a1 * inv;
+  lse = nonempty ? (mm + log2f(ll)) * kLn2 : -INFINITY;
+}
+
+// LSE merge of (lse2, o0, o1) into st (natural log).  An operand with a
+// non-finite lse is empty and skipped (DECODE:866-890).
+struct MergeState {
+  float lse;   // natural log; -inf = empty
+  float o[2];  // normalised output of the owned dims
+};
+
+__device__ __forceinline__ void merge_into(MergeState& st, float lse2, float o0, float o1) {
+  if (!isfinite(lse2)) return;
+  if (!isfinite(st.lse)) {
+    st.lse = lse2;
+    st.o[0] = o0;
+    st.o[1] = o1;
+    return;
+  }
+  const float mx = fmaxf(st.lse, lse2);
+  const float w1 = __expf(st.lse - mx), w2 = __expf(lse2 - mx);
+  const float inv = 1.0f / (w1 + w2);
+  st.o[0] = (w1 * st.o[0] + w2 * o0) * inv;
+  st.o[1] = (w1 * st.o[1] + w2 * o1) * inv;
+  st.lse = mx + __logf(w1 + w2);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+}
+
 // =========================================================== 1. decide ====
 
 // Lanes of a wave form four rows of 16; row r of pass p scans query head
@@ -217,237 +650,20 @@ constexpr int kSplitSlots = 256;
 constexpr int kLsePrefetchSlots = 64;
 constexpr int kProbeSlots = 4;  // probe scan: slot pairs per lane batch and pass
 
+// Per-head decisions and group spans of group g (wave 0; lanes 0..G-1 own a
+// head each), DECODE:1147-1402.  Publishes in LDS what fused_group needs:
+// per head its band start, the slot of a reusable cached entry (-1: none)
+// and that entry's lse; the group's band begin, new_end and whether
+// match_decide finishes the group itself.
 template <int G, int kMode>
-__global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
-  constexpr int kPasses = (G + 3) / 4;
-  constexpr int kSlotBatch = 16 / kPasses;  // 16 row loads in flight per lane
-  const int g = blockIdx.x;
-  const int n = g / p.s.Hkv;
-  const int hkv = g - n * p.s.Hkv;
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int row = lane >> 4;
-  const int c = lane & 15;
+__device__ __forceinline__ void decide_group(const DecideParams& p, const float (*s_d)[kMaxGroup],
+                                             const int (*s_p)[kMaxGroup], const int (*s_s)[kMaxGroup],
+                                             const float (*s_lse)[kLsePrefetchSlots], bool lse_in_lds, int g,
+                                             int n, int hkv, int P, int req, bool eligible, int* s_rect,
+                                             int* s_mslot, float* s_entry, int* s_span) {
+  const int lane = threadIdx.x & 63;
   const int M = p.s.M;
   const int Hq = p.s.Hq;
-
-  const int P = p.past_lens[n];
-  const int req = p.req_ids[n];
-  const bool ready = request_ready(p.cache_ready, p.cache_epoch, p.request_epoch, req, p.s.R);
-  // DECODE:974-981
-  const int cand_begin = max(0, P - M);
-  int cand_end = P;
-  if (p.candidate_mode == 1) cand_end = max(cand_begin, P - p.lookback_right);
-  const bool eligible = P >= p.gen_min_limit && cand_end > cand_begin && ready;
-
-  __shared__ float s_d[kWaves][kMaxGroup];
-  __shared__ int s_p[kWaves][kMaxGroup];
-  __shared__ int s_s[kWaves][kMaxGroup];
-  __shared__ float s_lse[kMaxGroup][kLsePrefetchSlots];  // lse of every slot (small rings)
-
-  // Every load of the scan is independent of the readiness gate and of the
-  // other loads (a request id outside [0, R) reads request 0's rows, and the
-  // results are masked), so the kernel waits for one round of loads, not a
-  // chain.  For rings of at most kLsePrefetchSlots slots the entries' lse
-  // are fetched in the same round, so the decision reads them from LDS.
-  const bool req_ok = req >= 0 && req < p.s.R;
-  const int64_t cache_req = static_cast<int64_t>(req_ok ? req : 0) * M;
-  const bool lse_in_lds = kMode == 0 && M <= kLsePrefetchSlots;
-  if (lse_in_lds && wave == 0 && lane < M) {
-#pragma unroll
-    for (int hh = 0; hh < G; ++hh) s_lse[hh][lane] = p.lse_cache[(cache_req + lane) * Hq + hkv * G + hh];
-  }
-
-  float best_d[kPasses];
-  int best_p[kPasses], best_s[kPasses];
-  float q[kPasses][8];
-#pragma unroll
-  for (int ps = 0; ps < kPasses; ++ps) {
-    best_d[ps] = INFINITY;
-    best_p[ps] = INT_MAX;
-    best_s[ps] = -1;
-    const int hl = row + 4 * ps;
-    uint4 w = make_uint4(0, 0, 0, 0);
-    if (hl < G) {
-      const int64_t off = (static_cast<int64_t>(n) * Hq + hkv * G + hl) * kHeadDim + c * 8;
-      w = *reinterpret_cast<const uint4*>(p.q_pre + off);
-    }
-    unpack8(w, q[ps]);
-  }
-
-  const int per_split = ceil_div(M, p.splits);
-  const int s_lo = kMode == 1 ? static_cast<int>(blockIdx.y) * per_split : 0;
-  const int s_hi = kMode == 1 ? min(M, s_lo + per_split) : M;
-  if (kMode == 1 && p.probe != 0) {
-    // Probe scan (the reference's default, DECODE:1001-1075).  The squared
-    // distance over dims [0, 64) is a lower bound of the full one, so a slot
-    // whose probe exceeds thr_dist (plus a relative slack of 1e-4, far above
-    // the rounding of a 128-term fp32 sum) cannot be a hit and its second
-    // half-row is not fetched; every other slot gets its full distance.
-    // Hit decisions are those of the full scan; only the best distance of a
-    // head without a hit may differ.  Lane (row, c) takes slot 2u + (c >> 3)
-    // of the batch and 16-byte chunk (c & 7) of its first half, then chunk
-    // 8 + (c & 7) -- or, for a pruned slot, a chunk of its head's query row,
-    // a cache hit instead of HBM traffic (no divergent loads); a batch the
-    // whole wave pruned skips the second round.  Ring rows are read once per
-    // step, with the non-temporal policy.
-    constexpr int kProbeBatch = kProbeSlots / kPasses;  // slot pairs per lane batch
-    const int half = c >> 3, cc = c & 7;
-    float qa[kPasses][8], qb[kPasses][8];
-#pragma unroll
-    for (int ps = 0; ps < kPasses; ++ps) {
-      const int hl = min(row + 4 * ps, G - 1);
-      const uint16_t* qp = p.q_pre + (static_cast<int64_t>(n) * Hq + hkv * G + hl) * kHeadDim + cc * 8;
-      unpack8(*reinterpret_cast<const uint4*>(qp), qa[ps]);
-      unpack8(*reinterpret_cast<const uint4*>(qp + 64), qb[ps]);
-    }
-    const float thr_prune = p.thr_dist + fabsf(p.thr_dist) * 1e-4f + 1e-4f;
-    for (int s0 = s_lo + wave; s0 < s_hi; s0 += kWaves * 2 * kProbeBatch) {
-      int pos[kProbeBatch], slot[kProbeBatch];
-      bool in_window[kProbeBatch];
-#pragma unroll
-      for (int u = 0; u < kProbeBatch; ++u) {
-        slot[u] = s0 + (2 * u + half) * kWaves;
-        pos[u] = ring_slot_to_pos(P, M, slot[u]);
-        in_window[u] = eligible && slot[u] < s_hi && pos[u] >= cand_begin && pos[u] < cand_end;
-      }
-      uint4 w[kPasses][kProbeBatch];
-#pragma unroll
-      for (int ps = 0; ps < kPasses; ++ps) {
-        const int hl = min(row + 4 * ps, G - 1);
-#pragma unroll
-        for (int u = 0; u < kProbeBatch; ++u) {
-          const int64_t off = ((cache_req + min(slot[u], s_hi - 1)) * Hq + hkv * G + hl) * kHeadDim + cc * 8;
-          w[ps][u] = load_stream16(p.query_cache + off);  // read once: no cache pollution
-        }
-      }
-      float acc[kPasses][kProbeBatch];
-      bool eval[kPasses][kProbeBatch];
-#pragma unroll
-      for (int ps = 0; ps < kPasses; ++ps)
-#pragma unroll
-        for (int u = 0; u < kProbeBatch; ++u) {
-          float cf[8];
-          unpack8(w[ps][u], cf);
-          float a = 0.0f;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const float df = qa[ps][i] - cf[i];
-            a = fmaf(df, df, a);
-          }
-          acc[ps][u] = a;
-          eval[ps][u] = in_window[u] && row + 4 * ps < G && row8_sum(a) <= thr_prune;
-        }
-      bool any_eval = false;
-#pragma unroll
-      for (int ps = 0; ps < kPasses; ++ps)
-#pragma unroll
-        for (int u = 0; u < kProbeBatch; ++u) any_eval |= eval[ps][u];
-      if (!__any(any_eval)) continue;  // the whole batch pruned (the common case): no second half-rows
-#pragma unroll
-      for (int ps = 0; ps < kPasses; ++ps) {
-        const int hl = min(row + 4 * ps, G - 1);
-#pragma unroll
-        for (int u = 0; u < kProbeBatch; ++u) {
-          // a pruned slot's lanes read their head's query row instead (hot in
-          // the cache: every workgroup of the group reads it); the value is unused
-          const uint16_t* src =
-              eval[ps][u] ? p.query_cache + ((cache_req + min(slot[u], s_hi - 1)) * Hq + hkv * G + hl) * kHeadDim + 64 + cc * 8
-                          : p.q_pre + (static_cast<int64_t>(n) * Hq + hkv * G + hl) * kHeadDim + cc * 8;
-          w[ps][u] = load_stream16(src);
-        }
-      }
-#pragma unroll
-      for (int ps = 0; ps < kPasses; ++ps)
-#pragma unroll
-        for (int u = 0; u < kProbeBatch; ++u) {
-          float cf[8];
-          unpack8(w[ps][u], cf);
-          float b = acc[ps][u];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const float df = qb[ps][i] - cf[i];
-            b = fmaf(df, df, b);
-          }
-          const float d = row8_sum(b);
-          if (eval[ps][u] && better_pair(d, pos[u], best_d[ps], best_p[ps])) {
-            best_d[ps] = d;
-            best_p[ps] = pos[u];
-            best_s[ps] = slot[u];
-          }
-        }
-    }
-    // the two half-rows of lanes tracked different slots: lane c takes the
-    // better of its own and lane c ^ 8's
-#pragma unroll
-    for (int ps = 0; ps < kPasses; ++ps) {
-      const float od = __shfl_xor(best_d[ps], 8);
-      const int op = __shfl_xor(best_p[ps], 8), os = __shfl_xor(best_s[ps], 8);
-      if (better_pair(od, op, best_d[ps], best_p[ps])) {
-        best_d[ps] = od;
-        best_p[ps] = op;
-        best_s[ps] = os;
-      }
-    }
-  } else if (kMode != 2) {
-    for (int s0 = s_lo + wave; s0 < s_hi; s0 += kWaves * kSlotBatch) {
-      // every pass's loads of the batch are in flight before any reduction
-      uint4 w[kPasses][kSlotBatch];
-      int pos[kSlotBatch];
-      bool in_window[kSlotBatch];
-#pragma unroll
-      for (int u = 0; u < kSlotBatch; ++u) {
-        const int slot = s0 + u * kWaves;
-        pos[u] = ring_slot_to_pos(P, M, slot);
-        in_window[u] = eligible && slot < s_hi && pos[u] >= cand_begin && pos[u] < cand_end;
-      }
-#pragma unroll
-      for (int ps = 0; ps < kPasses; ++ps) {
-        const int hl = min(row + 4 * ps, G - 1);
-#pragma unroll
-        for (int u = 0; u < kSlotBatch; ++u) {
-          const int slot = min(s0 + u * kWaves, s_hi - 1);  // past the range: re-reads its last row
-          const int64_t off = ((cache_req + slot) * Hq + hkv * G + hl) * kHeadDim + c * 8;
-          w[ps][u] = load_stream16(p.query_cache + off);  // ring rows are read once per step
-        }
-      }
-#pragma unroll
-      for (int ps = 0; ps < kPasses; ++ps) {
-        const int hl = row + 4 * ps;
-#pragma unroll
-        for (int u = 0; u < kSlotBatch; ++u) {
-          float cf[8];
-          unpack8(w[ps][u], cf);
-          float acc = 0.0f;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const float df = q[ps][i] - cf[i];
-            acc = fmaf(df, df, acc);
-          }
-          acc = row16_sum(acc);
-          if (in_window[u] && hl < G && better_pair(acc, pos[u], best_d[ps], best_p[ps])) {
-            best_d[ps] = acc;
-            best_p[ps] = pos[u];
-            best_s[ps] = s0 + u * kWaves;
-          }
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int ps = 0; ps < kPasses; ++ps) {
-    const int hl = row + 4 * ps;
-    if (c == 0 && hl < G) {
-      s_d[wave][hl] = best_d[ps];
-      s_p[wave][hl] = best_p[ps];
-      s_s[wave][hl] = best_s[ps];
-    }
-  }
-  __syncthreads();
-  if (wave != 0) return;
-
-  // ---- per-head decisions (lanes 0..G-1 of wave 0), DECODE:1147-1299 ----
   const int h = lane;
   const bool head_lane = h < G;
   const int hq = hkv * G + (head_lane ? h : 0);
@@ -461,6 +677,11 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
         bs = s_s[w][h];
       }
     }
+  }
+  if (!eligible) {  // the readiness gate and the candidate window, applied after the scan
+    bd = INFINITY;
+    bp = INT_MAX;
+    bs = -1;
   }
   const int64_t ho = static_cast<int64_t>(n) * Hq + hq;
   const int64_t mo = ho * p.s.max_match_tiles;
@@ -566,8 +787,9 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
   const int fs_begin = min(F, new_end);
   // DECODE:1315-1328 validity of a hit head for MAC reuse
   bool valid = false;
+  float pl = -INFINITY;
   if (head_lane && hit && mslot >= 0) {
-    const float pl = lse_in_lds ? s_lse[h][mslot] : p.lse_cache[(static_cast<int64_t>(req) * M + mslot) * Hq + hq];
+    pl = lse_in_lds ? s_lse[h][mslot] : p.lse_cache[(static_cast<int64_t>(req) * M + mslot) * Hq + hq];
     const int clen = new_end - prefix_end;
     valid = isfinite(pl) && clen >= 0 && clen <= M;
   }
@@ -600,6 +822,14 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
     p.head_new_end[ho] = new_end;
   }
   if (lane == 0 && g == 0) *p.task_counter = 0;
+  // a group of few tokens is finished by this kernel (no tasks, no merge)
+  const long long tokens = static_cast<long long>(fs_begin) + (new_end - rb) + max(P + 1 - new_end, 0);
+  const int fused = (p.fuse_tokens > 0 && tokens <= p.fuse_tokens) ? 1 : 0;
+  if (head_lane) {
+    s_rect[h] = rect_start;
+    s_mslot[h] = hit ? mslot : -1;
+    s_entry[h] = hit ? pl : -INFINITY;
+  }
   if (lane == 0) {
     const int64_t go = static_cast<int64_t>(n) * p.s.Hkv + hkv;
     p.group_mode[go] = mode;
@@ -607,6 +837,427 @@ __global__ void __launch_bounds__(kBlock) match_decide_kernel(DecideParams p) {
     p.group_rect_end[go] = new_end;
     p.group_tail_begin[go] = new_end;
     p.group_tail_end[go] = P + 1;
+    p.group_fused[g] = fused;
+    if (!fused) *p.long_groups = 1;
+    s_span[0] = rb;
+    s_span[1] = new_end;
+    s_span[2] = fused;
+  }
+}
+
+// The decision-independent part of a group's blocks: sink [0, min(F,
+// new_end)) as range 0 and tail [new_end, P + 1) as range 1 (range 2 empty).
+__device__ __forceinline__ BlockList rest_blocks(int P, int new_end, int F) {
+  BlockList bl;
+  const int sink_end = min(F, new_end);
+  bl.begin0 = 0;
+  bl.end0 = sink_end;
+  bl.first1 = ceil_div(max(sink_end, 0), kMfmaBlk);
+  bl.begin1 = new_end;
+  bl.end1 = P + 1;
+  bl.first2 = bl.first1 + ceil_div(max(P + 1 - new_end, 0), kMfmaBlk);
+  bl.begin2 = bl.end2 = new_end;
+  bl.nblk = bl.first2;
+  return bl;
+}
+
+// A group of few tokens (at most fuse_tokens: in practice the hit groups,
+// whose band is at most the ring capacity, and short requests) is finished
+// by the workgroup that decided it: its sink, band and tail are streamed by
+// the four waves (band blocks first, so each wave's band state is complete
+// when it reaches its first sink or tail block), the wave states are combined
+// in LDS, and the merge of DECODE:4280-4685 follows in place -- ring state =
+// cached entry (+) band -> ring row at past_len % M (ready requests only);
+// out = ring state (+) sink (+) tail -- with no partials, no task and no
+// merge launch for the group.
+template <int G>
+__device__ __forceinline__ void fused_group(const DecideParams& p, int n, int hkv, int P, int req, bool ready,
+                                            int band_begin, int new_end, const int* s_rect,
+                                            const int* s_mslot, const float* s_entry, uint4 qpost_w,
+                                            const KvStream& ks, const int (&pre)[2][8]) {
+  constexpr int kPairs = (G * 64 + kBlock - 1) / kBlock;  // dim pairs per thread in the epilogue
+  __shared__ uint4 s_kv[2][kWaves][kTileU4];  // K and V tiles; the combine area afterwards
+  __shared__ uint4 s_q[16 * 16];
+  __shared__ float s_ml[2][kWaves][G][2];
+  static_assert(sizeof(float) * 2 * kWaves * G * kOPitch <= sizeof(s_kv), "combine area");
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = tid & 15;
+  const int Hq = p.s.Hq;
+  const int M = p.s.M;
+  const bool req_ok = req >= 0 && req < p.s.R;
+
+  s_q[tid] = qpost_w;
+  // the cached entries (hit heads) and the pre-RoPE query rows of the
+  // epilogue, in flight during the stream
+  uint32_t ent[kPairs], qpre[kPairs];
+#pragma unroll
+  for (int i = 0; i < kPairs; ++i) {
+    const int e = tid + i * kBlock;
+    ent[i] = 0;
+    qpre[i] = 0;
+    if (e < G * 64) {
+      const int h = e >> 6, d0 = 2 * (e & 63), hq = hkv * G + h;
+      const int ms = s_mslot[h];
+      if (ms >= 0 && req_ok)
+        ent[i] = *reinterpret_cast<const uint32_t*>(p.attn_cache +
+                                                    ((static_cast<int64_t>(req) * M + ms) * Hq + hq) * kHeadDim + d0);
+      qpre[i] = *reinterpret_cast<const uint32_t*>(p.q_pre + (static_cast<int64_t>(n) * Hq + hq) * kHeadDim + d0);
+    }
+  }
+  __syncthreads();
+  bf16x8_t qb[4];
+  load_q_operands(s_q, qb);
+
+  // blocks: sink [0, min(F, new_end)), tail [new_end, P + 1), band [band_begin, new_end)
+  BlockList bl = rest_blocks(P, new_end, p.F);
+  bl.begin2 = band_begin;
+  bl.end2 = new_end;
+  bl.nblk = bl.first2 + ceil_div(max(new_end - band_begin, 0), kMfmaBlk);
+  WaveState rest, ring;
+  state_reset(rest);
+  state_reset(ring);
+  stream_blocks<G, true>(ks, bl, col < G ? s_rect[col] : 0, p.q_scale, qb, &s_kv[0][wave][0],
+                         &s_kv[1][wave][0], rest, ring, pre[0], pre[1]);
+  __syncthreads();  // every wave is done with its tiles
+  float* so = reinterpret_cast<float*>(&s_kv[0][0][0]);
+  state_to_lds<G>(ring, so, &s_ml[0][0][0][0]);
+  state_to_lds<G>(rest, so + kWaves * G * kOPitch, &s_ml[1][0][0][0]);
+  __syncthreads();
+
+  const int dest = P % M;
+#pragma unroll
+  for (int i = 0; i < kPairs; ++i) {
+    const int e = tid + i * kBlock;
+    if (e >= G * 64) break;
+    const int h = e >> 6, d0 = 2 * (e & 63), hq = hkv * G + h;
+    const int64_t ho = static_cast<int64_t>(n) * Hq + hq;
+    MergeState st{-INFINITY, {0.0f, 0.0f}};
+    float o0, o1, l;
+    combine_waves<G>(so, &s_ml[0][0][0][0], h, d0, o0, o1, l);
+    merge_into(st, l, o0, o1);
+    merge_into(st, s_entry[h], bf16_lo(ent[i]), bf16_hi(ent[i]));
+    if (ready && P >= 0) {  // ring row (a negative past_len has no ring slot)
+      const int64_t rowi = (static_cast<int64_t>(req) * M + dest) * Hq + hq;
+      const bool valid = isfinite(st.lse);
+      *reinterpret_cast<uint32_t*>(p.ring_q + rowi * kHeadDim + d0) = qpre[i];
+      *reinterpret_cast<uint32_t*>(p.attn_cache + rowi * kHeadDim + d0) = valid ? pack_bf16x2(st.o[0], st.o[1]) : 0u;
+      if (d0 == 0) p.ring_lse[rowi] = valid ? st.lse : -INFINITY;
+    }
+    combine_waves<G>(so + kWaves * G * kOPitch, &s_ml[1][0][0][0], h, d0, o0, o1, l);
+    merge_into(st, l, o0, o1);
+    const bool valid = isfinite(st.lse);
+    *reinterpret_cast<uint32_t*>(p.out + ho * kHeadDim + d0) = valid ? pack_bf16x2(st.o[0], st.o[1]) : 0u;
+    if (p.out_lse != nullptr && d0 == 0) p.out_lse[ho] = valid ? st.lse : -INFINITY;
+  }
+}
+
+template <int G, int kMode>
+__global__ void __launch_bounds__(kBlock, 2) match_decide_kernel(DecideParams p) {
+  constexpr int kPasses = (G + 3) / 4;
+  constexpr int kSlotBatch = 16 / kPasses;  // 16 row loads in flight per lane
+  const int g = blockIdx.x;
+  const int n = g / p.s.Hkv;
+  const int hkv = g - n * p.s.Hkv;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int row = lane >> 4;
+  const int c = lane & 15;
+  const int M = p.s.M;
+  const int Hq = p.s.Hq;
+
+  const int P = p.past_lens[n];
+  const int req = p.req_ids[n];
+  // DECODE:974-981; the readiness gate (a load of its own) is applied after
+  // the scan's loads are in flight
+  const int cand_begin = max(0, P - M);
+  int cand_end = P;
+  if (p.candidate_mode == 1) cand_end = max(cand_begin, P - p.lookback_right);
+  const bool cand_ok = P >= p.gen_min_limit && cand_end > cand_begin;
+
+  __shared__ float s_d[kWaves][kMaxGroup];
+  __shared__ int s_p[kWaves][kMaxGroup];
+  __shared__ int s_s[kWaves][kMaxGroup];
+  __shared__ float s_lse[kMaxGroup][kLsePrefetchSlots];  // lse of every slot (small rings)
+
+  // Every load of the scan is independent of the readiness gate and of the
+  // other loads (a request id outside [0, R) reads request 0's rows, and the
+  // results are masked), so the kernel waits for one round of loads, not a
+  // chain.  For rings of at most kLsePrefetchSlots slots the entries' lse
+  // are fetched in the same round, so the decision reads them from LDS.
+  float best_d[kPasses];
+  int best_p[kPasses], best_s[kPasses];
+  uint4 qw[kPasses];  // this lane's chunk of its heads' pre-RoPE queries, unpacked where used
+#pragma unroll
+  for (int ps = 0; ps < kPasses; ++ps) {
+    best_d[ps] = INFINITY;
+    best_p[ps] = INT_MAX;
+    best_s[ps] = -1;
+    const int hl = row + 4 * ps;
+    qw[ps] = make_uint4(0, 0, 0, 0);
+    if (kMode != 2 && hl < G) {
+      const int64_t off = (static_cast<int64_t>(n) * Hq + hkv * G + hl) * kHeadDim + c * 8;
+      qw[ps] = *reinterpret_cast<const uint4*>(p.q_pre + off);
+    }
+  }
+
+  if (p.phase_cycles != nullptr && p.stamp_first && g == 0 && tid == 0 && blockIdx.y == 0)
+    p.phase_cycles[0] = static_cast<int64_t>(wall_clock64());
+  // the post-RoPE query tile of a group this kernel may finish (rows g >= G
+  // zero), loaded with the scan's round
+  // Loads a group this kernel may finish needs (issued unconditionally and
+  // consumed only after the decision, so that no wait for them precedes the
+  // scan's loads): the post-RoPE query tile (rows >= G zeroed when stored),
+  // the current token's pool row (as two 32-bit words) and the req_to_token
+  // entries of this wave's first two sink / tail blocks.
+  uint4 qpost_w = make_uint4(0, 0, 0, 0);
+  int cur_lo = -1, cur_hi = -1;
+  int pre[2][8];
+  KvStream ks{};
+  if constexpr (kMode != 1) {
+    qpost_w = *reinterpret_cast<const uint4*>(
+        p.q_post + (static_cast<int64_t>(n) * Hq + hkv * G + min(tid >> 4, G - 1)) * kHeadDim + (tid & 15) * 8);
+    const int32_t* ocl = static_cast<const int32_t*>(p.out_cache_loc);
+    const int64_t w0 = p.s.out_cache_loc_is_i64 ? 2 * static_cast<int64_t>(n) : n;
+    cur_lo = ocl[w0];
+    cur_hi = ocl[p.s.out_cache_loc_is_i64 ? w0 + 1 : w0];
+    ks = make_stream(p.req_to_token, p.s.r2t_rows, p.s.r2t_stride, req, P, -1, p.s.pool_tokens, p.k_buffer,
+                     p.v_buffer, p.s.Hkv, hkv, c);
+    const BlockList rblk = rest_blocks(P, cache_end_for_pos(P, p.S), p.F);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      int base, end;
+      block_span(rblk, wave + kWaves * u, base, end);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pre[u][i] = ks.raw_row(base + 8 * row + i);
+    }
+  }
+  const bool req_ok = req >= 0 && req < p.s.R;
+  const int64_t cache_req = static_cast<int64_t>(req_ok ? req : 0) * M;
+  const bool lse_in_lds = kMode == 0 && M <= kLsePrefetchSlots;
+  float lse_reg[G];  // stored to s_lse once the scan's loads are in flight
+  if (lse_in_lds && wave == 0 && lane < M) {
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) lse_reg[hh] = p.lse_cache[(cache_req + lane) * Hq + hkv * G + hh];
+  }
+
+  const int per_split = ceil_div(M, p.splits);
+  const int s_lo = kMode == 1 ? static_cast<int>(blockIdx.y) * per_split : 0;
+  const int s_hi = kMode == 1 ? min(M, s_lo + per_split) : M;
+  if (kMode == 1 && p.probe != 0) {
+    // Probe scan (the reference's default, DECODE:1001-1075).  The squared
+    // distance over dims [0, 64) is a lower bound of the full one, so a slot
+    // whose probe exceeds thr_dist (plus a relative slack of 1e-4, far above
+    // the rounding of a 128-term fp32 sum) cannot be a hit and its second
+    // half-row is not fetched; every other slot gets its full distance.
+    // Hit decisions are those of the full scan; only the best distance of a
+    // head without a hit may differ.  Lane (row, c) takes slot 2u + (c >> 3)
+    // of the batch and 16-byte chunk (c & 7) of its first half, then chunk
+    // 8 + (c & 7) -- or, for a pruned slot, a chunk of its head's query row,
+    // a cache hit instead of HBM traffic (no divergent loads); a batch the
+    // whole wave pruned skips the second round.  Ring rows are read once per
+    // step, with the non-temporal policy.
+    constexpr int kProbeBatch = kProbeSlots / kPasses;  // slot pairs per lane batch
+    const int half = c >> 3, cc = c & 7;
+    uint4 qaw[kPasses], qbw[kPasses];  // unpacked where used
+#pragma unroll
+    for (int ps = 0; ps < kPasses; ++ps) {
+      const int hl = min(row + 4 * ps, G - 1);
+      const uint16_t* qp = p.q_pre + (static_cast<int64_t>(n) * Hq + hkv * G + hl) * kHeadDim + cc * 8;
+      qaw[ps] = *reinterpret_cast<const uint4*>(qp);
+      qbw[ps] = *reinterpret_cast<const uint4*>(qp + 64);
+    }
+    const float thr_prune = p.thr_dist + fabsf(p.thr_dist) * 1e-4f + 1e-4f;
+    for (int s0 = s_lo + wave; s0 < s_hi; s0 += kWaves * 2 * kProbeBatch) {
+      int pos[kProbeBatch], slot[kProbeBatch];
+      bool in_window[kProbeBatch];
+#pragma unroll
+      for (int u = 0; u < kProbeBatch; ++u) {
+        slot[u] = s0 + (2 * u + half) * kWaves;
+        pos[u] = ring_slot_to_pos(P, M, slot[u]);
+        in_window[u] = cand_ok && slot[u] < s_hi && pos[u] >= cand_begin && pos[u] < cand_end;
+      }
+      uint4 w[kPasses][kProbeBatch];
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps) {
+        const int hl = min(row + 4 * ps, G - 1);
+#pragma unroll
+        for (int u = 0; u < kProbeBatch; ++u) {
+          const int64_t off = ((cache_req + min(slot[u], s_hi - 1)) * Hq + hkv * G + hl) * kHeadDim + cc * 8;
+          w[ps][u] = load_stream16(p.query_cache + off);  // read once: no cache pollution
+        }
+      }
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps) {
+        pin_vgpr(qaw[ps]);
+        pin_vgpr(qbw[ps]);
+      }
+      float acc[kPasses][kProbeBatch];
+      bool eval[kPasses][kProbeBatch];
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps)
+#pragma unroll
+        for (int u = 0; u < kProbeBatch; ++u) {
+          float cf[8], qa[8];
+          unpack8(w[ps][u], cf);
+          unpack8(qaw[ps], qa);
+          float a = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float df = qa[i] - cf[i];
+            a = fmaf(df, df, a);
+          }
+          acc[ps][u] = a;
+          eval[ps][u] = in_window[u] && row + 4 * ps < G && row8_sum(a) <= thr_prune;
+        }
+      bool any_eval = false;
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps)
+#pragma unroll
+        for (int u = 0; u < kProbeBatch; ++u) any_eval |= eval[ps][u];
+      if (!__any(any_eval)) continue;  // the whole batch pruned (the common case): no second half-rows
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps) {
+        const int hl = min(row + 4 * ps, G - 1);
+#pragma unroll
+        for (int u = 0; u < kProbeBatch; ++u) {
+          // a pruned slot's lanes read their head's query row instead (hot in
+          // the cache: every workgroup of the group reads it); the value is unused
+          const uint16_t* src =
+              eval[ps][u] ? p.query_cache + ((cache_req + min(slot[u], s_hi - 1)) * Hq + hkv * G + hl) * kHeadDim + 64 + cc * 8
+                          : p.q_pre + (static_cast<int64_t>(n) * Hq + hkv * G + hl) * kHeadDim + cc * 8;
+          w[ps][u] = load_stream16(src);
+        }
+      }
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps)
+#pragma unroll
+        for (int u = 0; u < kProbeBatch; ++u) {
+          float cf[8], qb[8];
+          unpack8(w[ps][u], cf);
+          unpack8(qbw[ps], qb);
+          float b = acc[ps][u];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float df = qb[i] - cf[i];
+            b = fmaf(df, df, b);
+          }
+          const float d = row8_sum(b);
+          if (eval[ps][u] && better_pair(d, pos[u], best_d[ps], best_p[ps])) {
+            best_d[ps] = d;
+            best_p[ps] = pos[u];
+            best_s[ps] = slot[u];
+          }
+        }
+    }
+    // the two half-rows of lanes tracked different slots: lane c takes the
+    // better of its own and lane c ^ 8's
+#pragma unroll
+    for (int ps = 0; ps < kPasses; ++ps) {
+      const float od = __shfl_xor(best_d[ps], 8);
+      const int op = __shfl_xor(best_p[ps], 8), os = __shfl_xor(best_s[ps], 8);
+      if (better_pair(od, op, best_d[ps], best_p[ps])) {
+        best_d[ps] = od;
+        best_p[ps] = op;
+        best_s[ps] = os;
+      }
+    }
+  } else if (kMode != 2) {
+    // every pass's loads of a batch are in flight before any reduction
+    auto scan_batch = [&](int s0) {
+      uint4 w[kPasses][kSlotBatch];
+      int pos[kSlotBatch];
+      bool in_window[kSlotBatch];
+#pragma unroll
+      for (int u = 0; u < kSlotBatch; ++u) {
+        const int slot = s0 + u * kWaves;
+        pos[u] = ring_slot_to_pos(P, M, slot);
+        in_window[u] = cand_ok && slot < s_hi && pos[u] >= cand_begin && pos[u] < cand_end;
+      }
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps) {
+        const int hl = min(row + 4 * ps, G - 1);
+#pragma unroll
+        for (int u = 0; u < kSlotBatch; ++u) {
+          const int slot = min(s0 + u * kWaves, s_hi - 1);  // past the range: re-reads its last row
+          const int64_t off = ((cache_req + slot) * Hq + hkv * G + hl) * kHeadDim + c * 8;
+          w[ps][u] = load_stream16(p.query_cache + off);  // ring rows are read once per step
+        }
+      }
+      uint4 qv[kPasses];  // unpacked only once the ring loads are issued
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps) {
+        qv[ps] = qw[ps];
+        pin_vgpr(qv[ps]);
+      }
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps) {
+        const int hl = row + 4 * ps;
+#pragma unroll
+        for (int u = 0; u < kSlotBatch; ++u) {
+          float cf[8], q[8];
+          unpack8(w[ps][u], cf);
+          unpack8(qv[ps], q);
+          float acc = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float df = q[i] - cf[i];
+            acc = fmaf(df, df, acc);
+          }
+          acc = row16_sum(acc);
+          if (in_window[u] && hl < G && better_pair(acc, pos[u], best_d[ps], best_p[ps])) {
+            best_d[ps] = acc;
+            best_p[ps] = pos[u];
+            best_s[ps] = s0 + u * kWaves;
+          }
+        }
+      }
+    };
+    // A ring that one batch per wave covers (32 slots with G = 8, 64 with
+    // G <= 4) is scanned without a loop: the queries' unpacking then cannot
+    // be hoisted in front of the ring loads, where its wait would hold them.
+    if (s_hi - s_lo <= kWaves * kSlotBatch) {
+      scan_batch(s_lo + wave);
+    } else {
+      for (int s0 = s_lo + wave; s0 < s_hi; s0 += kWaves * kSlotBatch) scan_batch(s0);
+    }
+  }
+#pragma unroll
+  for (int ps = 0; ps < kPasses; ++ps) {
+    const int hl = row + 4 * ps;
+    if (c == 0 && hl < G) {
+      s_d[wave][hl] = best_d[ps];
+      s_p[wave][hl] = best_p[ps];
+      s_s[wave][hl] = best_s[ps];
+    }
+  }
+  if (lse_in_lds && wave == 0 && lane < M) {
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) s_lse[hh][lane] = lse_reg[hh];
+  }
+  const bool ready = request_ready(p.cache_ready, p.cache_epoch, p.request_epoch, req, p.s.R);
+  const bool eligible = cand_ok && ready;
+  __syncthreads();
+  if (kMode != 1 && p.phase_cycles != nullptr && g == 0 && tid == 0)
+    p.phase_cycles[1] = static_cast<int64_t>(wall_clock64());
+  __shared__ int s_rect[kMaxGroup], s_mslot[kMaxGroup];
+  __shared__ float s_entry[kMaxGroup];
+  __shared__ int s_span[3];  // band begin, new_end, fused
+  if (wave == 0) decide_group<G, kMode>(p, s_d, s_p, s_s, s_lse, lse_in_lds, g, n, hkv, P, req, eligible,
+                                        s_rect, s_mslot, s_entry, s_span);
+  if constexpr (kMode != 1) {
+    __syncthreads();
+    if (s_span[2] == 0) return;
+    pin_vgpr(cur_lo);  // combined here, not where they are loaded
+    pin_vgpr(cur_hi);
+    const int64_t cl = p.s.out_cache_loc_is_i64
+                           ? static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(cur_hi)) << 32) |
+                                                  static_cast<uint32_t>(cur_lo))
+                           : static_cast<int64_t>(cur_lo);
+    ks.cur_row = (cl >= 0 && cl < p.s.pool_tokens) ? static_cast<int>(cl) : -1;
+    if ((tid >> 4) >= G) qpost_w = make_uint4(0, 0, 0, 0);
+    fused_group<G>(p, n, hkv, P, req, ready, s_span[0], s_span[1], s_rect, s_mslot, s_entry, qpost_w, ks, pre);
   }
 }
 
@@ -680,6 +1331,7 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* s_tmp, int& tota
 constexpr int kTasksPerWorkgroup = 12;  // default of AttnParams::tasks_per_wg
 constexpr int kMinChunk = 2048;
 constexpr int kMaxChunk = 16384;
+constexpr int kFuseTokens = 1024;  // default of DecideParams::fuse_tokens
 
 // Every workgroup of span_attention derives the same task list: the chunk C
 // from the total token count of all groups (kTasksPerWorkgroup tasks per
@@ -701,13 +1353,24 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
   const int per_thread = ceil_div(NG, kBlock);
   const int g_lo = min(tid * per_thread, NG);
   const int g_hi = min(g_lo + per_thread, NG);
+  // match_decide finished every group: only workgroup 0 stays, to publish
+  // the per-group descriptors and the counters
+  const bool any_long = *p.long_groups != 0;
+  if (!any_long && blockIdx.x != 0) {
+    total_tasks_out = 0;
+    chunk_out = 0;
+    active_wgs_out = 0;
+    return;
+  }
   long long tok = 0;
-  for (int g = g_lo; g < g_hi; ++g) {
+  for (int g = g_lo; any_long && g < g_hi; ++g) {  // (all four loads in one round)
+    const int fused = p.group_fused[g];  // finished by match_decide
     const int ne = p.group_rect_end[g];
-    tok += group_tokens(min(p.F, ne), p.group_rect_begin[g], ne, p.group_tail_end[g]);
+    const int t = group_tokens(min(p.F, ne), p.group_rect_begin[g], ne, p.group_tail_end[g]);
+    tok += fused != 0 ? 0 : t;
   }
   // reduce token count (64-bit) across the block
-  {
+  if (any_long) {
     long long x = tok;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
@@ -718,6 +1381,12 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) tok += s_tok[w];
     __syncthreads();
+  }
+  if (tok == 0 && blockIdx.x != 0) {  // nothing to attend: only workgroup 0 publishes the counters
+    total_tasks_out = 0;
+    chunk_out = 0;
+    active_wgs_out = 0;
+    return;
   }
   // A step with many tokens streams fastest with one workgroup per CU; a
   // small (latency-bound) one wants every resident workgroup.
@@ -730,18 +1399,19 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
   chunk = min(chunk, kMaxChunk);
   int* s_offb = s_off + NG + 1;
   int my_a = 0, my_b = 0;
-  for (int g = g_lo; g < g_hi; ++g) {
+  for (int g = g_lo; tok > 0 && g < g_hi; ++g) {
     GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, g, p.F, chunk, p.cap);
-    const int na = full_band_pieces(sp);
+    const bool fused = p.group_fused[g] != 0;
+    const int na = fused ? 0 : full_band_pieces(sp);
     s_off[g] = na;
-    s_offb[g] = sp.n_sink + sp.n_band + sp.n_tail - na;
+    s_offb[g] = fused ? 0 : sp.n_sink + sp.n_band + sp.n_tail - na;
     my_a += na;
     my_b += s_offb[g];
   }
   int total_a = 0, total_b = 0;
   int base_a = block_exclusive_scan(my_a, s_tmp, total_a);
   int base_b = block_exclusive_scan(my_b, s_tmp, total_b);
-  for (int g = g_lo; g < g_hi; ++g) {
+  for (int g = g_lo; tok > 0 && g < g_hi; ++g) {
     const int ca = s_off[g], cb = s_offb[g];
     s_off[g] = base_a;
     s_offb[g] = total_a + base_b;
@@ -761,11 +1431,11 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
     for (int g = tid; g < NG; g += kBlock) {
       GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, g, p.F, chunk, p.cap);
       p.group_chunk[g] = sp.chunk;
-      p.group_ntasks[g] = sp.n_sink + sp.n_band + sp.n_tail;
+      p.group_ntasks[g] = p.group_fused[g] != 0 ? 0 : sp.n_sink + sp.n_band + sp.n_tail;
       p.group_rect_tiles[g] = sp.n_band;
       p.group_tail_tiles[g] = sp.n_tail;
       const int mode = p.group_mode[g];
-      tails += sp.n_tail;
+      if (p.group_fused[g] == 0) tails += sp.n_tail;
       if (mode != MAC_GROUP_MAC_HIT) {
         ++nonhit;
         // the reference's reduce condition with its default threshold: the
@@ -937,8 +1607,12 @@ __global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
   const int c = lane & 15;
   const int NG = p.s.N * p.s.Hkv;
 
+  if (p.phase_cycles != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
+    p.phase_cycles[2] = static_cast<int64_t>(wall_clock64());
   int total_tasks = 0, chunk = 0, active_wgs = 0;
   plan_tasks(p, s_off, s_tmp, total_tasks, chunk, active_wgs);
+  if (p.phase_cycles != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
+    p.phase_cycles[3] = static_cast<int64_t>(wall_clock64());
   if (static_cast<int>(blockIdx.x) >= active_wgs) return;
 
   // ---- tasks ----
@@ -975,7 +1649,7 @@ __global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
     }
 
     auto phys_of = [&](int pos) -> int64_t {
-      if (pos >= b || !req_ok) return -1;
+      if (pos >= b || !req_ok || (pos != P && pos >= p.s.r2t_stride)) return -1;
       const int64_t ph = pos == P ? cur_loc : static_cast<int64_t>(r2t[pos]);
       return (ph >= 0 && ph < p.s.pool_tokens) ? ph : -1;
     };
@@ -1102,273 +1776,77 @@ __global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
 
 // ------------------------------------------------- MFMA span attention ----
 //
-// Same plan and task list as span_attention_kernel.  One 64-lane wave owns a
-// 32-token block at a time (waves take blocks wave, wave+4, ...):
-//
-//  * Loads: each 256-byte K or V row is read by 16 consecutive lanes (lane
-//    l reads 16-byte chunk l%16 of the row of token 8*(l/16) + i in load i),
-//    so every load instruction covers whole 128-byte lines, with the
-//    non-temporal policy (the rows are read once per step).  Measured on
-//    MI355X this streams ~12% faster than loading the MFMA operands straight
-//    from HBM, whose layout splits lines across instructions.  The block
-//    after the current one is always in flight in registers; its
-//    req_to_token entries are loaded one block earlier still.
-//  * The rows are staged in two 8 KiB per-wave LDS tiles, token-major.  In
-//    the K tile, 16-byte chunk c of token t sits at position c ^ k_swz(t)
-//    (see below), so the 16 tokens one A-operand read touches hit 16
-//    different bank groups; in the V tile at c ^ 2 (t & 7), which does the
-//    same for the transposing reads.
-//  * S^T[t][g] = sum_d K[t][d] Q[g][d] and O^T[d][g] += sum_t V[t][d] P[g][t]
-//    both run on v_mfma_f32_16x16x32_bf16.  MFMA row 4a + i of score tile t
-//    is token 8a + 4t + i, so the lane holding head g = l%16 ends with the
-//    scores of tokens 8q .. 8q + 7 (q = l/16): after conversion to bf16 they
-//    are the B operand of the PV product as they stand, and its A operand
-//    V^T[16 dt + g][8q .. 8q + 7] is two ds_read_b64_tr_b16 (gfx950's
-//    transposing LDS read) of the V tile.  The lane keeps its head's softmax
-//    state and 32 O^T accumulators, so the online-softmax rescale is
-//    lane-local.  Heads g >= G are zero padding rows of the 16-wide MFMA.
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& w) { return __builtin_bit_cast(bf16x8_t, w); }
-
-// K tile: 16-byte chunk c of token t at position c ^ k_swz(t) of its row.
-// The S^T tiles read tokens 8a + 4t + i (a, i < 4) in one instruction; this
-// swizzle puts the 16 of them on 16 different chunk positions.
-__device__ __forceinline__ int k_swz(int t) { return 4 * ((t >> 3) & 3) + (t & 3); }
-
-constexpr int kMfmaBlk = 32;  // tokens per wave block
-
-// One task of the MFMA kernel: the four waves of the workgroup take its
-// blocks in turn and combine their softmax states through LDS.  (A function
-// of its own, called once per task, so the compiler recomputes the LDS
-// addresses per task instead of holding them across the task loop: the
-// registers go to the block loop, which measured 2% faster for steps of many
-// short tasks.)
+// Same plan and task list as span_attention_kernel; a task is one range of
+// the block stream above (band pieces mask each head's positions before its
+// own band start).  The four waves' states are combined through LDS into one
+// normalised partial per head.
 template <int G>
-__device__ __forceinline__ void mfma_task(const AttnParams& p, const TaskInfo& ti,
-                                          uint4 (*s_k)[kMfmaBlk * 16], uint4 (*s_v)[kMfmaBlk * 16],
+__device__ __forceinline__ void mfma_task(const AttnParams& p, const TaskInfo& ti, uint4 (*s_kv)[kWaves][kTileU4],
                                           uint4* s_q, float (*s_ml)[G][2]) {
-  constexpr int kBlk = kMfmaBlk;
-  // the per-wave o of the task epilogue reuses the K tiles
-  auto s_o = reinterpret_cast<float (*)[G][kHeadDim]>(&s_k[0][0]);
   const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) control flow
-  const int lane = tid & 63;
-  const int quad = lane >> 4;  // lane / 16
-  const int col = lane & 15;   // lane % 16
-  const int Hq = p.s.Hq;
-  const int Hkv = p.s.Hkv;
-  const int64_t kv_stride = static_cast<int64_t>(Hkv) * kHeadDim;
-  const bool head_ok = col < G;
-  const uint16_t* vtile = reinterpret_cast<const uint16_t*>(&s_v[wave][0]);
-  // load-side token of load i for this lane: 8*quad + i; chunk: col
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = tid & 15;
+  const int n = ti.n, hkv = ti.hkv;
+  // Q of the group's heads (rows g >= G zero), staged once per task
   {
-    const int n = ti.n, hkv = ti.hkv, a = ti.a, b = ti.b, P = ti.P;
-    const int32_t* r2t = p.req_to_token + static_cast<int64_t>(ti.req_ok ? ti.req : 0) * p.s.r2t_stride;
-    const uint16_t* kbase = p.k_buffer + static_cast<int64_t>(hkv) * kHeadDim + col * 8;
-    const uint16_t* vbase = p.v_buffer + static_cast<int64_t>(hkv) * kHeadDim + col * 8;
-
-    // Q of the group's heads (rows g >= G zero), staged once per task; lane
-    // (quad, col) reads Q[col][8*(4s+quad) .. +8] as the B operand of k-step s.
-    int head_begin = 0;
-    {
-      const int64_t qoff = static_cast<int64_t>(n) * Hq * kHeadDim + static_cast<int64_t>(hkv) * G * kHeadDim;
-      for (int e = tid; e < 16 * 16; e += kBlock) {
-        const int g = e >> 4, c = e & 15;
-        uint4 w = make_uint4(0, 0, 0, 0);
-        if (g < G) w = *reinterpret_cast<const uint4*>(p.q_post + qoff + g * kHeadDim + c * 8);
-        s_q[e] = w;
-      }
-      if (ti.band && head_ok) head_begin = p.head_rect_start[static_cast<int64_t>(n) * Hq + hkv * G + col];
-      __syncthreads();
-    }
-    // Physical rows: raw_row() only issues the req_to_token load (index
-    // clamped into the row); phys_ok() checks it one block later, so waiting
-    // for it never drains the K/V loads issued after it.  -1 = masked token.
-    const int r2t_last = max(min(P, p.s.r2t_stride) - 1, 0);
-    const int cur_row = (ti.cur_loc >= 0 && ti.cur_loc < p.s.pool_tokens) ? static_cast<int>(ti.cur_loc) : -1;
-    const unsigned pool_rows = static_cast<unsigned>(min(p.s.pool_tokens, static_cast<int64_t>(INT_MAX)));
-    auto raw_row = [&](int pos) -> int { return r2t[min(max(pos, 0), r2t_last)]; };
-    auto phys_ok = [&](int pos, int raw) -> int {
-      const int ph = pos == P ? cur_row : raw;
-      return (pos < b && ti.req_ok && static_cast<unsigned>(ph) < pool_rows) ? ph : -1;
-    };
-    auto block_base = [&](int k) { return a + (wave + kWaves * k) * kBlk; };  // k-th block of this wave
-
-    float m = kNegBig, l = 0.0f;
-    f32x4_t acc[8];
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-    uint4 kr[8], vr[8];  // rows of tokens 8*quad + i, chunk col (current block)
-    int ph[8];           // checked rows of the current block
-    int raw[8];          // raw rows of the next block
-    auto issue = [&](const int (&rows)[8]) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) vr[i] = load_stream16(vbase + static_cast<int64_t>(max(rows[i], 0)) * kv_stride);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) kr[i] = load_stream16(kbase + static_cast<int64_t>(max(rows[i], 0)) * kv_stride);
-    };
-    {
-      const int b0 = block_base(0), b1 = block_base(1);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ph[i] = phys_ok(b0 + 8 * quad + i, raw_row(b0 + 8 * quad + i));
-#pragma unroll
-      for (int i = 0; i < 8; ++i) raw[i] = raw_row(b1 + 8 * quad + i);
-      __builtin_amdgcn_sched_barrier(0);
-      issue(ph);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-
-    const int nblk = ceil_div(b - a, kBlk);
-    const int my_blocks = wave < nblk ? ceil_div(nblk - wave, kWaves) : 0;
-    for (int k = 0; k < my_blocks; ++k) {
-      const int base = block_base(k);
-      const int b1 = block_base(k + 1), b2 = block_base(k + 2);
-      int nph[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) nph[i] = phys_ok(b1 + 8 * quad + i, raw[i]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) raw[i] = raw_row(b2 + 8 * quad + i);
-      __builtin_amdgcn_sched_barrier(0);
-      // token validity of this block: bit t set if token t has a row
-      uint32_t vmask = 0;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint64_t bal = __ballot(ph[i] >= 0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) vmask |= static_cast<uint32_t>((bal >> (16 * r)) & 1) << (8 * r + i);
-      }
-      // stage K and V rows (V of masked tokens zeroed) into the wave's tiles
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int tok = 8 * quad + i;
-        const uint32_t keep = ph[i] >= 0 ? 0xffffffffu : 0u;
-        uint4 w = vr[i];
-        w.x &= keep;
-        w.y &= keep;
-        w.z &= keep;
-        w.w &= keep;
-        s_k[wave][tok * 16 + (col ^ k_swz(tok))] = kr[i];
-        s_v[wave][tok * 16 + (col ^ (2 * (tok & 7)))] = w;
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      // the next block's rows go in flight while this block is computed
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ph[i] = nph[i];
-      issue(ph);
-      __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-      // S^T = K Q^T for the block's 32 tokens
-      f32x4_t st[2];
-#pragma unroll
-      for (int tile = 0; tile < 2; ++tile) {
-        f32x4_t c4 = {0.0f, 0.0f, 0.0f, 0.0f};
-        const int tok = 8 * (col >> 2) + 4 * tile + (col & 3);  // MFMA row col of this tile
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-          c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(s_k[wave][tok * 16 + ((4 * s + quad) ^ k_swz(tok))]),
-                                                      as_bf16x8(s_q[col * 16 + 4 * s + quad]), c4, 0, 0, 0);
-        st[tile] = c4;
-      }
-
-      // scale, mask, online softmax (lane-local except the block max)
-      float sv[8];
-      float bmax = kNegBig;
-#pragma unroll
-      for (int tile = 0; tile < 2; ++tile) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int tok = 8 * quad + 4 * tile + r;
-          const bool ok = head_ok && ((vmask >> tok) & 1) && base + tok >= head_begin;
-          const float x = ok ? st[tile][r] * p.q_scale : -INFINITY;
-          sv[4 * tile + r] = x;
-          bmax = fmaxf(bmax, x);
-        }
-      }
-      bmax = quad_max(bmax);
-      // Lazy rescale: the reference point m only moves when the block max
-      // exceeds it by more than kRescaleSlack (log2 units), so most blocks
-      // skip the 32-accumulator rescale; p <= 2^kRescaleSlack stays exact in
-      // fp32 and well inside bf16 range.
-      constexpr float kRescaleSlack = 8.0f;
-      if (__any(bmax > m + kRescaleSlack)) {
-        const float m_new = fmaxf(m, bmax);
-        const float alpha = fast_exp2(m - m_new);
-        m = m_new;
-        l *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
-      }
-      bf16x8_t pb;
-      float psum = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float pe = fast_exp2(sv[e] - m);
-        psum += pe;
-        pb[e] = static_cast<__bf16>(pe);
-      }
-      l += psum;
-      // O^T += V^T P^T: the A operand V^T[16 dt + col][tokens 8 quad .. +8]
-      // is two transposing reads of tokens 8 quad + 4 h + (col >> 2), dims
-      // 16 dt + 4 (col & 3) .. +3 (16-byte chunk 2 dt + ((col & 3) >> 1))
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        bf16x4_t part[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int t = 8 * quad + 4 * h + (col >> 2);
-          const int c = (2 * dt + ((col & 3) >> 1)) ^ (2 * (t & 7));
-          part[h] = lds_read_tr16(vtile + t * 128 + c * 8 + (col & 1) * 4);
-        }
-        const bf16x8_t va = __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7);
-        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, acc[dt], 0, 0, 0);
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-    }
-
-    l = quad_sum(l);
-    // ---- wave result -> LDS (over the K tiles), then combine the four waves ----
-    __syncthreads();  // every wave is done with its K tile
-    if (head_ok) {
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s_o[wave][col][16 * dt + 4 * quad + r] = acc[dt][r];
-      if (quad == 0) {
-        s_ml[wave][col][0] = m;
-        s_ml[wave][col][1] = l;
-      }
-    }
-    __syncthreads();
-    write_partial<G>(p, ti.g, ti.j, s_o, s_ml);  // next_task's barrier closes the task
+    const int64_t qoff = (static_cast<int64_t>(n) * p.s.Hq + hkv * G) * kHeadDim;
+    const int g = tid >> 4, c = tid & 15;
+    uint4 w = make_uint4(0, 0, 0, 0);
+    if (g < G) w = *reinterpret_cast<const uint4*>(p.q_post + qoff + g * kHeadDim + c * 8);
+    s_q[tid] = w;
   }
+  const int head_begin =
+      (ti.band && col < G) ? p.head_rect_start[static_cast<int64_t>(n) * p.s.Hq + hkv * G + col] : 0;
+  __syncthreads();
+  bf16x8_t qb[4];
+  load_q_operands(s_q, qb);
+  const KvStream ks = make_stream(p.req_to_token, p.s.r2t_rows, p.s.r2t_stride, ti.req, ti.P, ti.cur_loc,
+                                  p.s.pool_tokens, p.k_buffer, p.v_buffer, p.s.Hkv, hkv, col);
+  WaveState st, unused;
+  state_reset(st);
+  stream_blocks<G, false>(ks, one_range(ti.a, ti.b), head_begin, p.q_scale, qb, &s_kv[0][wave][0],
+                          &s_kv[1][wave][0], st, unused);
+  // ---- wave results -> LDS (over the tiles), then combine the four waves ----
+  __syncthreads();  // every wave is done with its tiles
+  float* so = reinterpret_cast<float*>(&s_kv[0][0][0]);
+  state_to_lds<G>(st, so, &s_ml[0][0][0]);
+  __syncthreads();
+  const int64_t slot = static_cast<int64_t>(ti.g) * p.cap + ti.j;
+  for (int e = tid; e < G * 64; e += kBlock) {
+    const int h = e >> 6, d0 = 2 * (e & 63);
+    float o0, o1, l;
+    combine_waves<G>(so, &s_ml[0][0][0], h, d0, o0, o1, l);
+    const int64_t oi = static_cast<int64_t>(ti.g) * p.o_group_stride + (static_cast<int64_t>(ti.j) * G + h) * kHeadDim + d0;
+    if (p.partial_bf16)
+      *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.partial_o) + oi) = pack_bf16x2(o0, o1);
+    else
+      *reinterpret_cast<float2*>(static_cast<float*>(p.partial_o) + oi) = make_float2(o0, o1);
+    if (d0 == 0) p.partial_lse[slot * G + h] = l;
+  }
+  // next_task's barrier closes the task
 }
 
 template <int G>
 __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnParams p) {
   extern __shared__ int s_off[];  // 2 (NG + 1) task offsets (dynamic)
   __shared__ int s_tmp[kWaves];
-  __shared__ uint4 s_k[kWaves][kMfmaBlk * 16];
-  __shared__ uint4 s_v[kWaves][kMfmaBlk * 16];
+  __shared__ uint4 s_kv[2][kWaves][kTileU4];
   __shared__ uint4 s_q[16 * 16];
   __shared__ float s_ml[kWaves][G][2];
-  static_assert(sizeof(float) * kWaves * G * kHeadDim <= sizeof(uint4) * kWaves * kMfmaBlk * 16, "s_o alias");
+  static_assert(sizeof(float) * kWaves * G * kOPitch <= sizeof(s_kv), "combine area");
 
+  if (p.phase_cycles != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
+    p.phase_cycles[2] = static_cast<int64_t>(wall_clock64());
   const int NG = p.s.N * p.s.Hkv;
   int total_tasks = 0, chunk = 0, active_wgs = 0;
   plan_tasks(p, s_off, s_tmp, total_tasks, chunk, active_wgs);
+  if (p.phase_cycles != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
+    p.phase_cycles[3] = static_cast<int64_t>(wall_clock64());
   if (static_cast<int>(blockIdx.x) >= active_wgs) return;
 
   __shared__ int s_task;
   for (int t = next_task(p, s_task); t < total_tasks; t = next_task(p, s_task))
-    mfma_task<G>(p, decode_task(p, s_off, NG, chunk, t), s_k, s_v, s_q, s_ml);
+    mfma_task<G>(p, decode_task(p, s_off, NG, chunk, t), s_kv, s_q, s_ml);
 }
 
 // ============================================================ 3. merge ====
@@ -1381,27 +1859,6 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
 // ring state = cached entry (hit heads) (+) band partials -> ring row (ready
 // requests only); out / out_lse = ring state (+) sink and tail partials.  An empty partial (lse = -inf) has weight 0,
 // the reference's skip rule (DECODE:866-890).
-struct MergeState {
-  float lse;   // natural log; -inf = empty
-  float o[2];  // normalised output of the owned dims
-};
-
-__device__ __forceinline__ void merge_into(MergeState& st, float lse2, float o0, float o1) {
-  if (!isfinite(lse2)) return;
-  if (!isfinite(st.lse)) {
-    st.lse = lse2;
-    st.o[0] = o0;
-    st.o[1] = o1;
-    return;
-  }
-  const float mx = fmaxf(st.lse, lse2);
-  const float w1 = __expf(st.lse - mx), w2 = __expf(lse2 - mx);
-  const float inv = 1.0f / (w1 + w2);
-  st.o[0] = (w1 * st.o[0] + w2 * o0) * inv;
-  st.o[1] = (w1 * st.o[1] + w2 * o1) * inv;
-  st.lse = mx + __logf(w1 + w2);
-}
-
 template <int G>
 __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
   constexpr int kBatch = 8;
@@ -1413,6 +1870,13 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int d0 = 2 * lane;
+  const bool stamp = p.phase_cycles != nullptr && g == 0 && h == 0 && tid == 0;
+  if (stamp) p.phase_cycles[4] = static_cast<int64_t>(wall_clock64());
+  if (g == 0 && h == 0 && tid == 0) *p.long_groups = 0;  // read by span_attention, set again by match_decide
+  if (p.group_fused[g] != 0) {  // finished by match_decide
+    if (stamp) p.phase_cycles[5] = static_cast<int64_t>(wall_clock64());
+    return;
+  }
   const int M = p.s.M;
   const int Hq = p.s.Hq;
   const int hq = hkv * G + h;
@@ -1520,6 +1984,7 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
                                 : 0u;
   *reinterpret_cast<uint32_t*>(p.out + ho * kHeadDim + d0) = packed;
   if (p.out_lse != nullptr && lane == 0) p.out_lse[ho] = valid ? ring.lse : -INFINITY;
+  if (stamp) p.phase_cycles[5] = static_cast<int64_t>(wall_clock64());
 }
 
 // ============================================================ host side ====
@@ -1587,6 +2052,16 @@ long long narrow_min_tokens() {
   return v;
 }
 
+// Tokens up to which match_decide finishes a group itself
+// (MAC_AMD_FUSE_TOKENS, read per call like the reference's switches; 0
+// sends every group through span_attention and merge_write).  Results do not
+// depend on it beyond rounding.
+int fuse_tokens() {
+  const char* e = std::getenv("MAC_AMD_FUSE_TOKENS");
+  const int x = e != nullptr ? std::atoi(e) : kFuseTokens;
+  return x < 0 ? 0 : x;
+}
+
 int attn_impl() {
   static const int impl = [] {
     const char* e = std::getenv("MAC_AMD_ATTN_IMPL");
@@ -1646,7 +2121,9 @@ int launch_all(const DecideParams& dp, const AttnParams& ap, const MergeParams& 
   if (dp.splits > 1) {
     hipLaunchKernelGGL((match_decide_kernel<G, 1>), dim3(NG, dp.splits), dim3(kBlock), 0, stream, dp);
     MAC_HIP(hipGetLastError());
-    hipLaunchKernelGGL((match_decide_kernel<G, 2>), dim3(NG), dim3(kBlock), 0, stream, dp);
+    DecideParams dp2 = dp;
+    dp2.stamp_first = 0;  // the range scan recorded the step's start
+    hipLaunchKernelGGL((match_decide_kernel<G, 2>), dim3(NG), dim3(kBlock), 0, stream, dp2);
   } else {
     hipLaunchKernelGGL((match_decide_kernel<G, 0>), dim3(NG), dim3(kBlock), 0, stream, dp);
   }
@@ -1724,7 +2201,9 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   MAC_REQUIRE(static_cast<int64_t>(N) * Hkv <= kMaxPlanGroups,
               "N * Hkv = %lld exceeds the %d groups one launch can plan", static_cast<long long>(N) * Hkv,
               kMaxPlanGroups);
-  MAC_REQUIRE(a->complete_task_len >= static_cast<int64_t>(N) * Hkv + 1, "complete task workspace too small");
+  MAC_REQUIRE(a->complete_task_len >= 2 * static_cast<int64_t>(N) * Hkv + 2, "complete task workspace too small");
+  MAC_REQUIRE(a->debug_enabled < 2 || a->phase_cycles == nullptr || a->phase_cycles_len >= 6,
+              "phase_cycles must have at least 6 elements");
   MAC_REQUIRE(a->req_to_token_rows > 0 && a->req_to_token_stride >= 0, "req_to_token must be 2-D");
   if (N == 0) return MAC_OK;
   MAC_REQUIRE(a->q_post && a->q_pre && a->k_buffer && a->v_buffer && a->req_to_token && a->req_ids &&
@@ -1811,6 +2290,23 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   dp.bench_skip_ratio_std = static_cast<float>(a->bench_skip_ratio_std);
   dp.bench_match_lag_mean = static_cast<float>(a->bench_match_lag_mean);
   dp.bench_match_lag_std = static_cast<float>(a->bench_match_lag_std);
+  int64_t* stamps = a->debug_enabled >= 2 ? a->phase_cycles : nullptr;
+  dp.fuse_tokens = fuse_tokens();
+  dp.group_fused = a->complete_task_go + static_cast<int64_t>(N) * Hkv;
+  dp.long_groups = a->complete_task_go + 2 * static_cast<int64_t>(N) * Hkv;
+  dp.q_post = static_cast<const uint16_t*>(a->q_post);
+  dp.k_buffer = static_cast<const uint16_t*>(a->k_buffer);
+  dp.v_buffer = static_cast<const uint16_t*>(a->v_buffer);
+  dp.req_to_token = a->req_to_token;
+  dp.out_cache_loc = a->out_cache_loc;
+  dp.ring_q = static_cast<uint16_t*>(a->query_cache);
+  dp.attn_cache = static_cast<uint16_t*>(a->attn_cache);
+  dp.ring_lse = a->lse_cache;
+  dp.out = static_cast<uint16_t*>(a->out);
+  dp.out_lse = a->out_lse;
+  dp.q_scale = static_cast<float>(a->sm_scale) * kLog2e;
+  dp.phase_cycles = stamps;
+  dp.stamp_first = 1;
 
   const int cap = a->max_tiles_context;
   const int64_t o_group_stride = static_cast<int64_t>(cap) * G * kHeadDim;
@@ -1847,6 +2343,9 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   ap.min_chunk = min_chunk();
   ap.narrow_grid = impl ? cus : INT_MAX;  // the VALU kernel is instruction-bound: every resident workgroup
   ap.narrow_min_tokens = narrow_min_tokens();
+  ap.group_fused = dp.group_fused;
+  ap.long_groups = dp.long_groups;
+  ap.phase_cycles = stamps;
 
   MergeParams mp{};
   mp.s = s;
@@ -1873,6 +2372,9 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   mp.o_group_stride = o_group_stride;
   mp.cap = cap;
   mp.F = dp.F;
+  mp.group_fused = dp.group_fused;
+  mp.long_groups = dp.long_groups;
+  mp.phase_cycles = stamps;
 
   // Persistent grid: what the device keeps resident, but no more workgroups
   // than the largest task count the caller's max_context allows.

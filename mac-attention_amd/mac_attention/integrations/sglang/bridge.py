@@ -23,7 +23,7 @@ import torch  # loads the HIP runtime the library must share
 _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))))
 LIB_PATH = os.environ.get("MAC_HIP_LIBRARY", os.path.join(_PKG_ROOT, "libmac_hip.so"))
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 _MAX_GROUP = 8
 _HEAD_DIM = 128
 
@@ -67,6 +67,7 @@ class MacDecodeArgs(ctypes.Structure):
         ("bench_match_lag_std", _f64),
         ("bench_seed", _i32), ("bench_miss_mask", _i32), ("bench_layer_id", _i32),
         ("mixed_group_fallback", _i32), ("bench_exact_quota", _i32),
+        ("phase_cycles", _p), ("phase_cycles_len", _i32),
     ]
 
 
@@ -454,6 +455,8 @@ class PersistentDecodeExtension:
         a.bench_layer_id = int(bench_layer_id)
         a.mixed_group_fallback = _env_flag("MAC_PERSISTENT_MIXED_GROUP_FALLBACK", 1)
         a.bench_exact_quota = _env_flag("MAC_BENCH_EXACT_QUOTA", 1)
+        a.phase_cycles = _ptr(phase_cycles)
+        a.phase_cycles_len = int(phase_cycles.numel())
         return a, q_post.device
 
 

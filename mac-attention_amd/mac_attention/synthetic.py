@@ -310,7 +310,7 @@ def to_device(torch, case: Case, device="cuda", out_cache_loc_dtype=None):
 
 
 def run_decode(torch, ext, dev: dict, case: Case, *, max_context, tile_tokens=4, match_tile_slots=4,
-               partial_dtype=None, bench=None, ws=None):
+               partial_dtype=None, bench=None, ws=None, debug_enabled=0):
     """Call the 68-argument binding on device tensors ``dev`` (from
     ``to_device``); returns (out, out_lse, workspace)."""
     n, hq, hkv, dim, m = case.shape
@@ -333,7 +333,7 @@ def run_decode(torch, ext, dev: dict, case: Case, *, max_context, tile_tokens=4,
         dev["lse_cache"], out, out_lse, *ws,
         max_context, tile_tokens, match_tile_slots, case.semantic_pos_ahead,
         case.front_sink_tokens, case.gen_min_limit, case.lookback_right, case.candidate_mode,
-        case.threshold, case.sm_scale, 0, b["bench_mode"],
+        case.threshold, case.sm_scale, debug_enabled, b["bench_mode"],
         b["bench_hit_rate"], b["bench_hit_rate_std"], b["bench_skip_ratio"],
         b["bench_skip_ratio_std"], b["bench_match_lag_mean"], b["bench_match_lag_std"],
         b["bench_seed"], b["bench_miss_mask"], b["bench_layer_id"],

@@ -51,13 +51,29 @@ def _check_against_oracle(case, dev, out, out_lse, ws, res, tol=1e-2, what=""):
     assert_close(lc, res.lse_cache, 3e-2, f"{what} lse_cache")
 
 
+# Groups of at most MAC_AMD_FUSE_TOKENS tokens are finished inside
+# match_decide (attention, merge and ring row in one workgroup); "0" sends
+# every group through span_attention and merge_write.  Both must give the
+# oracle's results.
+FUSE = {"fused": None, "split": "0"}
+
+
+def _set_fuse(monkeypatch, mode):
+    if FUSE[mode] is None:
+        monkeypatch.delenv("MAC_AMD_FUSE_TOKENS", raising=False)
+    else:
+        monkeypatch.setenv("MAC_AMD_FUSE_TOKENS", FUSE[mode])
+
+
+@pytest.mark.parametrize("fuse", list(FUSE))
 @pytest.mark.parametrize("partial", ["f32", "bf16"])
 @pytest.mark.parametrize("builder", kat_cases.ALL + golden_cases.LOADERS, ids=lambda f: f.__name__)
-def test_reference_kat(builder, partial, ext, monkeypatch):
+def test_reference_kat(builder, partial, fuse, ext, monkeypatch):
     kat = builder()
     for k, v in kat.env.items():
         monkeypatch.setenv(k, v)
-    print(f"case={kat.name} partial={partial}", flush=True)
+    _set_fuse(monkeypatch, fuse)
+    print(f"case={kat.name} partial={partial} fuse={fuse}", flush=True)
     c = kat.case
     res = oracle_run(c)
     dev = syn.to_device(torch, c)
@@ -133,10 +149,12 @@ RANDOM_CASES = [
 ]
 
 
+@pytest.mark.parametrize("fuse", list(FUSE))
 @pytest.mark.parametrize("cfg", RANDOM_CASES, ids=lambda c: f"B{c[0]}_Hq{c[1]}_Hkv{c[2]}_seed{c[-1]}")
-def test_random_vs_oracle(cfg, ext):
+def test_random_vs_oracle(cfg, fuse, ext, monkeypatch):
     b, hq, hkv, kv_lens, m, s, f, hit_rate, seed = cfg
-    print(f"random case {cfg}", flush=True)
+    _set_fuse(monkeypatch, fuse)
+    print(f"random case {cfg} fuse={fuse}", flush=True)
     c = syn.random_case(batch=b, hq=hq, hkv=hkv, kv_lens=kv_lens, capacity=m, semantic_pos_ahead=s,
                         front_sink_tokens=f, hit_rate=hit_rate, match_lag=m // 2, seed=seed)
     res = oracle_run(c)
@@ -210,3 +228,29 @@ def test_more_groups_than_one_launch_plans_is_refused(ext):
     dev = syn.to_device(torch, c)
     with pytest.raises(RuntimeError, match="groups one launch can plan"):
         syn.run_decode(torch, ext, dev, c, max_context=160, tile_tokens=32)
+
+
+def test_phase_cycles_stamps(ext):
+    """debug_enabled >= 2 stores six device-clock stamps in phase_cycles
+    (the reference's phase_cycles, DECODE:4751-4929): non-decreasing, and the
+    step's ring-row and output writes are unchanged by the stamping."""
+    c = syn.random_case(batch=3, hq=32, hkv=8, kv_lens=[900, 5000, 3000], capacity=32,
+                        semantic_pos_ahead=64, front_sink_tokens=8, hit_rate=0.6, match_lag=8, seed=41)
+    res = oracle_run(c)
+    for debug in (0, 2):
+        dev = syn.to_device(torch, c)
+        ws = syn.workspace(torch, batch=3, hq=32, hkv=8, capacity=32, max_context=5008, tile_tokens=16,
+                           match_tile_slots=8, semantic_pos_ahead=64, front_sink_tokens=8, device="cuda")
+        ws[29].fill_(-7)
+        out, out_lse, ws = syn.run_decode(torch, ext, dev, c, max_context=5008, tile_tokens=16,
+                                          match_tile_slots=8, ws=ws, debug_enabled=debug)
+        torch.cuda.synchronize()
+        _check_against_oracle(c, dev, out, out_lse, ws, res, what=f"debug {debug}")
+        stamps = ws[29].cpu().tolist()
+        if debug == 0:
+            assert stamps == [-7] * len(stamps)
+        else:
+            first = stamps[:6]
+            assert all(s > 0 for s in first), first
+            assert all(b >= a for a, b in zip(first, first[1:])), first
+            assert stamps[6:] == [-7] * (len(stamps) - 6)
