@@ -10,7 +10,7 @@ constexpr int kHeadDim = 128;      // the only head size the reference supports 
 constexpr int kMaxGroup = 8;       // largest GQA group (DECODE:5086, kMaxWarps)
 constexpr int kBlock = 256;        // threads per workgroup for every decode kernel
 constexpr int kWaves = kBlock / 64;
-constexpr int kMaxPlanGroups = 4096;  // N * Hkv handled by the in-workgroup task planner
+constexpr int kMaxPlanBuckets = 4096;  // entries per class of the task planner's LDS offset table
 
 // bf16 <-> f32.  A 32-bit word holds two bf16 values, low element first.
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }

@@ -152,6 +152,7 @@ struct AttnParams {
   float q_scale;  // sm_scale * log2(e)
   const int32_t* group_fused;  // groups match_decide finished (no tasks here)
   const int32_t* long_groups;  // 0: match_decide finished every group
+  int plan_bucket;             // groups per entry of the plan's LDS offset table
   int64_t* phase_cycles;
 };
 
@@ -1341,16 +1342,21 @@ constexpr int kFuseTokens = 1024;  // default of DecideParams::fuse_tokens
 // and the whole bands of hit groups).  Workgroups fetch A tasks before B
 // tasks, so the end of the kernel is filled with short tasks and the idle
 // time of the last workgroups is bounded by a short task, not a full chunk.
-// s_off[0..NG] holds the exclusive prefix sums of the per-group A counts,
-// s_off[NG+1 .. 2NG+1] those of the B counts.  Workgroup 0 also publishes the
-// per-group chunk and task counts for merge_write and the task counters.
+// s_off[0..NB] holds the exclusive prefix sums of the A counts of buckets of
+// plan_bucket consecutive groups (NB buckets; one group per bucket for up to
+// kMaxPlanBuckets groups), s_off[NB+1 .. 2NB+1] those of the B counts;
+// decode_task finds a task's bucket in the table and its group from the
+// bucket's spans.  Workgroup 0 also publishes the per-group chunk and task
+// counts for merge_write and the task counters.
 __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& total_tasks_out,
                            int& chunk_out, int& active_wgs_out) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int NG = p.s.N * p.s.Hkv;
-  const int per_thread = ceil_div(NG, kBlock);
+  const int gpb = p.plan_bucket;
+  const int NB = ceil_div(NG, gpb);  // offset-table entries per class
+  const int per_thread = ceil_div(NB, kBlock) * gpb;  // whole buckets per thread
   const int g_lo = min(tid * per_thread, NG);
   const int g_hi = min(g_lo + per_thread, NG);
   // match_decide finished every group: only workgroup 0 stays, to publish
@@ -1397,31 +1403,40 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
   int chunk = static_cast<int>((tok + target_tasks - 1) / target_tasks);
   chunk = ceil_div(max(chunk, p.min_chunk), 64) * 64;
   chunk = min(chunk, kMaxChunk);
-  int* s_offb = s_off + NG + 1;
+  // Offset table: entry b of class A (s_off) / class B (s_offb) is the
+  // first task of bucket b (groups b gpb .. b gpb + gpb - 1; one group per
+  // bucket unless the batch has more groups than the table has entries).
+  int* s_offb = s_off + NB + 1;
   int my_a = 0, my_b = 0;
   for (int g = g_lo; tok > 0 && g < g_hi; ++g) {
     GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, g, p.F, chunk, p.cap);
     const bool fused = p.group_fused[g] != 0;
     const int na = fused ? 0 : full_band_pieces(sp);
-    s_off[g] = na;
-    s_offb[g] = fused ? 0 : sp.n_sink + sp.n_band + sp.n_tail - na;
+    const int nb = fused ? 0 : sp.n_sink + sp.n_band + sp.n_tail - na;
+    const int b = g / gpb;
+    if (g % gpb == 0) {
+      s_off[b] = 0;
+      s_offb[b] = 0;
+    }
+    s_off[b] += na;
+    s_offb[b] += nb;
     my_a += na;
-    my_b += s_offb[g];
+    my_b += nb;
   }
   int total_a = 0, total_b = 0;
   int base_a = block_exclusive_scan(my_a, s_tmp, total_a);
   int base_b = block_exclusive_scan(my_b, s_tmp, total_b);
-  for (int g = g_lo; tok > 0 && g < g_hi; ++g) {
-    const int ca = s_off[g], cb = s_offb[g];
-    s_off[g] = base_a;
-    s_offb[g] = total_a + base_b;
+  for (int b = g_lo / gpb; tok > 0 && b * gpb < g_hi; ++b) {
+    const int ca = s_off[b], cb = s_offb[b];
+    s_off[b] = base_a;
+    s_offb[b] = total_a + base_b;
     base_a += ca;
     base_b += cb;
   }
   const int total_tasks = total_a + total_b;
   if (tid == 0) {
-    s_off[NG] = total_a;
-    s_offb[NG] = total_tasks;
+    s_off[NB] = total_a;
+    s_offb[NB] = total_tasks;
   }
   __syncthreads();
 
@@ -1516,21 +1531,34 @@ struct TaskInfo {
 __device__ __forceinline__ TaskInfo decode_task(const AttnParams& p, const int* s_off, int NG, int chunk,
                                                 int t) {
   TaskInfo ti;
-  const bool class_a = t < s_off[NG];
-  const int* off = class_a ? s_off : s_off + NG + 1;
-  int lo = 0, hi = NG - 1;  // last g with off[g] <= t
+  const int gpb = p.plan_bucket;
+  const int NB = ceil_div(NG, gpb);
+  const bool class_a = t < s_off[NB];
+  const int* off = class_a ? s_off : s_off + NB + 1;
+  int lo = 0, hi = NB - 1;  // last bucket b with off[b] <= t
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
     if (off[mid] <= t) lo = mid; else hi = mid - 1;
   }
-  ti.g = lo;
-  ti.n = lo / p.s.Hkv;
-  ti.hkv = lo - ti.n * p.s.Hkv;
-  const GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, lo, p.F, chunk, p.cap);
+  // the group of the bucket that holds task t (its earlier groups' counts
+  // come from their spans)
+  int k = t - off[lo];
+  int g = lo * gpb;
+  GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, g, p.F, chunk, p.cap);
+  for (; g + 1 < min((lo + 1) * gpb, NG); ++g) {
+    const bool fused = p.group_fused[g] != 0;
+    const int na = full_band_pieces(sp);
+    const int cnt = fused ? 0 : (class_a ? na : sp.n_sink + sp.n_band + sp.n_tail - na);
+    if (k < cnt) break;
+    k -= cnt;
+    sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, g + 1, p.F, chunk, p.cap);
+  }
+  ti.g = g;
+  ti.n = g / p.s.Hkv;
+  ti.hkv = g - ti.n * p.s.Hkv;
   // piece index j of the group (sink pieces, band pieces, tail pieces), which
   // is also the partial's slot: class A takes the full band pieces, class B
   // the sink pieces, the band remainder and the tail pieces, in that order
-  const int k = t - off[lo];
   const int na = full_band_pieces(sp);
   if (class_a)
     ti.j = sp.n_sink + k;
@@ -1595,7 +1623,7 @@ template <int G>
 __global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
   constexpr int U = 2;                 // tokens per row per iteration
   constexpr int kStep = kWaves * 4 * U;  // tokens per workgroup iteration
-  extern __shared__ int s_off[];  // 2 (NG + 1) task offsets (dynamic)
+  extern __shared__ int s_off[];  // 2 (NB + 1) bucket task offsets (dynamic)
   __shared__ int s_tmp[kWaves];
   __shared__ float s_o[kWaves][G][kHeadDim];
   __shared__ float s_ml[kWaves][G][2];
@@ -1828,7 +1856,7 @@ __device__ __forceinline__ void mfma_task(const AttnParams& p, const TaskInfo& t
 
 template <int G>
 __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnParams p) {
-  extern __shared__ int s_off[];  // 2 (NG + 1) task offsets (dynamic)
+  extern __shared__ int s_off[];  // 2 (NB + 1) bucket task offsets (dynamic)
   __shared__ int s_tmp[kWaves];
   __shared__ uint4 s_kv[2][kWaves][kTileU4];
   __shared__ uint4 s_q[16 * 16];
@@ -2129,7 +2157,7 @@ int launch_all(const DecideParams& dp, const AttnParams& ap, const MergeParams& 
   }
   MAC_HIP(hipGetLastError());
   if (ev) MAC_HIP(hipEventRecord(ev[1], stream));
-  const size_t plan_lds = 2 * sizeof(int) * (static_cast<size_t>(NG) + 1);
+  const size_t plan_lds = 2 * sizeof(int) * (static_cast<size_t>(ceil_div(NG, ap.plan_bucket)) + 1);
   if (impl)
     hipLaunchKernelGGL(span_attention_mfma_kernel<G>, dim3(attn_grid), dim3(kBlock), plan_lds, stream, ap);
   else
@@ -2198,9 +2226,8 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   MAC_REQUIRE(a->semantic_pos_ahead >= 0, "semantic_pos_ahead must be non-negative");
   MAC_REQUIRE(a->bench_mode == 0 || a->bench_mode == 1 || a->bench_mode == 2,
               "unsupported synthetic MAC bench mode");
-  MAC_REQUIRE(static_cast<int64_t>(N) * Hkv <= kMaxPlanGroups,
-              "N * Hkv = %lld exceeds the %d groups one launch can plan", static_cast<long long>(N) * Hkv,
-              kMaxPlanGroups);
+  MAC_REQUIRE(static_cast<int64_t>(N) * Hkv <= INT_MAX / 2, "N * Hkv = %lld groups is too many",
+              static_cast<long long>(N) * Hkv);
   MAC_REQUIRE(a->complete_task_len >= 2 * static_cast<int64_t>(N) * Hkv + 2, "complete task workspace too small");
   MAC_REQUIRE(a->debug_enabled < 2 || a->phase_cycles == nullptr || a->phase_cycles_len >= 6,
               "phase_cycles must have at least 6 elements");
@@ -2221,7 +2248,10 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   MAC_HIP(hipGetDevice(&dev));
   int cus = 0, per_cu = 0;
   const int impl = attn_impl();
-  const size_t plan_lds = 2 * sizeof(int) * (static_cast<size_t>(N) * Hkv + 1);
+  // The planner's LDS table has one entry per bucket of plan_bucket groups
+  // (one group per entry up to kMaxPlanBuckets groups).
+  const int plan_bucket = ceil_div(N * Hkv, kMaxPlanBuckets);
+  const size_t plan_lds = 2 * sizeof(int) * (static_cast<size_t>(ceil_div(N * Hkv, plan_bucket)) + 1);
   int rc = attn_residency(dev, G, impl, plan_lds, &cus, &per_cu);
   if (rc != MAC_OK) return rc;
 
@@ -2344,6 +2374,7 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   ap.narrow_grid = impl ? cus : INT_MAX;  // the VALU kernel is instruction-bound: every resident workgroup
   ap.narrow_min_tokens = narrow_min_tokens();
   ap.group_fused = dp.group_fused;
+  ap.plan_bucket = plan_bucket;
   ap.long_groups = dp.long_groups;
   ap.phase_cycles = stamps;
 
