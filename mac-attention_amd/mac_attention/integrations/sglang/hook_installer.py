@@ -2,17 +2,23 @@
 
 Interface of attention/src/mac_attention/integrations/sglang/hook_installer.py
 of the reference (HookSpec :18-23, targets :46-243, resolution and wrapping
-:246-330): a hook spec names ``"module:Class.attr"``, a hook callable and its
-kind -- ``around`` hooks receive the original function first, ``after`` hooks
-receive its result first and may replace it.  Wrapped functions carry
-``__mac_attention_hooked__`` so installing twice is a no-op.
+:246-330, scheduler-process launch sites :313-372): a hook spec names
+``"module:Class.attr"``, a hook callable and its kind -- ``around`` hooks
+receive the original function first, ``after`` hooks receive its result
+first and may replace it.  Wrapped functions carry ``__mac_attention_hooked__``
+so installing twice is a no-op.
 
-This build hooks what the gfx950 decode path needs: the server-args plumbing
-(settings, validation) and FlashInferAttnBackend.forward_decode, which tries
-the fused MAC step before the backend's own decode.  The model-side hooks of
-the reference (RoPE preservation inside LlamaAttention, the prefill ring
-update inside forward_extend, scheduler marks) call the functions of
-``persistent`` the same way and are left to the serving integration.
+Targets, by group:
+  * server arguments: the MAC settings and flags (plugin.py);
+  * scheduler: which prefill rows reach the ring (schedule_hooks.py);
+  * models: LlamaAttention and the Qwen2 / Qwen3 MoE attentions keep their
+    pre-RoPE queries and hand the layer's MAC state to the attention backend
+    (model_hooks.py; the Qwen classes are optional);
+  * FlashInfer backend: settings at construction, the ring update after each
+    prefill chunk (forward_extend) and the fused MAC decode step
+    (forward_decode).
+Profiling-only and CUDA-graph-trace hooks of the reference are not part of
+this build.
 """
 
 from __future__ import annotations
@@ -20,11 +26,18 @@ from __future__ import annotations
 from dataclasses import dataclass
 from functools import wraps
 from importlib import import_module
-from typing import Any, Callable, Iterable, Literal
+from typing import Any, Callable, Iterable, Iterator, Literal
 
 HookKind = Literal["around", "after"]
 
 _INSTALLED: list[str] = []
+
+_ATTN_CLASSES = (
+    ("sglang.srt.models.llama", "LlamaAttention", False),
+    ("sglang.srt.models.qwen2_moe", "Qwen2MoeAttention", True),
+    ("sglang.srt.models.qwen3_moe", "Qwen3MoeAttention", True),
+)
+_FLASHINFER = "sglang.srt.layers.attention.flashinfer_backend:FlashInferAttnBackend"
 
 
 @dataclass(frozen=True)
@@ -36,15 +49,31 @@ class HookSpec:
 
 
 def iter_hook_specs() -> Iterable[HookSpec]:
+    from . import model_hooks, schedule_hooks
     from .persistent import flashinfer_forward_decode_around
     from .plugin import (server_args_add_cli_args_around, server_args_from_cli_args_after,
                          server_args_post_init_after)
 
-    yield HookSpec("sglang.srt.server_args:ServerArgs.add_cli_args", server_args_add_cli_args_around, "around")
-    yield HookSpec("sglang.srt.server_args:ServerArgs.from_cli_args", server_args_from_cli_args_after, "after")
-    yield HookSpec("sglang.srt.server_args:ServerArgs.__post_init__", server_args_post_init_after, "after")
-    yield HookSpec("sglang.srt.layers.attention.flashinfer_backend:FlashInferAttnBackend.forward_decode",
-                   flashinfer_forward_decode_around, "around")
+    server = "sglang.srt.server_args:ServerArgs"
+    yield HookSpec(f"{server}.add_cli_args", server_args_add_cli_args_around, "around")
+    yield HookSpec(f"{server}.from_cli_args", server_args_from_cli_args_after, "after")
+    yield HookSpec(f"{server}.__post_init__", server_args_post_init_after, "after")
+
+    sched = "sglang.srt.managers.schedule_batch:ScheduleBatch"
+    yield HookSpec(f"{sched}.prepare_for_extend", schedule_hooks.schedule_prepare_for_extend_after, "after")
+    yield HookSpec(f"{sched}.mix_with_running", schedule_hooks.schedule_mix_with_running_after, "after")
+    yield HookSpec(f"{sched}.get_model_worker_batch", schedule_hooks.schedule_get_model_worker_batch_after,
+                   "after", optional=True)
+    yield HookSpec("sglang.srt.model_executor.forward_batch_info:ForwardBatch.init_new",
+                   schedule_hooks.forward_batch_init_new_after, "after")
+
+    for module, cls, optional in _ATTN_CLASSES:
+        yield HookSpec(f"{module}:{cls}.__init__", model_hooks.attention_init_after, "after", optional)
+        yield HookSpec(f"{module}:{cls}.forward", model_hooks.attention_forward_around, "around", optional)
+
+    yield HookSpec(f"{_FLASHINFER}.__init__", model_hooks.flashinfer_backend_init_after, "after")
+    yield HookSpec(f"{_FLASHINFER}.forward_extend", model_hooks.flashinfer_forward_extend_around, "around")
+    yield HookSpec(f"{_FLASHINFER}.forward_decode", flashinfer_forward_decode_around, "around")
 
 
 def _resolve_target(target: str) -> tuple[Any, str]:
@@ -54,6 +83,20 @@ def _resolve_target(target: str) -> tuple[Any, str]:
     for name in owners:
         obj = getattr(obj, name)
     return obj, attr
+
+
+def resolvable_specs(specs: Iterable[HookSpec] | None = None) -> Iterator[HookSpec]:
+    """The specs to register: every required one, and the optional ones whose
+    target this SGLang has."""
+    for spec in (iter_hook_specs() if specs is None else specs):
+        if spec.optional:
+            try:
+                owner, attr = _resolve_target(spec.target)
+            except (ImportError, AttributeError):
+                continue
+            if not hasattr(owner, attr):
+                continue
+        yield spec
 
 
 def _wrap(spec: HookSpec, original: Callable[..., Any]) -> Callable[..., Any]:
@@ -97,10 +140,13 @@ def install_hook(spec: HookSpec) -> bool:
     return True
 
 
-def install_hooks(strict: bool = True, specs: Iterable[HookSpec] | None = None) -> tuple[str, ...]:
+def install_hooks(strict: bool = True, specs: Iterable[HookSpec] | None = None,
+                  child_processes: bool = True) -> tuple[str, ...]:
     """Installs every spec (default: ``iter_hook_specs()``).  With
     ``strict`` a target that cannot be resolved raises; otherwise it is
-    skipped.  Returns the targets wrapped by this call."""
+    skipped.  ``child_processes``: also point SGLang's scheduler-process
+    launch sites at an entry point that installs the hooks in the child
+    (sites this SGLang lacks are skipped).  Returns what this call wrapped."""
     done = []
     for spec in (iter_hook_specs() if specs is None else specs):
         try:
@@ -109,6 +155,10 @@ def install_hooks(strict: bool = True, specs: Iterable[HookSpec] | None = None) 
         except (ImportError, AttributeError):
             if strict and not spec.optional:
                 raise
+    if child_processes:
+        from .child_process import install_child_wrappers
+
+        done.extend(install_child_wrappers())
     _INSTALLED.extend(done)
     return tuple(done)
 

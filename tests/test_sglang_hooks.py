@@ -1,0 +1,166 @@
+"""The SGLang hook set against stand-in SGLang modules (SGLang is not
+installed here): every target the serving path needs is wrapped, the
+scheduler's ring marks travel to the forward batch, the plugin entry point
+registers with SGLang's hook registry (or wraps in place without one), and
+scheduler processes install the hooks themselves.  Reference behaviour:
+hook_installer.py:46-372, schedule_hooks.py:8-66, child_process.py:1-21,
+plugin.py:37-69, pyproject.toml:27-28."""
+
+import argparse
+import enum
+import os
+import sys
+import types
+
+import pytest
+import torch
+
+import sglang_standin
+from helpers import REPO
+from mac_attention.integrations.sglang import child_process, hook_installer, plugin, schedule_hooks
+
+REQUIRED = {
+    "sglang.srt.server_args:ServerArgs.add_cli_args",
+    "sglang.srt.server_args:ServerArgs.from_cli_args",
+    "sglang.srt.server_args:ServerArgs.__post_init__",
+    "sglang.srt.managers.schedule_batch:ScheduleBatch.prepare_for_extend",
+    "sglang.srt.managers.schedule_batch:ScheduleBatch.mix_with_running",
+    "sglang.srt.managers.schedule_batch:ScheduleBatch.get_model_worker_batch",
+    "sglang.srt.model_executor.forward_batch_info:ForwardBatch.init_new",
+    "sglang.srt.models.llama:LlamaAttention.__init__",
+    "sglang.srt.models.llama:LlamaAttention.forward",
+    "sglang.srt.layers.attention.flashinfer_backend:FlashInferAttnBackend.__init__",
+    "sglang.srt.layers.attention.flashinfer_backend:FlashInferAttnBackend.forward_extend",
+    "sglang.srt.layers.attention.flashinfer_backend:FlashInferAttnBackend.forward_decode",
+}
+CHILD_SITES = {
+    "sglang.srt.entrypoints.engine:run_scheduler_process",
+    "sglang.srt.entrypoints.http_server:run_scheduler_process",
+    "sglang.srt.managers.data_parallel_controller:run_scheduler_process",
+    "sglang.srt.entrypoints.engine:Engine.run_scheduler_process_func",
+    "sglang.srt.entrypoints.http_server:launch_server.run_scheduler_process_func",
+    "sglang.srt.managers.data_parallel_controller:run_data_parallel_controller_process.run_scheduler_process_func",
+}
+
+
+@pytest.fixture
+def sg(monkeypatch):
+    monkeypatch.setattr(hook_installer, "_INSTALLED", [])
+    for k in [k for k in os.environ if k.startswith(("MAC_", "ENABLE_MAC"))]:
+        monkeypatch.delenv(k)
+    return sglang_standin.install(monkeypatch)
+
+
+def test_install_wraps_every_serving_target(sg):
+    done = set(hook_installer.install_hooks(strict=True))
+    assert REQUIRED <= done, REQUIRED - done
+    assert CHILD_SITES <= done, CHILD_SITES - done
+    assert not any("qwen" in t for t in done)  # optional classes this SGLang lacks are skipped
+    assert getattr(sg.LlamaAttention.forward, "__mac_attention_hooked__", False)
+    assert hook_installer.install_hooks(strict=True) == ()  # idempotent
+    assert hook_installer.is_installed()
+
+
+def test_scheduler_process_installs_hooks_then_runs_sglang(sg, monkeypatch):
+    hook_installer.install_hooks(strict=True)
+    installs = []
+    real = hook_installer.install_hooks
+    monkeypatch.setattr(hook_installer, "install_hooks", lambda *a, **k: installs.append(1) or real(*a, **k))
+    assert sg.http.launch_server("args") == "scheduler ran"
+    assert sg.dpc.run_data_parallel_controller_process("args") == "scheduler ran"
+    assert sg.engine.Engine.run_scheduler_process_func is child_process.run_scheduler_process_with_mac_hooks
+    assert sg.engine.run_scheduler_process is child_process.run_scheduler_process_with_mac_hooks
+    ran = [c for c in sg.calls if isinstance(c, tuple) and c[0] == "run_scheduler_process"]
+    assert ran == [("run_scheduler_process", ("args",), {})] * 2
+    assert installs == [1, 1]  # each scheduler process installed the hooks before SGLang's scheduler ran
+
+
+def test_plugin_registers_with_sglang_hook_registry(sg, monkeypatch):
+    registered = []
+
+    class HookType(enum.Enum):
+        AROUND = "around"
+        AFTER = "after"
+
+    class HookRegistry:
+        @staticmethod
+        def register(target, hook, kind):
+            registered.append((target, hook, kind))
+
+    mod = types.ModuleType("sglang.srt.plugins.hook_registry")
+    mod.HookRegistry, mod.HookType = HookRegistry, HookType
+    monkeypatch.setitem(sys.modules, "sglang.srt.plugins", types.ModuleType("sglang.srt.plugins"))
+    monkeypatch.setitem(sys.modules, "sglang.srt.plugins.hook_registry", mod)
+    plugin.register_plugin()
+    targets = {t for t, _, _ in registered}
+    assert REQUIRED <= targets and not any("qwen" in t for t in targets)
+    kinds = {t: k for t, _, k in registered}
+    assert kinds["sglang.srt.models.llama:LlamaAttention.forward"] is HookType.AROUND
+    assert kinds["sglang.srt.server_args:ServerArgs.__post_init__"] is HookType.AFTER
+    assert not hook_installer.is_installed()  # the registry wraps; nothing was patched in place
+    assert not getattr(sg.LlamaAttention.forward, "__mac_attention_hooked__", False)
+
+
+def test_plugin_without_registry_wraps_in_place(sg):
+    plugin.register_plugin()
+    assert getattr(sg.LlamaAttention.forward, "__mac_attention_hooked__", False)
+    assert hook_installer.is_installed()
+
+
+def test_plugin_does_not_register_twice_after_a_launcher_installed(sg, monkeypatch):
+    hook_installer.install_hooks(strict=True)
+    called = []
+    mod = types.ModuleType("sglang.srt.plugins.hook_registry")
+    mod.HookRegistry = types.SimpleNamespace(register=lambda *a: called.append(a))
+    mod.HookType = types.SimpleNamespace(AROUND=1, AFTER=2)
+    monkeypatch.setitem(sys.modules, "sglang.srt.plugins", types.ModuleType("sglang.srt.plugins"))
+    monkeypatch.setitem(sys.modules, "sglang.srt.plugins.hook_registry", mod)
+    plugin.register_plugin()
+    assert called == []
+
+
+def test_ring_marks_travel_from_scheduler_to_forward_batch(sg, monkeypatch):
+    monkeypatch.setenv("MAC_ATTENTION_ENABLE", "1")
+    monkeypatch.setenv("MAC_LOOKBACK_TOKENS_LEFT", "16")
+    hook_installer.install_hooks(strict=True)
+    reqs = [types.SimpleNamespace(origin_input_ids=[0] * n) for n in (100, 10, 40)]
+    batch = sg.ScheduleBatch(reqs, prefix_lens=[0, 0, 30], seq_lens=torch.tensor([60, 10, 40]))
+    batch.prepare_for_extend()
+    # request 0: ring keeps [84, 100), not in this chunk; 1: all of [0, 10); 2: [30, 40)
+    assert batch.mac_prefill_cache_update_starts == [-1, 0, 30]
+    running = sg.ScheduleBatch([types.SimpleNamespace(origin_input_ids=[0])] * 2, [], [])
+    batch.mix_with_running(running)
+    assert batch.mac_prefill_cache_update_starts == [-1, 0, 30, -1, -1]
+    worker = batch.get_model_worker_batch()
+    assert worker.mac_prefill_cache_update_starts == [-1, 0, 30, -1, -1]
+    fb = sg.ForwardBatch.init_new(worker, model_runner=None)
+    assert fb.mac_prefill_cache_update_starts == [-1, 0, 30, -1, -1]
+
+
+def test_marks_rule():
+    assert schedule_hooks.ring_update_starts([100, 100, 5], [0, 90, 0], [50, 100, 5], 16) == [-1, 90, 0]
+
+
+def test_mac_off_leaves_batches_unmarked_and_attention_unchanged(sg):
+    hook_installer.install_hooks(strict=True)
+    batch = sg.ScheduleBatch([types.SimpleNamespace(origin_input_ids=[0] * 8)], [0], [8])
+    batch.prepare_for_extend()
+    assert batch.mac_prefill_cache_update_starts is None
+    ident = lambda x: (x, None)  # noqa: E731
+    attn = sg.LlamaAttention(2, 1, 4, ident, lambda pos, q, k: (q, k), lambda q, k, v, fb: q, ident)
+    x = torch.arange(16.0).view(1, 16)
+    out = attn.forward(torch.zeros(1, dtype=torch.long), x, types.SimpleNamespace())
+    assert torch.equal(out, x[:, :8])
+    assert "LlamaAttention.forward (SGLang's own)" in sg.calls
+
+
+def test_pyproject_declares_the_plugin_entry_point():
+    import tomli
+
+    with open(os.path.join(REPO, "pyproject.toml"), "rb") as f:
+        meta = tomli.load(f)
+    eps = meta["project"]["entry-points"]["sglang.srt.plugins"]
+    assert eps == {"mac_attention": "mac_attention.integrations.sglang.plugin:register_plugin"}
+    mod_name, fn = eps["mac_attention"].split(":")
+    __import__(mod_name)
+    assert callable(getattr(sys.modules[mod_name], fn))
