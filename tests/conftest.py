@@ -26,3 +26,17 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+def pytest_terminal_summary(terminalreporter):
+    """Decisions excused from exact parity (similarity within 1e-6 of the
+    threshold), logged by helpers.near_threshold_heads."""
+    try:
+        from helpers import NEAR_THRESHOLD_BAND, NEAR_THRESHOLD_LOG
+    except Exception:  # pragma: no cover
+        return
+    if NEAR_THRESHOLD_LOG:
+        terminalreporter.write_sep("-", f"near-threshold decisions (|s - thr| <= {NEAR_THRESHOLD_BAND:g}), "
+                                        "logged and excused from exact parity")
+        for e in NEAR_THRESHOLD_LOG:
+            terminalreporter.write_line(str(e))

@@ -147,3 +147,30 @@ def host_subset(torch, dev: dict, requests, *, semantic_pos_ahead, front_sink_to
         if t.numel() > 0:
             setattr(c, name, t[rid].cpu().numpy().astype(np.uint8 if name == "cache_ready" else np.int64))
     return c
+
+
+# ------------------------------------------------- near-threshold decisions ----
+# The north star allows a decision to differ from the oracle only where the
+# similarity s = 1 - sqrt(d / (2 D)) of the head's best ring entry lies
+# within 1e-6 of the threshold (fp32 vs double distance rounding can flip it
+# there); such heads are logged here and reported at the end of the run.
+NEAR_THRESHOLD_BAND = 1e-6
+NEAR_THRESHOLD_LOG: list = []
+
+
+def similarity(dist, head_dim=128):
+    return 1.0 - np.sqrt(np.maximum(np.asarray(dist, np.float64), 0.0) / (2.0 * head_dim))
+
+
+def near_threshold_heads(res, threshold=0.45, what="", requests=None):
+    """Bool [N, Hq]: heads whose best distance puts their similarity within
+    NEAR_THRESHOLD_BAND of the threshold.  Each one is appended to
+    NEAR_THRESHOLD_LOG (what, request, head, s, oracle decision)."""
+    d = res.head["best_dist"]
+    s = similarity(d)
+    near = np.isfinite(d) & (np.abs(s - threshold) <= NEAR_THRESHOLD_BAND)
+    for n, h in zip(*np.nonzero(near)):
+        req = int(requests[n]) if requests is not None else int(n)
+        NEAR_THRESHOLD_LOG.append(dict(what=what, request=req, head=int(h), similarity=float(s[n, h]),
+                                       threshold=threshold, oracle_hit=int(res.head["hit"][n, h])))
+    return near

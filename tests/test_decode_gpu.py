@@ -11,7 +11,7 @@ import pytest
 
 import golden_cases
 import kat_cases
-from helpers import assert_close, bits, oracle_run, rel_l2, syn
+from helpers import assert_close, bits, near_threshold_heads, oracle_run, rel_l2, syn
 
 torch = pytest.importorskip("torch")
 
@@ -33,6 +33,8 @@ def _np(t):
 
 def _check_against_oracle(case, dev, out, out_lse, ws, res, tol=1e-2, what=""):
     n_req = case.q_post.shape[0]
+    near = near_threshold_heads(res, threshold=case.threshold, what=what)
+    assert not near.any(), f"{what}: inputs put a decision within 1e-6 of the threshold (logged)"
     np.testing.assert_array_equal(_np(ws[3])[:n_req], res.head["hit"], err_msg=f"{what} head_hit")
     np.testing.assert_array_equal(_np(ws[5])[:n_req], res.head["match_pos"], err_msg=f"{what} match_pos")
     np.testing.assert_array_equal(_np(ws[4])[:n_req], res.head["match_slot"], err_msg=f"{what} match_slot")
