@@ -14,8 +14,8 @@ decode step (lower is better), plus
   roofline      -- the dominant kernel (span_attention): algorithmic bytes per
                    launch / its average duration from HIP events on its stream;
   step_roofline -- all algorithmic bytes of the step / graph-replayed step time;
-  cpu_baseline  -- the CPU oracle (oracle/mac_oracle.c, one thread) timed on a
-                   bounded sample of the same workload, scaled to µs per step;
+  cpu_baseline  -- the FP32 PyTorch restatement of the step (oracle/torch_oracle.py)
+                   on all host cores, over every request of the headline step;
   sweep         -- µs/step and achieved GB/s across hit ratios for GQA-4 and
                    GQA-8, and the same kernel forced to exact attention through
                    the readiness gate (the hit-0 path);
@@ -60,7 +60,6 @@ def parse_args():
     ap.add_argument("--sweep", choices=["none", "short", "full"], default="short")
     ap.add_argument("--sweep-replays", type=int, default=30)
     ap.add_argument("--sweep-hits", default="0,0.25,0.5,0.75,0.8,0.9,1.0")
-    ap.add_argument("--cpu-requests", type=int, default=48)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--phase-runs", type=int, default=5)
     ap.add_argument("--json-out", default=None)
@@ -230,47 +229,55 @@ def measure(torch, step: Step, warmup, steps, phase_runs):
 
 
 def cpu_baseline(args, hit):
-    """Times the CPU oracle on `cpu_requests` requests of the headline shape."""
+    """The FP32 PyTorch restatement of the decode step (oracle/torch_oracle.py,
+    pinned against the C oracle in tests/test_torch_oracle.py) timed on this
+    host's CPU cores, on all ``args.batch`` requests of the headline step.
+    Every request reads one request's K/V rows (same req_to_token row) so host
+    memory stays at one request's rows while each request does its full work;
+    the hit decisions are those of the synthetic_head override at ``hit``
+    (matches planted where it puts them, found by the restatement's own
+    ring scan)."""
     import numpy as np
+    import torch
 
     from mac_attention import synthetic as syn
-    from oracle import oracle as orc
+    from oracle import torch_oracle as tor
 
-    nreq = max(1, args.cpu_requests)
-    # One request's K/V rows are generated and every sampled request reads them
-    # (same req_to_token row), so host memory stays at one request's 0.5 GB
-    # while the oracle does the full per-request work.
-    c = syn.random_case(batch=1, hq=args.hq, hkv=args.hkv, kv_lens=[args.ctx + 1],
-                        capacity=args.ring, semantic_pos_ahead=args.semantic_pos_ahead,
-                        front_sink_tokens=args.front_sink, hit_rate=1.0, seed=7,
-                        entry_builder="random", separate_pre_post=False)
-    rep = lambda a: np.ascontiguousarray(np.repeat(a, nreq, axis=0))  # noqa: E731
-    c.q_post = c.q_pre = rep(c.q_pre)
-    c.req_to_token = rep(c.req_to_token)
-    c.query_cache, c.attn_cache = rep(c.query_cache), rep(c.attn_cache)
-    c.lse_cache = np.zeros((nreq,) + c.lse_cache.shape[1:], np.float32)
-    c.req_ids = np.arange(nreq, dtype=np.int32)
-    c.past_lens = rep(c.past_lens)
-    c.out_cache_loc = rep(c.out_cache_loc)
-    params = orc.DecodeParams(semantic_pos_ahead=c.semantic_pos_ahead,
-                              front_sink_tokens=c.front_sink_tokens, bench_mode=1,
-                              bench_hit_rate=hit, sm_scale=c.sm_scale)
-    inputs = dict(q_post=syn.to_bits(c.q_post), q_pre=syn.to_bits(c.q_pre),
-                  k_buffer=syn.to_bits(c.k), v_buffer=syn.to_bits(c.v),
-                  req_to_token=c.req_to_token, req_ids=c.req_ids, past_lens=c.past_lens,
-                  out_cache_loc=c.out_cache_loc, query_cache=syn.to_bits(c.query_cache),
-                  attn_cache=syn.to_bits(c.attn_cache), lse_cache=c.lse_cache)
-    t0 = time.perf_counter()
-    res = orc.decode(**inputs, params=params)
-    sec = time.perf_counter() - t0
-    us_step = sec * 1e6 * args.batch / nreq
-    return dict(value=round(us_step, 1), unit="us/step", cores=1, kind="port",
-                sample=(f"{nreq} of {args.batch} requests of the headline shape sharing one "
-                        f"request's K/V rows (kv_len "
-                        f"{args.ctx + 1}, Hq {args.hq}, Hkv {args.hkv}, ring {args.ring}, "
-                        f"synthetic_head hit {hit}), {sec:.2f} s single-threaded C oracle, "
-                        f"scaled linearly to {args.batch} requests"),
-                sample_head_hits=int(res.head["hit"].sum()))
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(7)
+    kv_len, hq, hkv, m, S = args.ctx + 1, args.hq, args.hkv, args.ring, args.semantic_pos_ahead
+    k = tor.bf16(torch.randn(kv_len, hkv, D, generator=g))
+    v = tor.bf16(torch.randn(kv_len, hkv, D, generator=g))
+    r2t = torch.arange(kv_len, dtype=torch.int64)
+    params = tor.StepParams(semantic_pos_ahead=S, front_sink_tokens=args.front_sink, sm_scale=1.0 / math.sqrt(D))
+    hits = misses = 0
+    elapsed = 0.0
+    for n in range(args.batch):
+        q_pre = tor.bf16(torch.randn(hq, D, generator=g))
+        q_post = tor.bf16(torch.randn(hq, D, generator=g))
+        ring_q = tor.bf16(torch.randn(m, hq, D, generator=g) + 10.0)
+        ring_o = tor.bf16(torch.randn(m, hq, D, generator=g))
+        ring_l = torch.zeros(m, hq)
+        for h in range(hq):
+            hit_h, slot = syn.synthetic_hit_and_slot(
+                bench_mode=1, batch=args.batch, hq=hq, hkv=hkv, past_len=args.ctx, n=n, hq_i=h,
+                hkv_i=h // (hq // hkv), hit_rate=hit, capacity=m, semantic_pos_ahead=S, bench_seed=1,
+                match_lag_mean=64.0)
+            if hit_h and slot >= 0:
+                ring_q[slot, h] = q_pre[h]
+        t0 = time.perf_counter()
+        r = tor.decode_request(q_post=q_post, q_pre=q_pre, k=k, v=v, r2t_row=r2t, P=args.ctx, cur_loc=args.ctx,
+                               ring_q=ring_q, ring_o=ring_o, ring_lse=ring_l, params=params)
+        elapsed += time.perf_counter() - t0
+        hits += int(r["head_hit"].sum())
+        misses += int(hq - r["head_hit"].sum())
+    return dict(value=round(elapsed * 1e6, 1), unit="us/step", cores=cores, kind="port", precision="fp32",
+                sample=(f"all {args.batch} requests of the headline step (kv_len {kv_len}, Hq {hq}, Hkv {hkv}, "
+                        f"ring {m}, synthetic_head hit {hit}: {hits} hit heads, {misses} missed) through "
+                        f"oracle/torch_oracle.py in float32 on {cores} host cores; every request reads one "
+                        f"request's K/V rows"),
+                sample_head_hits=hits)
 
 
 def stream_read_peak(torch):
@@ -617,7 +624,11 @@ def main():
     traffic, traffic_src = pmc_traffic(args)
     roof = dict(bound="hbm", achieved=headline["attention_kernel_gbs"], peak=HBM_PEAK_GBS,
                 unit="GB/s", frac=round(headline["attention_kernel_gbs"] / HBM_PEAK_GBS, 4),
-                traffic=traffic, traffic_source=traffic_src, kernel="span_attention", kernel_us=attn_us,
+                traffic=traffic, traffic_source=traffic_src,
+                traffic_note=("HBM bytes per launch from a separate rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE run "
+                              "of this workload (the committed summary named in traffic_source), not this run"
+                              if traffic is not None else None),
+                kernel="span_attention", kernel_us=attn_us,
                 bytes_per_launch=headline["attention_kernel_bytes"])
     line = {
         "metric": METRIC,
