@@ -671,13 +671,18 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
 
 // request_length[req] += len (indexed-by-request form), after the ring rows
 // were addressed with the old value.
+// request_length[req] += len for every request the window kernel wrote
+// (the validity test of request_rows: a request it skipped is not bumped).
 __global__ void bump_kernel(int32_t* request_length, const int32_t* req_ids, const int32_t* qo_indptr,
-                            int B, int R) {
+                            const int32_t* kv_indptr, int64_t total_q, int64_t kv_len_total, int B, int R) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= B) return;
   const int req = req_ids[b];
-  const int len = qo_indptr[b + 1] - qo_indptr[b];
-  if (len <= 0 || req < 0 || req >= R) return;
+  const int q0 = qo_indptr[b], q1 = qo_indptr[b + 1];
+  const int k0 = kv_indptr[b], k1 = kv_indptr[b + 1];
+  const int len = q1 - q0;
+  const bool ok = q0 >= 0 && q1 <= total_q && k0 >= 0 && k1 <= kv_len_total && len > 0 && k1 - k0 >= len;
+  if (!ok || req < 0 || req >= R) return;
   atomicAdd(&request_length[req], len);
 }
 
@@ -850,7 +855,7 @@ extern "C" int mac_prefill_rectify_update_cache_bf16(const MacRectifyArgs* a, vo
   HIP_OK(hipGetLastError());
   if (!p.rl_by_batch) {
     hipLaunchKernelGGL(bump_kernel, dim3((a->B + 255) / 256), dim3(256), 0, s, a->request_length, a->req_ids,
-                       a->qo_indptr, a->B, a->R);
+                       a->qo_indptr, a->kv_indptr, p.total_q, p.kv_len_total, a->B, a->R);
     HIP_OK(hipGetLastError());
   }
   return MAC_OK;

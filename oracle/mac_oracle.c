@@ -819,7 +819,7 @@ EXPORT void mac_oracle_rectify_update_cache(
     const int32_t* kv_indptr, const int32_t* kv_indices, uint16_t* q_cache, uint16_t* attn_cache,
     float* lse_cache, uint16_t* q_post_cache, int32_t* request_length, int request_length_len,
     const int32_t* req_ids, int B, int R, int M, int Hq, int Hkv, int D, int S, int F,
-    int sink_mode, double sm_scale) {
+    int sink_mode, double sm_scale, int64_t total_q, int64_t kv_indices_len) {
   if (M <= 0 || B == 0) return;
   const int G = Hq / Hkv;
   const int by_batch = request_length_len == B;
@@ -841,6 +841,12 @@ EXPORT void mac_oracle_rectify_update_cache(
     int Ni = qo_indptr[b + 1] - qo_indptr[b];
     if (Ni <= 0 || req < 0 || req >= R) continue;
     int kvlen = kv_indptr[b + 1] - kv_indptr[b];
+    /* a request whose query or key ranges fall outside the buffers the
+     * caller described, or with fewer keys than queries, is skipped whole:
+     * no ring row and no request_length bump (as the window pass skips it) */
+    if (qo_indptr[b] < 0 || qo_indptr[b + 1] > total_q || kv_indptr[b] < 0 ||
+        kv_indptr[b + 1] > kv_indices_len || kvlen < Ni)
+      continue;
     int start = Ni > M ? Ni - M : 0;
     int L = before[b] < 0 ? 0 : before[b];
     int base_dest = (int)(((int64_t)L + start) % M);

@@ -338,7 +338,8 @@ def rectify_update_cache(q_post, src_q, o_full, lse_full, k_buffer, v_buffer, qo
         _ptr(attn_cache, _u16p), _ptr(lse_cache, _f32p), _ptr(q_post_cache, _u16p),
         _ptr(request_length, _i32p), int(request_length.shape[0]), _ptr(req_ids, _i32p),
         int(req_ids.shape[0]), r, m, hq, int(k_buffer.shape[1]), d, int(semantic_pos_ahead),
-        int(front_sink_tokens), int(sink_mode), ctypes.c_double(sm_scale))
+        int(front_sink_tokens), int(sink_mode), ctypes.c_double(sm_scale),
+        ctypes.c_int64(q_post.shape[0]), ctypes.c_int64(kv_indices.shape[0]))
 
 
 # ---------------------------------------------------- decode RoPE + scatter ---

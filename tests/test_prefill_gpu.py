@@ -248,6 +248,25 @@ def test_rectify_by_batch_request_length_and_bad_request(rect_ext):
     np.testing.assert_array_equal(g["rl"].cpu().numpy(), [5, 6, 7])
 
 
+def test_rectify_skips_requests_outside_the_buffers(rect_ext):
+    """The fused rectification skips a request with fewer keys than queries
+    and one whose key range runs past kv_indices, as the window pass does:
+    no ring row is written and request_length is not bumped for them (the
+    oracle applies the same rule); the other requests are rectified."""
+    S, M, R = 8, 16, 5  # R != B: request_length indexed by request (and bumped)
+    case = syn.prefill_case(qo_lens=[30, 10, 12, 8], kv_lens=[40, 10, 20, 16], hq=4, hkv=2, seed=29)
+    case.kv_indptr = case.kv_indptr.copy()
+    case.kv_indptr[2] = 45                 # request 1: 5 keys for 10 queries
+    case.kv_indices = case.kv_indices[:80]  # request 3: keys [70, 86) past the 80 entries
+    full = orc.window_attention(_bf(case.q), _bf(case.k), _bf(case.v), case.qo_indptr, case.kv_indptr,
+                                np.concatenate([case.kv_indices, np.zeros(6, np.int32)]), window_left=-1,
+                                sm_scale=case.sm_scale)
+    e, g, _ = _run_rectify(rect_ext, case, S=S, F=0, sink_mode=0, M=M, R=R, req_ids=[0, 1, 2, 3],
+                           request_length=[100, 200, 300, 400, 500], q_post_cache=False, full=full, seed=9)
+    _compare_ring(e, g, "out-of-buffer requests")
+    np.testing.assert_array_equal(g["rl"].cpu().numpy(), [130, 200, 312, 400, 500])
+
+
 def test_rectify_equals_gpu_composition(rect_ext, merge_ext, cache_ext):
     """The fused op equals the reference's three calls run on the GPU
     (window pass -> downdate -> mac_prefill_update_cache), rows with E > 0."""
