@@ -173,6 +173,20 @@ typedef struct MacDecodeArgs {
  * ([5]), group_mode ([15]) and task_counts ([22]). */
 MAC_API int mac_persistent_decode_bf16(const MacDecodeArgs* args, void* stream);
 
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory or hand over workspaces (code under graph capture, tight serving
+ * loops, harnesses that forbid allocation).  Same step and effects on the
+ * caller's tensors as mac_persistent_decode_bf16 (out / out_lse, the ring row
+ * at past_len % M, phase_cycles), with every workspace in one static device
+ * array of the library (about 65 MiB per GPU, held until the process ends):
+ * the workspace pointers and their sizes in `args` (match_*, head_*, group_*,
+ * complete_task_*, task_counts, partial_*) are ignored and the decisions are
+ * not returned.  Limits: N * Hq <= 4096 query heads, M <= 2048 ring slots;
+ * larger steps are rejected with MAC_ERR_INVALID_ARGUMENT.  Calls allocate
+ * nothing.  All calls on one GPU share its array: calls that overlap on one
+ * GPU (different streams) race. */
+MAC_API int mac_persistent_decode_bf16_noalloc(const MacDecodeArgs* args, void* stream);
+
 /* Replaces mac_prefill_update_cache (PREFILL:324-372, pybind PREFILL:500-502).
  * q_cache/attn_cache bf16 [R, M, H, D]; lse_cache f32 [R, M, H];
  * request_length i32 [request_length_len] with request_length_len == R

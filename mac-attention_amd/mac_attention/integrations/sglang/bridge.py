@@ -74,6 +74,7 @@ class MacDecodeArgs(ctypes.Structure):
 EXPORTED_SYMBOLS = (
     "mac_persistent_decode_bf16",
     "mac_persistent_decode_bf16_timed",
+    "mac_persistent_decode_bf16_noalloc",
     "mac_prefill_update_cache",
     "mac_mark_persistent_ready",
     "mac_invalidate_persistent_ready",
@@ -134,6 +135,8 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.mac_persistent_decode_bf16_timed.argtypes = [
         ctypes.POINTER(MacDecodeArgs), _p, ctypes.POINTER(ctypes.c_float)]
     lib.mac_persistent_decode_bf16_timed.restype = ctypes.c_int
+    lib.mac_persistent_decode_bf16_noalloc.argtypes = [ctypes.POINTER(MacDecodeArgs), _p]
+    lib.mac_persistent_decode_bf16_noalloc.restype = ctypes.c_int
     lib.mac_prefill_update_cache.argtypes = [
         _p, _p, _p, _p, _i32, _p, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i32, _p, _p,
     ]
@@ -229,6 +232,17 @@ class PersistentDecodeExtension:
         a, device = self._marshal(*args)
         with torch.cuda.device(device):
             rc = self._lib.mac_persistent_decode_bf16(ctypes.byref(a), _stream(device))
+        _raise_on(self._lib, rc)
+
+    def mac_persistent_decode_bf16_noalloc(self, *args) -> None:
+        """The same step through the library's no-allocation entry point
+        (no reference counterpart): the 68 arguments are checked as above,
+        the workspace tensors are then ignored (the library's static device
+        array holds them) and the decisions are not returned.  At most 4096
+        query heads per step and 2048 ring slots."""
+        a, device = self._marshal(*args)
+        with torch.cuda.device(device):
+            rc = self._lib.mac_persistent_decode_bf16_noalloc(ctypes.byref(a), _stream(device))
         _raise_on(self._lib, rc)
 
     def phase_times_ms(self, *args) -> tuple[float, float, float]:
