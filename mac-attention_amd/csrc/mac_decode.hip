@@ -513,13 +513,17 @@ __device__ __forceinline__ void stream_blocks(const KvStream& ks, const BlockLis
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) st.acc[dt] *= alpha;
     }
-    bf16x8_t pb;
+    // P goes to the PV product as bf16 hi + lo (two MFMAs per tile): the
+    // probabilities keep ~16 mantissa bits, so long spans accumulate the
+    // bf16 rounding of V only, not that of P as well.
+    bf16x8_t pb, pl;
     float psum = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float pe = fast_exp2(sv[e] - st.m);
       psum += pe;
       pb[e] = static_cast<__bf16>(pe);
+      pl[e] = static_cast<__bf16>(pe - static_cast<float>(pb[e]));
     }
     st.l += psum;
     // O^T += V^T P^T: the A operand V^T[16 dt + col][tokens 8 quad .. +8]
@@ -536,6 +540,7 @@ __device__ __forceinline__ void stream_blocks(const KvStream& ks, const BlockLis
       }
       const bf16x8_t va = __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7);
       st.acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, st.acc[dt], 0, 0, 0);
+      st.acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl, st.acc[dt], 0, 0, 0);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();

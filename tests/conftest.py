@@ -32,9 +32,13 @@ def pytest_terminal_summary(terminalreporter):
     """Decisions excused from exact parity (similarity within 1e-6 of the
     threshold), logged by helpers.near_threshold_heads."""
     try:
-        from helpers import NEAR_THRESHOLD_BAND, NEAR_THRESHOLD_LOG
+        from helpers import NEAR_THRESHOLD_BAND, NEAR_THRESHOLD_LOG, PARITY_LOG
     except Exception:  # pragma: no cover
         return
+    if PARITY_LOG:
+        terminalreporter.write_sep("-", "decode output vs oracle: largest relative L2 error per case")
+        for what, v in sorted(PARITY_LOG.items()):
+            terminalreporter.write_line(f"{v:.3e}  {what}")
     if NEAR_THRESHOLD_LOG:
         terminalreporter.write_sep("-", f"near-threshold decisions (|s - thr| <= {NEAR_THRESHOLD_BAND:g}), "
                                         "logged and excused from exact parity")

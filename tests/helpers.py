@@ -174,3 +174,12 @@ def near_threshold_heads(res, threshold=0.45, what="", requests=None):
         NEAR_THRESHOLD_LOG.append(dict(what=what, request=req, head=int(h), similarity=float(s[n, h]),
                                        threshold=threshold, oracle_hit=int(res.head["hit"][n, h])))
     return near
+
+
+# Relative L2 error of every decode output a parity test compared with the
+# oracle, by test label (printed at the end of the run).
+PARITY_LOG: dict = {}
+
+
+def log_rel_l2(what, value):
+    PARITY_LOG[what] = max(PARITY_LOG.get(what, 0.0), float(value))

@@ -20,7 +20,8 @@ import time
 import numpy as np
 import pytest
 
-from helpers import assert_close, bits, host_subset, near_threshold_heads, oracle_run, rel_l2, syn
+from helpers import (assert_close, bits, host_subset, log_rel_l2, near_threshold_heads, oracle_run, rel_l2,
+                     syn)
 
 torch = pytest.importorskip("torch")
 
@@ -83,6 +84,7 @@ def _check_subset(dev, out, out_lse, ws, sub, res, requests, what, tol=1e-2):
         np.testing.assert_array_equal(_np(ws[15])[n], res.group["mode"][i], err_msg=f"{tag} group_mode")
         got = _np(out[n])
         exp = bits(res.out[i])
+        log_rel_l2(what, rel_l2(got, exp))
         assert rel_l2(got, exp) < tol, f"{tag} out rel_l2 {rel_l2(got, exp):.3e}"
         assert_close(_np(out_lse[n]), res.out_lse[i], 2e-2, f"{tag} out_lse")
         dest = int(sub.past_lens[i]) % m
