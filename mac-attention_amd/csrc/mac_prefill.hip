@@ -669,10 +669,9 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
   }
 }
 
-// request_length[req] += len (indexed-by-request form), after the ring rows
-// were addressed with the old value.
-// request_length[req] += len for every request the window kernel wrote
-// (the validity test of request_rows: a request it skipped is not bumped).
+// request_length[req] += len (indexed-by-request form, after the ring rows
+// were addressed with the old value) for every request the window kernel
+// wrote: the validity test of request_rows, a request it skipped is not bumped.
 __global__ void bump_kernel(int32_t* request_length, const int32_t* req_ids, const int32_t* qo_indptr,
                             const int32_t* kv_indptr, int64_t total_q, int64_t kv_len_total, int B, int R) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
