@@ -164,18 +164,28 @@ class Step:
         kvl = ws[13].cpu().numpy()[: self.batch].astype(np.int64)
         hit = ws[3].cpu().numpy()[: self.batch]
         past = self.dev["past_lens"].cpu().numpy()[: self.batch].astype(np.int64)
+        ng = self.batch * self.hkv
+        # groups finished inside the match kernel (short spans): their K/V
+        # rows are read there, not by the span-attention kernel
+        fused = ws[16].cpu().numpy()[ng:2 * ng].reshape(self.batch, self.hkv) != 0
         sink = np.minimum(self.F, ne)
         tokens = sink + (ne - rb) + (kvl - ne)  # per group
         kv = int(tokens.sum()) * 2 * 2 * D
         r2t = int(tokens.max(axis=1).sum()) * 4
+        long = ~fused
+        kv_long = int(tokens[long].sum()) * 2 * 2 * D
+        r2t_long = int(np.where(long, tokens, 0).max(axis=1).sum()) * 4
         ready = not self.exact
         full_rows = int(self.hq * np.minimum(self.ring, past).sum()) * 2 * D if ready else 0
         scan = self.scan_bytes(past) if ready else 0
         cached = int(hit.sum()) * (2 * D + 4)
         heads = self.batch * self.hq
         small = heads * (2 * D + 2 * D + 2 * D + 4) + (heads * (2 * D + 2 * D + 2 * D + 4) if ready else 0)
-        attn = kv + r2t + heads * 2 * D
+        # the span-attention kernel: K/V and token indices of the long groups,
+        # partial rows of their heads written
+        attn = kv_long + r2t_long + int(long.sum()) * (self.hq // self.hkv) * 2 * D
         return dict(total=kv + r2t + scan + cached + small, attention_kernel=attn, kv=kv,
+                    fused_groups=int(fused.sum()), fused_kv=kv - kv_long,
                     ring_scan=scan, ring_scan_full_rows=full_rows, hit_heads=int(hit.sum()), heads=heads,
                     nonhit_groups=int((mode != 0).sum()), groups=int(mode.size))
 
@@ -224,7 +234,8 @@ def measure(torch, step: Step, warmup, steps, phase_runs):
         attention_kernel_gbs=round(b["attention_kernel"] / (phases[1] * 1e-3) / 1e9, 1),
         head_hit_ratio=round(b["hit_heads"] / b["heads"], 4),
         group_all_hit_fraction=round(1 - b["nonhit_groups"] / b["groups"], 4),
-        nonhit_groups=b["nonhit_groups"],
+        nonhit_groups=b["nonhit_groups"], fused_groups=b["fused_groups"],
+        fused_group_kv_bytes=b["fused_kv"],
     )
 
 

@@ -18,12 +18,15 @@ __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
-// Round to nearest even; NaN stays NaN.
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+// Round to nearest even; NaN stays NaN.  gfx950's conversion instruction
+// (one VALU op, two values when the compiler pairs them) in place of the
+// bit arithmetic.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f)); }
+// Two values in one v_cvt_pk_bf16_f32: a in the low half, b in the high.
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+  const bf16x2_v v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 __device__ __forceinline__ void unpack8(const uint4& w, float* f) {
@@ -72,7 +75,7 @@ __device__ __forceinline__ bf16x4_t lds_read_tr16(const uint16_t* p) {
 // results.
 __device__ __forceinline__ float max3_nonan(float a, float b, float c) {
   float r;
-  asm volatile("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
   return r;
 }
 __device__ __forceinline__ float max8_nonan(const float (&x)[8]) {
@@ -83,12 +86,13 @@ __device__ __forceinline__ float max8_nonan(const float (&x)[8]) {
 // an MFMA result tile) with gfx950's row-swapping VALU permutes: no LDS
 // round trip, so no wait on the wave's outstanding LDS reads.
 // v_permlane16_swap(x, x) leaves rows (r, r ^ 1) of x in its two results;
-// v_permlane32_swap(x, x) leaves rows (r, r ^ 2).
+// v_permlane32_swap(x, x) leaves rows (r, r ^ 2).  quad_max takes no NaN
+// operands (max3_nonan).
 __device__ __forceinline__ float quad_max(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const float y = max3_nonan(__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[1]));
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return max3_nonan(__uint_as_float(b[0]), __uint_as_float(b[1]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float quad_sum(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);

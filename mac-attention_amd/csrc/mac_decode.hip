@@ -635,7 +635,7 @@ __device__ __forceinline__ void merge_into(MergeState& st, float lse2, float o0,
 }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+  return pack2_bf16(a, b);
 }
 
 // =========================================================== 1. decide ====
@@ -2004,17 +2004,13 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
     const bool valid = isfinite(ring.lse);
     *reinterpret_cast<uint32_t*>(p.query_cache + rowi * kHeadDim + d0) =
         *reinterpret_cast<const uint32_t*>(p.q_pre + ho * kHeadDim + d0);
-    const uint32_t packed = valid ? (static_cast<uint32_t>(f32_to_bf16(ring.o[0])) |
-                                     (static_cast<uint32_t>(f32_to_bf16(ring.o[1])) << 16))
-                                  : 0u;
+    const uint32_t packed = valid ? pack2_bf16(ring.o[0], ring.o[1]) : 0u;
     *reinterpret_cast<uint32_t*>(p.attn_cache + rowi * kHeadDim + d0) = packed;
     if (lane == 0) p.lse_cache[rowi] = valid ? ring.lse : -INFINITY;
   }
   merge_into(ring, rest.lse, rest.o[0], rest.o[1]);
   const bool valid = isfinite(ring.lse);
-  const uint32_t packed = valid ? (static_cast<uint32_t>(f32_to_bf16(ring.o[0])) |
-                                   (static_cast<uint32_t>(f32_to_bf16(ring.o[1])) << 16))
-                                : 0u;
+  const uint32_t packed = valid ? pack2_bf16(ring.o[0], ring.o[1]) : 0u;
   *reinterpret_cast<uint32_t*>(p.out + ho * kHeadDim + d0) = packed;
   if (p.out_lse != nullptr && lane == 0) p.out_lse[ho] = valid ? ring.lse : -INFINITY;
   if (stamp) p.phase_cycles[5] = static_cast<int64_t>(wall_clock64());

@@ -238,15 +238,22 @@ __device__ __forceinline__ int request_rows(const WindowParams& p, int b) {
 //    again shared by the wave's heads.
 // LDS layouts: K chunk c (16 bytes) of key k at position c ^ (4 ((k >> 3) &
 // 3) + (k & 3)) of its 256-byte row, which puts the 16 keys one A-operand
-// read touches on 16 different 16-byte bank groups; V rows padded to 288
-// bytes, which does the same for the 4 keys x 32 bytes of a transposing read
-// and keeps its address an immediate offset per 16-dim tile.
+// read touches on 16 different 16-byte bank groups; V row k at byte
+// 288 k + 128 (k >> 3) (rows padded to 288 bytes, each group of 8 keys a
+// further 128 bytes on): a transposing read takes 32 lanes per cycle, keys
+// 8a + 4h + (0..3) and 8a + 8 + 4h + (0..3) x 32 bytes, which this puts on
+// the 32 different 8-byte bank pairs of the 64 banks (with the padding alone
+// the two key groups collide), and its address stays an immediate offset
+// per 16-dim tile.
 // Key validity of a block is one 32-bit mask in LDS; a lane turns it into
 // the mask of its 8 keys with the row's window bounds by shifts.  The running
 // maximum is moved lazily (only when a block exceeds it by 2^8), which leaves
 // the result exact and skips most accumulator rescales.
 
 constexpr int kVRow = 18;  // 16-byte units per staged V row: 256 bytes + 32 of padding
+// 16-byte position of V row k in the staged tile
+__device__ __forceinline__ int v_row(int k) { return k * kVRow + 8 * (k >> 3); }
+constexpr int kVTile = kBlk * kVRow + 8 * (kBlk / 8 - 1);  // 16-byte units of a staged V tile
 
 // Residency: the one-head-per-wave window pass fits 168 VGPRs, so it runs
 // three workgroups per CU (more waves per SIMD to overlap the softmax VALU
@@ -261,7 +268,7 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
   int* s_kv = s_dyn + 2 * (p.B + 1);
   __shared__ int s_part[kWaves];
   __shared__ uint4 s_k[2][kBlk * 16];  // K rows of a 32-key block (swizzled)
-  __shared__ uint4 s_v[2][kBlk * kVRow];  // V rows of the block (padded rows)
+  __shared__ uint4 s_v[2][kVTile];  // V rows of the block (v_row layout)
   __shared__ uint32_t s_okw[2][kWaves];  // per wave: bits of its 8 keys that have a pool row
 
   const int tid = threadIdx.x;
@@ -313,7 +320,7 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
   constexpr int kHeadsPerTask = 4 * HPW;
   const int nchunks = ceil_div(G, kHeadsPerTask);
   const int total_tasks = s_boff[B] * Hkv * nchunks;
-  const int64_t kv_stride = static_cast<int64_t>(Hkv) * kHeadDim;
+  const uint32_t row_bytes = static_cast<uint32_t>(Hkv) * kHeadDim * 2;  // one pool row of K or V
   const unsigned pool_rows = static_cast<unsigned>(min(p.pool_tokens, static_cast<int64_t>(INT_MAX)));
   // keys [pos - wl, pos] form a row's window (wl < 0: [0, pos])
   const int wl = kRectify ? p.S - 1 : p.window_left;
@@ -322,8 +329,8 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
   const int ld_key = 2 * (tid >> 4), ld_chunk = tid & 15;
   const int ld_pk0 = ld_key * 16 + (ld_chunk ^ (4 * ((ld_key >> 3) & 3) + (ld_key & 3)));
   const int ld_pk1 = (ld_key + 1) * 16 + (ld_chunk ^ (4 * (((ld_key + 1) >> 3) & 3) + ((ld_key + 1) & 3)));
-  const int ld_pv0 = ld_key * kVRow + ld_chunk;
-  const int ld_pv1 = (ld_key + 1) * kVRow + ld_chunk;
+  const int ld_pv0 = v_row(ld_key) + ld_chunk;
+  const int ld_pv1 = v_row(ld_key + 1) + ld_chunk;
   // compute side: K A-operand positions (tile t, k-step s) and V^T read
   // addresses (16-dim tile dt, half h) of this lane
   int pk[2][4];
@@ -338,7 +345,7 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
   // 16 dt + 4 (j & 3) .. + 3: element offset pv[h] + 16 dt of the V tile
   int pv[2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) pv[h] = (8 * quad + 4 * h + (col >> 2)) * (kVRow * 8) + 4 * (col & 3);
+  for (int h = 0; h < 2; ++h) pv[h] = v_row(8 * quad + 4 * h + (col >> 2)) * 8 + 4 * (col & 3);
 
   for (int task = blockIdx.x; task < total_tasks; task += gridDim.x) {
     __syncthreads();  // the previous task's waves are done with the tiles
@@ -393,18 +400,29 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
       }
     }
 
-    float m[HPW], l[HPW];
-    f32x4_t acc[HPW][8];
+    // l[h]: the softmax row sums.  Plain form: the lane's fp32 partial sums
+    // in l[h][0] (reduced over the row's four lanes at the end).  Fused form:
+    // accumulated by MFMAs with an all-ones A operand over P = hi + lo (every
+    // element of the lane's l[h] then holds its row's sum), off the VALU; the
+    // plain form cannot do that, since its P is bf16 hi alone and the sum of
+    // that is ~2^-9 off per key, beyond what its lse output allows.
+    float m[HPW];
+    f32x4_t acc[HPW][8], l[HPW];
 #pragma unroll
     for (int i = 0; i < HPW; ++i) {
       m[i] = kNegBig;
-      l[i] = 0.0f;
+      l[i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) acc[i][dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    const uint16_t* kbase = p.k + static_cast<int64_t>(hkv) * kHeadDim + ld_chunk * 8;
-    const uint16_t* vbase = p.v + static_cast<int64_t>(hkv) * kHeadDim + ld_chunk * 8;
+    const char* kbase = reinterpret_cast<const char*>(p.k + static_cast<int64_t>(hkv) * kHeadDim + ld_chunk * 8);
+    const char* vbase = reinterpret_cast<const char*>(p.v + static_cast<int64_t>(hkv) * kHeadDim + ld_chunk * 8);
+    // this request's kv_indices; entry offsets fit 32 bits (fewer than 2^30
+    // entries, checked on the host), so a load is a uniform base plus a
+    // 32-bit lane offset
+    const char* kvi = reinterpret_cast<const char*>(p.kv_indices + kv_begin);
+    bool fresh = true;  // no block computed yet: the first sets m without a rescale
     // segment 0: the front sink [0, min(F, w_lo)) of each row (fused form,
     // sink_mode 1); segment 1: the window [w_lo, pos]
     for (int seg = sink ? 0 : 1; seg < 2; ++seg) {
@@ -419,15 +437,15 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
       // the wait for it never includes K/V loads issued after it (the memory
       // counter retires in order).
       auto index_of = [&](int i, int t) -> int {
-        const int key = seg_lo + i * kBlk + ld_key + t;
-        return p.kv_indices[kv_begin + min(key, kvlen - 1)];
+        const uint32_t key = static_cast<uint32_t>(seg_lo + i * kBlk + ld_key + t);
+        return *reinterpret_cast<const int*>(kvi + min(key, static_cast<uint32_t>(kvlen - 1)) * 4u);
       };
       auto row_of = [&](int i, int t, int raw) -> int {
         const int key = seg_lo + i * kBlk + ld_key + t;
         return (key < seg_hi && static_cast<unsigned>(raw) < pool_rows) ? raw : -1;
       };
-      auto ld = [&](const uint16_t* base, int r) -> uint4 {
-        return *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(max(r, 0)) * kv_stride);
+      auto ld = [&](const char* base, int r) -> uint4 {  // one v_mad_u64_u32 per address
+        return *reinterpret_cast<const uint4*>(base + static_cast<uint64_t>(static_cast<uint32_t>(max(r, 0))) * row_bytes);
       };
       // the loader's K/V chunks of the block in flight (rc0/rc1: their rows)
       // and the raw indices of the block after it
@@ -449,10 +467,14 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
         {
           s_k[buf][ld_pk0] = kq0;
           s_k[buf][ld_pk1] = kq1;
-          const uint32_t z0 = rc0 >= 0 ? 0xffffffffu : 0u, z1 = rc1 >= 0 ? 0xffffffffu : 0u;
-          s_v[buf][ld_pv0] = make_uint4(vq0.x & z0, vq0.y & z0, vq0.z & z0, vq0.w & z0);
-          s_v[buf][ld_pv1] = make_uint4(vq1.x & z1, vq1.y & z1, vq1.z & z1, vq1.w & z1);
           const uint64_t b0 = __ballot(rc0 >= 0), b1 = __ballot(rc1 >= 0);
+          if ((b0 & b1) != ~0ull) {  // a masked key in the wave's rows: zero its V row (P is 0 there, V may be NaN)
+            const uint32_t z0 = rc0 >= 0 ? 0xffffffffu : 0u, z1 = rc1 >= 0 ? 0xffffffffu : 0u;
+            vq0 = make_uint4(vq0.x & z0, vq0.y & z0, vq0.z & z0, vq0.w & z0);
+            vq1 = make_uint4(vq1.x & z1, vq1.y & z1, vq1.z & z1, vq1.w & z1);
+          }
+          s_v[buf][ld_pv0] = vq0;
+          s_v[buf][ld_pv1] = vq1;
           if (lane == 0) {
             // lanes 16 r hold keys 8 wave + 2 r and 8 wave + 2 r + 1
             uint32_t bits = 0;
@@ -535,12 +557,16 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
             for (int r = 0; r < 4; ++r) sv[4 * t + r] = c4[h][t][r];
           float bmax = max8_nonan(sv);
           bmax = quad_max(bmax);
-          // lazy move of the reference point: p <= 2^8 stays exact in fp32
+          // lazy move of the reference point: p <= 2^8 stays exact in fp32;
+          // on the first block acc and l are still zero, nothing to rescale
+          // (a select, so that the branch below is the only one)
+          m[h] = fresh ? max3_nonan(m[h], bmax, bmax) : m[h];
           if (__any(bmax * p.q_scale > m[h] * p.q_scale + 8.0f)) {
-            const float m_new = fmaxf(m[h], bmax);
+            const float m_new = max3_nonan(m[h], bmax, bmax);
             const float alpha = fast_exp2((m[h] - m_new) * p.q_scale);
             m[h] = m_new;
-            l[h] *= alpha;
+            if (kRectify) l[h] *= alpha;
+            else l[h][0] *= alpha;
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) acc[h][dt] *= alpha;
           }
@@ -549,7 +575,7 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const float pe = fast_exp2(fmaf(sv[e], p.q_scale, mo));
-            psum += pe;
+            if (!kRectify) psum += pe;
             pb[h][e] = static_cast<__bf16>(pe);
             // The fused form also feeds the bf16 rounding residual of P
             // through a second MFMA (P = hi + lo, ~16 significant bits): the
@@ -558,9 +584,18 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
             // window state.
             if (kRectify) pl[h][e] = static_cast<__bf16>(pe - static_cast<float>(pb[h][e]));
           }
-          l[h] += psum;
+          if (!kRectify) l[h][0] += psum;
         }
-        // O^T += V^T P^T
+        fresh = false;
+        // O^T += V^T P^T (fused form: l += 1^T P^T as well)
+        const bf16x8_t ones = as_bf16x8(make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u));
+#pragma unroll
+        for (int h = 0; h < HPW; ++h) {
+          if (kRectify) {
+            l[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[h], l[h], 0, 0, 0);
+            l[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pl[h], l[h], 0, 0, 0);
+          }
+        }
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
@@ -577,15 +612,15 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
 #pragma unroll
       for (int h = 0; h < HPW; ++h) {
         if (h >= nheads) break;
-        const float lt = quad_sum(l[h]);
+        const float lt = quad_sum(l[h][0]);
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
         const int hq = hkv * G + hg0 + h;
         uint16_t* op = p.out + (grow * Hq + hq) * kHeadDim + 4 * quad;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
           uint2 w;
-          w.x = f32_to_bf16(acc[h][dt][0] * inv) | (static_cast<uint32_t>(f32_to_bf16(acc[h][dt][1] * inv)) << 16);
-          w.y = f32_to_bf16(acc[h][dt][2] * inv) | (static_cast<uint32_t>(f32_to_bf16(acc[h][dt][3] * inv)) << 16);
+          w.x = pack2_bf16(acc[h][dt][0] * inv, acc[h][dt][1] * inv);
+          w.y = pack2_bf16(acc[h][dt][2] * inv, acc[h][dt][3] * inv);
           *reinterpret_cast<uint2*>(op + 16 * dt) = w;
         }
         if (quad == 0) p.out_lse[grow * Hq + hq] = lt > 0.0f ? (m[h] * p.q_scale + fast_log2(lt)) * kLn2 : -INFINITY;
@@ -628,7 +663,7 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
     for (int hh = 0; hh < HPW; ++hh) {
       if (hh >= nheads) break;
       const int h = hkv * G + hg0 + hh;
-      const float lt = quad_sum(l[hh]);
+      const float lt = l[hh][0];
       const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
       const float lse_w = lt > 0.0f ? (m[hh] * p.q_scale + fast_log2(lt)) * kLn2 : -INFINITY;
       Downdate c;
@@ -648,8 +683,8 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
 #pragma unroll
         for (int i = 0; i < 4; ++i) r[i] = empty ? 0.0f : (fo[i] - c.t * (acc[hh][dt][i] * inv)) * c.scale;
         uint2 w;
-        w.x = f32_to_bf16(r[0]) | (static_cast<uint32_t>(f32_to_bf16(r[1])) << 16);
-        w.y = f32_to_bf16(r[2]) | (static_cast<uint32_t>(f32_to_bf16(r[3])) << 16);
+        w.x = pack2_bf16(r[0], r[1]);
+        w.y = pack2_bf16(r[2], r[3]);
         *reinterpret_cast<uint2*>(ap + 16 * dt) = w;
       }
       if (quad == 0) p.lse_cache[drow * Hq + h] = (p.sink_mode == 0 && p.F > 0) ? -INFINITY : c.lse;
@@ -753,13 +788,16 @@ extern "C" int mac_update_then_downdate_bf16_inplace(const void* out1, const voi
 namespace {
 
 int check_window_common(int B, int Hq, int Hkv, int D, int64_t total_q, int64_t pool, const void* q,
-                        const void* k, const void* v, const int32_t* qo, const int32_t* kvp, const int32_t* kvi) {
+                        const void* k, const void* v, const int32_t* qo, const int32_t* kvp, const int32_t* kvi,
+                        int64_t kv_len) {
   REQUIRE(D == kHeadDim, "head_dim must be 128 (got %d)", D);
   REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0, "Hq must be a positive multiple of Hkv");
   REQUIRE(B >= 0 && B <= kMaxB, "B must be in [0, %d] (got %d)", kMaxB, B);
   REQUIRE(total_q >= 0 && total_q <= INT_MAX && pool > 0, "bad total_q / pool_tokens");
   REQUIRE(total_q * Hq <= static_cast<int64_t>(INT_MAX) * 64, "total_q too large");
   REQUIRE(q && k && v && qo && kvp && kvi, "null pointer argument");
+  // the window kernel addresses a request's kv_indices with 32-bit byte offsets
+  REQUIRE(kv_len >= 0 && kv_len < (int64_t{1} << 30), "kv_indices must hold fewer than 2^30 entries");
   return MAC_OK;
 }
 
@@ -771,7 +809,7 @@ extern "C" int mac_prefill_window_attention_bf16(const MacWindowAttentionArgs* a
           sizeof(MacWindowAttentionArgs));
   REQUIRE(a->abi_version == MAC_ABI_VERSION, "abi_version mismatch");
   if (int rc = check_window_common(a->B, a->Hq, a->Hkv, a->D, a->total_q, a->pool_tokens, a->q, a->k_buffer,
-                                   a->v_buffer, a->qo_indptr, a->kv_indptr, a->kv_indices))
+                                   a->v_buffer, a->qo_indptr, a->kv_indptr, a->kv_indices, a->kv_indices_len))
     return rc;
   REQUIRE(a->out && a->out_lse, "out / out_lse must not be NULL");
   if (a->B == 0 || a->total_q == 0) return MAC_OK;
@@ -805,7 +843,7 @@ extern "C" int mac_prefill_rectify_update_cache_bf16(const MacRectifyArgs* a, vo
           sizeof(MacRectifyArgs));
   REQUIRE(a->abi_version == MAC_ABI_VERSION, "abi_version mismatch");
   if (int rc = check_window_common(a->B, a->Hq, a->Hkv, a->D, a->total_q, a->pool_tokens, a->q_post, a->k_buffer,
-                                   a->v_buffer, a->qo_indptr, a->kv_indptr, a->kv_indices))
+                                   a->v_buffer, a->qo_indptr, a->kv_indptr, a->kv_indices, a->kv_indices_len))
     return rc;
   REQUIRE(a->M > 0, "capacity (M) must be > 0");
   REQUIRE(a->R > 0, "R must be > 0");
