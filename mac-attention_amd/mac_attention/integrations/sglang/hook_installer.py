@@ -11,14 +11,17 @@ so installing twice is a no-op.
 Targets, by group:
   * server arguments: the MAC settings and flags (plugin.py);
   * scheduler: which prefill rows reach the ring (schedule_hooks.py);
-  * models: LlamaAttention and the Qwen2 / Qwen3 MoE attentions keep their
-    pre-RoPE queries and hand the layer's MAC state to the attention backend
-    (model_hooks.py; the Qwen classes are optional);
-  * FlashInfer backend: settings at construction, the ring update after each
-    prefill chunk (forward_extend) and the fused MAC decode step
-    (forward_decode).
+  * models: the model forward prepares the batch state once; LlamaAttention
+    and the Qwen2 / Qwen3 MoE attentions keep their pre-RoPE queries and
+    hand the layer's MAC state to the attention backend (model_hooks.py; the
+    Qwen classes are optional);
+  * FlashInfer backend: settings at construction, the ring marks kept on the
+    backend (init_forward_metadata), the ring update after each prefill
+    chunk (forward_extend) and the fused MAC decode step (forward_decode).
 Profiling-only and CUDA-graph-trace hooks of the reference are not part of
-this build.
+this build, nor its decode-graph metadata skipping and the wait for
+side-stream ring updates before a graph replay: the ring update here runs
+on the compute stream, in order with the replay.
 """
 
 from __future__ import annotations
@@ -36,6 +39,11 @@ _ATTN_CLASSES = (
     ("sglang.srt.models.llama", "LlamaAttention", False),
     ("sglang.srt.models.qwen2_moe", "Qwen2MoeAttention", True),
     ("sglang.srt.models.qwen3_moe", "Qwen3MoeAttention", True),
+)
+_MODEL_CLASSES = (
+    ("sglang.srt.models.llama", "LlamaModel", False),
+    ("sglang.srt.models.qwen2_moe", "Qwen2MoeModel", True),
+    ("sglang.srt.models.qwen3_moe", "Qwen3MoeModel", True),
 )
 _FLASHINFER = "sglang.srt.layers.attention.flashinfer_backend:FlashInferAttnBackend"
 
@@ -70,8 +78,12 @@ def iter_hook_specs() -> Iterable[HookSpec]:
     for module, cls, optional in _ATTN_CLASSES:
         yield HookSpec(f"{module}:{cls}.__init__", model_hooks.attention_init_after, "after", optional)
         yield HookSpec(f"{module}:{cls}.forward", model_hooks.attention_forward_around, "around", optional)
+    for module, cls, optional in _MODEL_CLASSES:
+        yield HookSpec(f"{module}:{cls}.forward", model_hooks.model_forward_around, "around", optional)
 
     yield HookSpec(f"{_FLASHINFER}.__init__", model_hooks.flashinfer_backend_init_after, "after")
+    yield HookSpec(f"{_FLASHINFER}.init_forward_metadata", model_hooks.flashinfer_init_forward_metadata_around,
+                   "around")
     yield HookSpec(f"{_FLASHINFER}.forward_extend", model_hooks.flashinfer_forward_extend_around, "around")
     yield HookSpec(f"{_FLASHINFER}.forward_decode", flashinfer_forward_decode_around, "around")
 

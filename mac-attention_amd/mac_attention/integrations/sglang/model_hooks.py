@@ -4,7 +4,8 @@ prefill chunk inside FlashInfer's forward_extend.
 
 Behaviour follows the reference's llama_hooks.py (attention forward
 :1341-1470, MACMetadata.prepare_forward_batch :932-1029, Qwen MoE attention
-:1064-1284) and flashinfer_hooks.py (forward_extend :2847-3010, prefill ring
+:1064-1284, model forward :1852-1876) and flashinfer_hooks.py
+(init_forward_metadata :703-735, forward_extend :2847-3010, prefill ring
 update :2237-2490).  The design here is this build's: one forward wrapper
 serves every supported attention class (a Qwen3 attention's q/k norm is
 applied when the module has one), the batch bookkeeping is one
@@ -69,33 +70,77 @@ def ensure_layer_state(module: Any, forward_batch: Any, hidden_states: torch.Ten
     return meta
 
 
-def prepare_batch(meta: Any, forward_batch: Any) -> None:
-    """Per-batch request bookkeeping (llama_hooks.py:932-1029): request ids,
-    the tokens already cached before this step (``cache_lens`` = seq_len -
-    new tokens, the decode step's past_len) and ``req_len`` by request, in
-    one mac_update_request_state launch."""
+_BATCH_STATE = "_mac_batch_state"
+
+
+def batch_state(forward_batch: Any, device: torch.device, *, fresh: bool = False) -> dict:
+    """The forward's request ids, sequence lengths and new-token counts as
+    int32 device tensors (plus host copies when they are at hand).  The model
+    forward hook builds it once per forward (``fresh``) and every layer
+    reuses it (llama_hooks.py:1852-1876 prepares the batch once in the model
+    forward); without that hook each layer builds its own and keeps none, so
+    a forward batch object reused across forwards never serves stale
+    lengths."""
+    cached = getattr(forward_batch, _BATCH_STATE, None)
+    if not fresh and cached is not None and cached["device"] == device:
+        return cached
     b = int(forward_batch.batch_size)
-    if b <= 0 or meta.req_ids is None:
-        return
-    dev = meta.req_ids.device
-    meta.req_ids[:b].copy_(forward_batch.req_pool_indices[:b].to(device=dev, dtype=torch.int32))
     capturing = persistent.is_graph_capturing()
-    meta.req_ids_host = None if capturing else _host_ints(forward_batch.req_pool_indices, b) or \
-        [int(x) for x in forward_batch.req_pool_indices[:b].tolist()]
-    seq = forward_batch.seq_lens[:b].to(device=dev, dtype=torch.int32)
+    req = forward_batch.req_pool_indices[:b].to(device=device, dtype=torch.int32)
+    seq = forward_batch.seq_lens[:b].to(device=device, dtype=torch.int32)
     if forward_batch.forward_mode.is_decode_or_idle():
         cur = torch.ones_like(seq)
     elif getattr(forward_batch, "extend_seq_lens", None) is not None:
-        cur = forward_batch.extend_seq_lens[:b].to(device=dev, dtype=torch.int32)
+        cur = forward_batch.extend_seq_lens[:b].to(device=device, dtype=torch.int32)
     else:
-        cur = torch.tensor(forward_batch.extend_seq_lens_cpu[:b], dtype=torch.int32, device=dev)
+        cur = torch.tensor(forward_batch.extend_seq_lens_cpu[:b], dtype=torch.int32, device=device)
+    req_host = None
+    if not capturing:
+        req_host = _host_ints(forward_batch.req_pool_indices, b) or [int(x) for x in req.tolist()]
     seq_host = None if capturing else _host_ints(getattr(forward_batch, "seq_lens_cpu", None), b)
-    if seq_host:
-        meta.cur_kv_len = max(seq_host)
+    state = dict(device=device, batch=b, req_ids=req, seq=seq, cur=cur, req_ids_host=req_host, seq_host=seq_host)
+    if fresh:
+        try:
+            setattr(forward_batch, _BATCH_STATE, state)
+        except AttributeError:  # a batch object that takes no new attributes: built per layer
+            pass
+    return state
+
+
+def prepare_batch(meta: Any, forward_batch: Any) -> None:
+    """Per-layer request bookkeeping (llama_hooks.py:932-1029): request ids,
+    the tokens already cached before this step (``cache_lens`` = seq_len -
+    new tokens, the decode step's past_len) and ``req_len`` by request, in
+    one mac_update_request_state launch, from the forward's batch_state."""
+    b = int(forward_batch.batch_size)
+    if b <= 0 or meta.req_ids is None:
+        return
+    st = batch_state(forward_batch, meta.req_ids.device)
+    meta.req_ids[:b].copy_(st["req_ids"])
+    meta.req_ids_host = st["req_ids_host"]
+    if st["seq_host"]:
+        meta.cur_kv_len = max(st["seq_host"])
     match = getattr(meta, "match_req_len", None)
     if match is None:
         match = meta.match_req_len = torch.zeros_like(meta.req_len)
-    meta.cache_ext.mac_update_request_state(meta.req_len, match, meta.cache_lens[:b], meta.req_ids[:b], seq, cur)
+    meta.cache_ext.mac_update_request_state(meta.req_len, match, meta.cache_lens[:b], meta.req_ids[:b], st["seq"],
+                                            st["cur"])
+
+
+def model_forward_around(original_fn: Any, self: Any, *args: Any, **kwargs: Any) -> Any:
+    """LlamaModel / Qwen MoE model forward (input_ids, positions,
+    forward_batch, ...): the settings and the batch state are attached to the
+    forward batch once, before any layer runs (llama_hooks.py:1852-1876)."""
+    input_ids = kwargs.get("input_ids", args[0] if len(args) > 0 else None)
+    positions = kwargs.get("positions", args[1] if len(args) > 1 else None)
+    forward_batch = kwargs.get("forward_batch", args[2] if len(args) > 2 else None)
+    config = get_mac_config()
+    if config.enable_mac and forward_batch is not None and int(getattr(forward_batch, "batch_size", 0) or 0) > 0:
+        ref = positions if torch.is_tensor(positions) else input_ids
+        if torch.is_tensor(ref) and ref.device.type == "cuda":
+            forward_batch.mac_config = config
+            batch_state(forward_batch, ref.device, fresh=True)
+    return original_fn(self, *args, **kwargs)
 
 
 # ----------------------------------------------------- attention forward ----
@@ -161,6 +206,23 @@ def attention_forward_around(original_fn: Any, self: Any, *args: Any, **kwargs: 
 def flashinfer_backend_init_after(result: Any, self: Any, *args: Any, **kwargs: Any) -> Any:
     """FlashInferAttnBackend.__init__: the settings the hooks read."""
     self.mac_config = get_mac_config()
+    return result
+
+
+def flashinfer_init_forward_metadata_around(original_fn: Any, self: Any, forward_batch: Any, *args: Any,
+                                            **kwargs: Any) -> Any:
+    """FlashInferAttnBackend.init_forward_metadata (flashinfer_hooks.py:703-735):
+    SGLang's own metadata, then the scheduler's ring marks and the chunk's
+    prefix / extend lengths kept on the backend as well.  A piecewise
+    CUDA-graph replay runs forward_extend on a static forward batch that
+    lost these plugin attributes; the suffix plan falls back to the
+    backend's copies (prefill_suffix.build_prefill_suffix_plan)."""
+    result = original_fn(self, forward_batch, *args, **kwargs)
+    config = getattr(self, "mac_config", None) or get_mac_config()
+    if config.enable_mac:
+        self.mac_prefill_cache_update_starts_current = getattr(forward_batch, "mac_prefill_cache_update_starts", None)
+        self.mac_extend_prefix_lens_cpu_current = getattr(forward_batch, "extend_prefix_lens_cpu", None)
+        self.mac_extend_seq_lens_cpu_current = getattr(forward_batch, "extend_seq_lens_cpu", None)
     return result
 
 

@@ -112,6 +112,19 @@ def install(monkeypatch):
 
     llama.LlamaAttention = LlamaAttention
 
+    class LlamaModel:
+        def __init__(self, layers):
+            self.layers = layers
+
+        def forward(self, input_ids, positions, forward_batch, input_embeds=None):
+            calls.append("LlamaModel.forward (SGLang's own)")
+            h = input_embeds
+            for layer in self.layers:
+                h = layer.forward(positions, h, forward_batch)
+            return h
+
+    llama.LlamaModel = LlamaModel
+
     fi = _module(monkeypatch, "sglang.srt.layers.attention.flashinfer_backend")
 
     class FlashInferAttnBackend:
@@ -121,6 +134,10 @@ def install(monkeypatch):
 
         def _get_wrapper_idx(self, layer):
             return 0
+
+        def init_forward_metadata(self, forward_batch):
+            calls.append("FlashInferAttnBackend.init_forward_metadata (SGLang's own)")
+            self.forward_metadata = types.SimpleNamespace(use_ragged=False, forward_batch=forward_batch)
 
         def forward_extend(self, q, k, v, layer, forward_batch, save_kv_cache=True):
             calls.append("FlashInferAttnBackend.forward_extend (SGLang's own)")
@@ -161,5 +178,6 @@ def install(monkeypatch):
 
     dpc.run_data_parallel_controller_process = run_data_parallel_controller_process
     return types.SimpleNamespace(ServerArgs=ServerArgs, ScheduleBatch=ScheduleBatch, ForwardBatch=ForwardBatch,
-                                 LlamaAttention=LlamaAttention, FlashInferAttnBackend=FlashInferAttnBackend,
+                                 LlamaAttention=LlamaAttention, LlamaModel=LlamaModel,
+                                 FlashInferAttnBackend=FlashInferAttnBackend,
                                  engine=engine, http=http, dpc=dpc, scheduler=scheduler, calls=calls)

@@ -29,7 +29,9 @@ REQUIRED = {
     "sglang.srt.model_executor.forward_batch_info:ForwardBatch.init_new",
     "sglang.srt.models.llama:LlamaAttention.__init__",
     "sglang.srt.models.llama:LlamaAttention.forward",
+    "sglang.srt.models.llama:LlamaModel.forward",
     "sglang.srt.layers.attention.flashinfer_backend:FlashInferAttnBackend.__init__",
+    "sglang.srt.layers.attention.flashinfer_backend:FlashInferAttnBackend.init_forward_metadata",
     "sglang.srt.layers.attention.flashinfer_backend:FlashInferAttnBackend.forward_extend",
     "sglang.srt.layers.attention.flashinfer_backend:FlashInferAttnBackend.forward_decode",
 }
@@ -164,3 +166,60 @@ def test_pyproject_declares_the_plugin_entry_point():
     mod_name, fn = eps["mac_attention"].split(":")
     __import__(mod_name)
     assert callable(getattr(sys.modules[mod_name], fn))
+
+
+def test_backend_keeps_ring_marks_for_static_graph_batches(sg, monkeypatch):
+    """init_forward_metadata copies the marks onto the backend; a forward batch
+    that lost them (piecewise CUDA-graph replay) plans the same ring rows
+    (flashinfer_hooks.py:703-735)."""
+    from mac_attention.integrations.sglang.prefill_suffix import build_prefill_suffix_plan
+
+    monkeypatch.setenv("MAC_ATTENTION_ENABLE", "1")
+    hook_installer.install_hooks(strict=True)
+    backend = sg.FlashInferAttnBackend()
+    live = sg.ForwardBatch(batch_size=3, mac_prefill_cache_update_starts=[-1, 0, 30],
+                           extend_prefix_lens_cpu=[0, 0, 30], extend_seq_lens_cpu=[60, 10, 10])
+    backend.init_forward_metadata(live)
+    assert "FlashInferAttnBackend.init_forward_metadata (SGLang's own)" in sg.calls
+    assert backend.mac_prefill_cache_update_starts_current == [-1, 0, 30]
+    want = build_prefill_suffix_plan(live, 3, 80, allow_backend_fallback=False)
+    static = sg.ForwardBatch(batch_size=3, attn_backend=backend)
+    got = build_prefill_suffix_plan(static, 3, 80)
+    assert want is not None and got is not None
+    assert (got.offsets, got.kv_offsets, got.req_indices, got.request_lengths) == \
+        (want.offsets, want.kv_offsets, want.req_indices, want.request_lengths)
+    assert build_prefill_suffix_plan(static, 3, 80, allow_backend_fallback=False) is None
+
+
+def test_batch_state_is_computed_once_per_forward(sg):
+    """The model forward's batch state (request ids, lengths, new tokens) is
+    built once and shared by every layer (llama_hooks.py:1852-1876)."""
+    from mac_attention.integrations.sglang import model_hooks
+    from sglang_standin import ForwardMode
+
+    cpu = torch.device("cpu")
+    fb = sg.ForwardBatch(batch_size=2, req_pool_indices=torch.tensor([5, 2]), seq_lens=torch.tensor([9, 4]),
+                         forward_mode=ForwardMode(decode=True), seq_lens_cpu=torch.tensor([9, 4]))
+    st = model_hooks.batch_state(fb, cpu, fresh=True)  # the model forward
+    assert model_hooks.batch_state(fb, cpu) is st  # its layers
+    fb.seq_lens = torch.tensor([10, 5])  # the next forward on the same object rebuilds it
+    assert model_hooks.batch_state(fb, cpu, fresh=True)["seq"].tolist() == [10, 5]
+    assert model_hooks.batch_state(sg.ForwardBatch(**{k: v for k, v in vars(fb).items()
+                                                      if k != "_mac_batch_state"}), cpu) is not st
+    assert st["req_ids"].dtype == torch.int32 and st["req_ids"].tolist() == [5, 2]
+    assert st["cur"].tolist() == [1, 1] and st["seq_host"] == [9, 4] and st["req_ids_host"] == [5, 2]
+    ext = sg.ForwardBatch(batch_size=2, req_pool_indices=torch.tensor([1, 3]), seq_lens=torch.tensor([20, 7]),
+                          forward_mode=ForwardMode(decode=False), extend_seq_lens=torch.tensor([12, 7]))
+    assert model_hooks.batch_state(ext, cpu)["cur"].tolist() == [12, 7]
+
+
+def test_model_forward_hook_passes_through(sg, monkeypatch):
+    monkeypatch.setenv("MAC_ATTENTION_ENABLE", "1")
+    hook_installer.install_hooks(strict=True)
+    ident = lambda x: (x, None)  # noqa: E731
+    attn = sg.LlamaAttention(2, 1, 4, ident, lambda pos, q, k: (q, k), lambda q, k, v, fb: q, ident)
+    model = sg.LlamaModel([attn])
+    x = torch.arange(16.0).view(1, 16)
+    out = model.forward(None, torch.zeros(1, dtype=torch.long), types.SimpleNamespace(batch_size=1), input_embeds=x)
+    assert torch.equal(out, x[:, :8])  # CPU tensors: SGLang's own forward, no MAC state
+    assert "LlamaModel.forward (SGLang's own)" in sg.calls
