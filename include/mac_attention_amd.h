@@ -63,7 +63,7 @@ enum { MAC_GROUP_MAC_HIT = 0, MAC_GROUP_FULL_FALLBACK = 1, MAC_GROUP_MIXED = 2 }
  * Workspaces (caller-owned, any content on entry):
  *   match_dist f32, match_pos/match_slot i32 [N, Hq, max_match_tiles]
  *   head_* i32 [N, Hq]; group_* i32 [N, Hkv] (leading dimension may exceed N)
- *   complete_task_go/tile i32 [complete_task_len >= 2 N Hkv + 2]
+ *   complete_task_go/tile i32 [complete_task_len >= 2 N Hkv + 6]
  *   task_counts i32 [>= 9]
  *   partial_o (f32, or bf16 if partial_o_is_bf16) [>= N, Hkv, max_tiles_context, G, D]
  *   partial_lse f32 [>= N, Hkv, max_tiles_context, G]

@@ -33,6 +33,11 @@
 //   group_rect_tiles / group_tail_tiles: number of band / tail tasks;
 //   complete_task_go[g]: chunk size C_g of group g; complete_task_tile[g]:
 //     number of tasks of group g (written by workgroup 0 of span_attention);
+//     complete_task_go[NG + g]: 1 if match_decide finished group g;
+//     complete_task_go[2 NG]: 1 if any group was left to span_attention;
+//     complete_task_go[2 NG + 2 .. + 4]: the previous step's short groups,
+//     long groups and tokens / 64 (step_fuse_rule);
+//     complete_task_tile[NG]: span_attention's task counter (NG = N Hkv);
 //   match_dist/pos/slot[..., 0]: best (distance, position, slot) of the scan;
 //   partial_o / partial_lse: one (o, lse) partial per task and head;
 //   task_counts: [0] tasks, [1] tail tasks, [3] non-hit groups whose band spans
@@ -103,6 +108,11 @@ struct DecideParams {
   int fuse_tokens;
   int32_t* group_fused;
   int32_t* long_groups;  // set to 1 by every group left to span_attention
+  // The previous step's counts for the short-group rule (step_fuse_rule;
+  // NULL: every short group is finished here)
+  const uint32_t* fuse_sync;
+  int fuse_cus;                // span_attention's workgroups in narrow mode
+  long long narrow_min_tokens;  // span_attention's narrow-mode threshold
   const uint16_t* q_post;
   const uint16_t* k_buffer;
   const uint16_t* v_buffer;
@@ -152,6 +162,8 @@ struct AttnParams {
   float q_scale;  // sm_scale * log2(e)
   const int32_t* group_fused;  // groups match_decide finished (no tasks here)
   const int32_t* long_groups;  // 0: match_decide finished every group
+  uint32_t* fuse_sync;         // workgroup 0 leaves the step's counts for the next step's short-group rule
+  int fuse_tokens;             // (NULL: no rule) a group of at most fuse_tokens tokens is short
   int plan_bucket;             // groups per entry of the plan's LDS offset table
   int64_t* phase_cycles;
 };
@@ -185,6 +197,29 @@ struct MergeParams {
   int32_t* long_groups;  // cleared here for the next step
   int64_t* phase_cycles;
 };
+
+// Whether this step's short groups are finished here.  Finishing a short
+// group in this kernel takes it out of span_attention and merge_write but
+// adds its stream to this kernel, which runs before them: worth it when no
+// group is long (span_attention and merge_write then have nothing to do), or
+// when span_attention runs one workgroup per CU and the short groups' band
+// and tail tasks would need more than one round of them.  Otherwise they are
+// left to span_attention, where they fill the workgroups that finish their
+// long tasks first.  The counts the rule needs are the whole step's, which a
+// workgroup cannot know when it decides (a device-wide count and wait, or
+// even just counting with atomics on shared words, cost more than the rule
+// saves), so it reads the previous step's, which span_attention's workgroup
+// 0 leaves in fuse_sync: [0] short groups, [1] long groups, [2] tokens / 64.
+// Decode steps of a batch change slowly, so the previous step's counts are
+// the usual case; the rule only moves work between kernels, and every group
+// gets the same results either way.
+__device__ __forceinline__ int step_fuse_rule(const DecideParams& p) {
+  const uint32_t* c = p.fuse_sync;
+  const uint32_t n_short = c[0], n_long = c[1];
+  const long long all_tokens = static_cast<long long>(c[2]) << 6;
+  if (n_long == 0) return 1;
+  return (all_tokens >= p.narrow_min_tokens && 2ll * n_short > p.fuse_cus) ? 1 : 0;
+}
 
 // DECODE:221-230.  A request id outside [0, R) is never ready: its ring rows
 // cannot be addressed, so it must not be matched against or written.
@@ -653,6 +688,9 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 // reduces the tiles (kMode 2) instead of scanning.  kMode 0 scans and decides
 // in one workgroup per group.
 constexpr int kSplitSlots = 256;
+// complete_task_go / _tile entries beyond 2 N Hkv: the long-group flag, one
+// spare, the previous step's counts for the short-group rule, one spare
+constexpr int kTaskExtra = 6;
 constexpr int kLsePrefetchSlots = 64;
 constexpr int kProbeSlots = 4;  // probe scan: slot pairs per lane batch and pass
 
@@ -830,7 +868,9 @@ __device__ __forceinline__ void decide_group(const DecideParams& p, const float 
   if (lane == 0 && g == 0) *p.task_counter = 0;
   // a group of few tokens is finished by this kernel (no tasks, no merge)
   const long long tokens = static_cast<long long>(fs_begin) + (new_end - rb) + max(P + 1 - new_end, 0);
-  const int fused = (p.fuse_tokens > 0 && tokens <= p.fuse_tokens) ? 1 : 0;
+  const bool is_short = p.fuse_tokens > 0 && tokens <= p.fuse_tokens;
+  int fused = is_short ? 1 : 0;
+  if (is_short && p.fuse_sync != nullptr && lane == 0) fused = step_fuse_rule(p);
   if (head_lane) {
     s_rect[h] = rect_start;
     s_mslot[h] = hit ? mslot : -1;
@@ -1447,9 +1487,14 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
 
   if (blockIdx.x == 0) {
     // descriptors for merge_write and the reference's task counters
-    int nonhit = 0, ff = 0, red = 0, max_ff = 0, max_mixed = 0, tails = 0;
+    int nonhit = 0, ff = 0, red = 0, max_ff = 0, max_mixed = 0, tails = 0, shorts = 0, longs = 0;
+    uint32_t units = 0;  // tokens / 64 of all groups, for the next step's short-group rule
     for (int g = tid; g < NG; g += kBlock) {
       GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, g, p.F, chunk, p.cap);
+      const int t = group_tokens(sp.sink_end, sp.band_begin, sp.new_end, sp.kv_len);
+      if (t <= p.fuse_tokens) ++shorts;
+      else ++longs;
+      units += static_cast<uint32_t>((t + 63) >> 6);
       p.group_chunk[g] = sp.chunk;
       p.group_ntasks[g] = p.group_fused[g] != 0 ? 0 : sp.n_sink + sp.n_band + sp.n_tail;
       p.group_rect_tiles[g] = sp.n_band;
@@ -1474,10 +1519,13 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
       ff += __shfl_xor(ff, off);
       red += __shfl_xor(red, off);
       tails += __shfl_xor(tails, off);
+      shorts += __shfl_xor(shorts, off);
+      longs += __shfl_xor(longs, off);
+      units += __shfl_xor(units, off);
       max_ff = max(max_ff, __shfl_xor(max_ff, off));
       max_mixed = max(max_mixed, __shfl_xor(max_mixed, off));
     }
-    __shared__ int s_cnt[kWaves][6];
+    __shared__ int s_cnt[kWaves][9];
     if (lane == 0) {
       s_cnt[wave][0] = nonhit;
       s_cnt[wave][1] = ff;
@@ -1485,14 +1533,22 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
       s_cnt[wave][3] = tails;
       s_cnt[wave][4] = max_ff;
       s_cnt[wave][5] = max_mixed;
+      s_cnt[wave][6] = shorts;
+      s_cnt[wave][7] = longs;
+      s_cnt[wave][8] = static_cast<int>(units);
     }
     __syncthreads();
     if (tid == 0) {
       int a[6] = {0, 0, 0, 0, 0, 0};
+      uint32_t f[3] = {0, 0, 0};
       for (int w = 0; w < kWaves; ++w) {
         for (int i = 0; i < 4; ++i) a[i] += s_cnt[w][i];
         a[4] = max(a[4], s_cnt[w][4]);
         a[5] = max(a[5], s_cnt[w][5]);
+        for (int i = 0; i < 3; ++i) f[i] += static_cast<uint32_t>(s_cnt[w][6 + i]);
+      }
+      if (p.fuse_sync != nullptr) {
+        for (int i = 0; i < 3; ++i) p.fuse_sync[i] = f[i];
       }
       p.task_counts[0] = total_tasks;
       p.task_counts[1] = a[3];
@@ -2142,6 +2198,13 @@ int attn_residency(int dev, int G, int impl, size_t dyn_lds, int* cus, int* per_
   return MAC_OK;
 }
 
+// MAC_AMD_FUSE_POLICY (read per call): "auto" (default) applies
+// step_fuse_rule; "always" finishes every short group in match_decide.
+bool fuse_policy_always() {
+  const char* e = std::getenv("MAC_AMD_FUSE_POLICY");
+  return e != nullptr && std::strcmp(e, "always") == 0;
+}
+
 template <int G>
 int launch_all(const DecideParams& dp, const AttnParams& ap, const MergeParams& mp, int attn_grid,
                int impl, hipStream_t stream, hipEvent_t* ev) {
@@ -2229,7 +2292,8 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
               "unsupported synthetic MAC bench mode");
   MAC_REQUIRE(static_cast<int64_t>(N) * Hkv <= INT_MAX / 2, "N * Hkv = %lld groups is too many",
               static_cast<long long>(N) * Hkv);
-  MAC_REQUIRE(a->complete_task_len >= 2 * static_cast<int64_t>(N) * Hkv + 2, "complete task workspace too small");
+  MAC_REQUIRE(a->complete_task_len >= 2 * static_cast<int64_t>(N) * Hkv + kTaskExtra,
+              "complete task workspace too small");
   MAC_REQUIRE(a->debug_enabled < 2 || a->phase_cycles == nullptr || a->phase_cycles_len >= 6,
               "phase_cycles must have at least 6 elements");
   MAC_REQUIRE(a->req_to_token_rows > 0 && a->req_to_token_stride >= 0, "req_to_token must be 2-D");
@@ -2325,6 +2389,11 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   dp.fuse_tokens = fuse_tokens();
   dp.group_fused = a->complete_task_go + static_cast<int64_t>(N) * Hkv;
   dp.long_groups = a->complete_task_go + 2 * static_cast<int64_t>(N) * Hkv;
+  dp.fuse_sync = (dp.fuse_tokens > 0 && !fuse_policy_always())
+                     ? reinterpret_cast<uint32_t*>(a->complete_task_go + 2 * static_cast<int64_t>(N) * Hkv + 2)
+                     : nullptr;
+  dp.fuse_cus = cus;
+  dp.narrow_min_tokens = impl ? narrow_min_tokens() : LLONG_MAX;
   dp.q_post = static_cast<const uint16_t*>(a->q_post);
   dp.k_buffer = static_cast<const uint16_t*>(a->k_buffer);
   dp.v_buffer = static_cast<const uint16_t*>(a->v_buffer);
@@ -2375,6 +2444,8 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   ap.narrow_grid = impl ? cus : INT_MAX;  // the VALU kernel is instruction-bound: every resident workgroup
   ap.narrow_min_tokens = narrow_min_tokens();
   ap.group_fused = dp.group_fused;
+  ap.fuse_sync = const_cast<uint32_t*>(dp.fuse_sync);
+  ap.fuse_tokens = dp.fuse_tokens;
   ap.plan_bucket = plan_bucket;
   ap.long_groups = dp.long_groups;
   ap.phase_cycles = stamps;
@@ -2454,7 +2525,7 @@ struct ScratchLayout {  // byte offsets into the scratch array
   static constexpr size_t H = kNoAllocMaxHeads;
   static constexpr size_t kMatch = up256(H * kNoAllocMatchTiles * 4);  // one match array
   static constexpr size_t kHead = up256(H * 4);                        // one head_* / group_* array
-  static constexpr size_t kTask = up256((2 * H + 2) * 4);              // complete_task_go / _tile
+  static constexpr size_t kTask = up256((2 * H + kTaskExtra) * 4);     // complete_task_go / _tile
   static constexpr size_t match_dist = 0;
   static constexpr size_t match_pos = match_dist + kMatch;
   static constexpr size_t match_slot = match_pos + kMatch;
@@ -2535,7 +2606,7 @@ extern "C" int mac_persistent_decode_bf16_noalloc(const MacDecodeArgs* a, void* 
   w.match_tile_slots = 256;
   w.max_tiles_context = kNoAllocPartialSlots;
   w.tile_tokens = (a->max_context + kNoAllocPartialSlots - 1) / kNoAllocPartialSlots;
-  w.complete_task_len = 2 * static_cast<int64_t>(a->N) * (a->Hkv > 0 ? a->Hkv : 1) + 2;
+  w.complete_task_len = 2 * static_cast<int64_t>(a->N) * (a->Hkv > 0 ? a->Hkv : 1) + kTaskExtra;
   w.workspace_rows = a->N;
   return mac::decode_impl(&w, stream_ptr, nullptr);
 }

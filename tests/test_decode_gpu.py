@@ -53,18 +53,21 @@ def _check_against_oracle(case, dev, out, out_lse, ws, res, tol=1e-2, what=""):
     assert_close(lc, res.lse_cache, 3e-2, f"{what} lse_cache")
 
 
-# Groups of at most MAC_AMD_FUSE_TOKENS tokens are finished inside
-# match_decide (attention, merge and ring row in one workgroup); "0" sends
-# every group through span_attention and merge_write.  Both must give the
-# oracle's results.
-FUSE = {"fused": None, "split": "0"}
+# Groups of at most MAC_AMD_FUSE_TOKENS tokens may be finished inside
+# match_decide (attention, merge and ring row in one workgroup).  "fused":
+# every such group is (MAC_AMD_FUSE_POLICY=always); "split": none is, every
+# group goes through span_attention and merge_write; "auto": the default
+# step-wide rule decides.  All must give the oracle's results.
+FUSE = {"fused": ("always", None), "split": (None, "0"), "auto": (None, None)}
 
 
 def _set_fuse(monkeypatch, mode):
-    if FUSE[mode] is None:
-        monkeypatch.delenv("MAC_AMD_FUSE_TOKENS", raising=False)
-    else:
-        monkeypatch.setenv("MAC_AMD_FUSE_TOKENS", FUSE[mode])
+    policy, tokens = FUSE[mode]
+    for name, value in (("MAC_AMD_FUSE_POLICY", policy), ("MAC_AMD_FUSE_TOKENS", tokens)):
+        if value is None:
+            monkeypatch.delenv(name, raising=False)
+        else:
+            monkeypatch.setenv(name, value)
 
 
 @pytest.mark.parametrize("fuse", list(FUSE))
@@ -250,3 +253,54 @@ def test_phase_cycles_stamps(ext):
             assert all(s > 0 for s in first), first
             assert all(b >= a for a, b in zip(first, first[1:])), first
             assert stamps[6:] == [-7] * (len(stamps) - 6)
+
+
+def _group_tokens(c):
+    """Tokens of every group (sink + band + tail) from the oracle's spans."""
+    r = oracle_run(c)
+    g = r.group
+    sink = np.minimum(c.front_sink_tokens, g["rect_end"])
+    return (sink + (g["rect_end"] - g["rect_begin"]) + (g["tail_end"] - g["rect_end"])).reshape(-1).tolist()
+
+
+@pytest.mark.parametrize("case", ["all_short", "one_long"])
+def test_step_fuse_rule(case, ext, monkeypatch):
+    """The default rule, which reads the previous step's counts: after a step
+    whose groups were all short (or with no history: zeroed counts) the short
+    groups are finished inside match_decide; after a small step with a long
+    group they are left to span_attention.  Results equal the oracle either
+    way; the step leaves its own counts for the next one and clears the
+    long-group flag."""
+    _set_fuse(monkeypatch, "auto")
+    if case == "all_short":
+        kv_lens, hit = [900, 300, 700, 64], 0.5
+    else:  # request 0: misses over 5000 tokens (long groups); the others short
+        kv_lens, hit = [5000, 300, 400, 200], 0.0
+    c = syn.random_case(batch=4, hq=32, hkv=8, kv_lens=kv_lens, capacity=16, semantic_pos_ahead=32,
+                        front_sink_tokens=4, hit_rate=hit, match_lag=8, seed=77)
+    print(f"fuse rule: {case}", flush=True)
+    res = oracle_run(c)
+    for rep in range(2):  # the second step starts from the first one's cleared counts
+        dev = syn.to_device(torch, c)
+        ws = syn.workspace(torch, batch=4, hq=32, hkv=8, capacity=16, max_context=5008, tile_tokens=32,
+                           match_tile_slots=4, semantic_pos_ahead=32, front_sink_tokens=4, device="cuda")
+        if rep == 0:
+            ws[16].zero_()
+        else:
+            ws[16].copy_(prev)
+        out, out_lse, ws = syn.run_decode(torch, ext, dev, c, max_context=5008, tile_tokens=32, ws=ws)
+        torch.cuda.synchronize()
+        _check_against_oracle(c, dev, out, out_lse, ws, res, what=f"{case} step {rep}")
+        ng = 4 * 8
+        go = _np(ws[16])
+        fused = go[ng:2 * ng]
+        long_groups = 0 if case == "all_short" else 8  # request 0's groups
+        if case == "all_short" or rep == 0:
+            assert fused.tolist() == [0] * long_groups + [1] * (ng - long_groups)
+        else:  # after a step with a long group and far fewer than 8M tokens
+            assert fused.tolist() == [0] * ng
+        assert go[2 * ng] == 0  # long-group flag cleared by merge_write
+        # span_attention's workgroup 0 leaves this step's counts for the next
+        assert go[2 * ng + 2:2 * ng + 4].tolist() == [ng - long_groups, long_groups]
+        assert go[2 * ng + 4] == sum(-(-t // 64) for t in _group_tokens(c))
+        prev = ws[16].clone()
