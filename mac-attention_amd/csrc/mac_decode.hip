@@ -212,11 +212,17 @@ struct MergeParams {
 // 0 leaves in fuse_sync: [0] short groups, [1] long groups, [2] tokens / 64.
 // Decode steps of a batch change slowly, so the previous step's counts are
 // the usual case; the rule only moves work between kernels, and every group
-// gets the same results either way.
+// gets the same results either way, up to rounding (the two paths sum in
+// different orders), so two calls on the same inputs can differ in the last
+// bits when their previous steps differed (MAC_AMD_FUSE_POLICY=always pins
+// the choice).
 __device__ __forceinline__ int step_fuse_rule(const DecideParams& p) {
   const uint32_t* c = p.fuse_sync;
   const uint32_t n_short = c[0], n_long = c[1];
   const long long all_tokens = static_cast<long long>(c[2]) << 6;
+  // counts of a different batch shape (or none yet: a workspace's first
+  // step) are no history: short groups are finished here
+  if (n_short + n_long != static_cast<uint32_t>(p.s.N) * static_cast<uint32_t>(p.s.Hkv)) return 1;
   if (n_long == 0) return 1;
   return (all_tokens >= p.narrow_min_tokens && 2ll * n_short > p.fuse_cus) ? 1 : 0;
 }

@@ -221,13 +221,21 @@ def config3(request):
     torch.cuda.empty_cache()
 
 
+@pytest.fixture
+def pinned_fusion(monkeypatch):
+    """Tests that compare two decode calls bit for bit pin the short-group
+    rule: by default it follows the previous call's counts, and the fused and
+    split paths agree only to rounding."""
+    monkeypatch.setenv("MAC_AMD_FUSE_POLICY", "always")
+
+
 def _restore(dev, pristine):
     for k in RING_ROWS:
         dev[k].copy_(pristine[k])
 
 
 @pytest.mark.parametrize("hit", [0.0, 0.25, 0.5, 0.75, 0.9, 1.0])
-def test_config3_hit_sweep(ext, config3, hit):
+def test_config3_hit_sweep(ext, config3, hit, pinned_fusion):
     """Every hit ratio bench.py times at the headline shape, GQA-4 and GQA-8:
     ring copies planted where the bench's synthetic_head override puts its
     hits, decided by the real ring scan and checked against the oracle on two
@@ -270,7 +278,7 @@ def ring2048(request):
 
 
 @pytest.mark.parametrize("hit", [0.0, 1.0])
-def test_reference_shape_hit_ends(ext, ring2048, hit):
+def test_reference_shape_hit_ends(ext, ring2048, hit, pinned_fusion):
     """The ends of bench.py's reference_shape sweep (ring 2048: the
     range-split, probe-pruned scan): scan decisions against the oracle on two
     requests, and the override's decisions equal to the scan's."""
@@ -368,7 +376,7 @@ def test_config4_ragged_serving_mix(ext, cache_ext):
     _check_subset(dev, out2, out_lse2, ws2, sub2, res2, check2, "config4 step2")
 
 
-def test_config4_graph_replays_follow_host_flips(ext, cache_ext):
+def test_config4_graph_replays_follow_host_flips(ext, cache_ext, pinned_fusion):
     """Config 4's serving mix captured once in a hipGraph and replayed while
     the host changes what the readiness gate sees between replays
     (DECODE:208-230, the in-graph demotion the serving path relies on):
@@ -561,7 +569,7 @@ def test_near_threshold_decisions_are_logged(ext):
 # ------------------------------------------------------------ hipGraph ----
 
 
-def test_graph_replay_matches_eager(ext):
+def test_graph_replay_matches_eager(ext, pinned_fusion):
     """The decode step captured in a graph and replayed (with eager work and
     synchronisation between replays) gives the eager result every time,
     including the ring-row writes and the readiness gate."""
