@@ -118,6 +118,8 @@ def prepare_batch(meta: Any, forward_batch: Any) -> None:
     st = batch_state(forward_batch, meta.req_ids.device)
     meta.req_ids[:b].copy_(st["req_ids"])
     meta.req_ids_host = st["req_ids_host"]
+    if st["req_ids_host"] and not forward_batch.forward_mode.is_decode_or_idle():
+        persistent.clear_low_hit_ejection(meta, st["req_ids_host"])  # a prefill rebuilds their rings
     if st["seq_host"]:
         meta.cur_kv_len = max(st["seq_host"])
     match = getattr(meta, "match_req_len", None)

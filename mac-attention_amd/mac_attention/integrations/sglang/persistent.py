@@ -259,6 +259,73 @@ def _low_hit_ejected(metadata: MacMetadata, reqs: list[int]) -> bool:
     return any(r < 0 or r >= len(ejected) or ejected[r] for r in reqs)
 
 
+def _env_number(name: str, default: float) -> float:
+    raw = os.environ.get(name)
+    if raw is None or not raw.strip():
+        return default
+    try:
+        return float(raw)
+    except ValueError:
+        return default
+
+
+def eject_low_hit_requests(metadata: MacMetadata, workspace: dict, batch_size: int, req_ids: torch.Tensor,
+                           past_lens: torch.Tensor) -> bool:
+    """The low-hit ejection policy of flashinfer_hooks.py:1500-1543, run after
+    a decode step outside graph capture.  With
+    ``MAC_ADAPTIVE_LOW_HIT_EJECT_THRESHOLD`` = t in [0, 1] (unset or negative:
+    off), a step in which at least the fraction t of the (request, KV head)
+    groups did not hit -- and, with ``MAC_ADAPTIVE_LOW_HIT_EJECT_MIN_KV`` = k
+    > 0, whose requests all hold at least k cached tokens -- takes its
+    requests off the MAC path: their readiness is invalidated and they are
+    flagged so that no ring update marks them ready again until their next
+    prefill (clear_low_hit_ejection).  ``MAC_ADAPTIVE_LOW_HIT_EJECT_LOG=1``
+    prints each ejection.  Reads the step's group modes (one host sync).
+    Returns whether the batch was ejected."""
+    if is_graph_capturing():
+        return False
+    threshold = _env_number("MAC_ADAPTIVE_LOW_HIT_EJECT_THRESHOLD", -1.0)
+    if threshold < 0.0 or batch_size <= 0:
+        return False
+    threshold = min(threshold, 1.0)
+    min_kv = max(0, int(_env_number("MAC_ADAPTIVE_LOW_HIT_EJECT_MIN_KV", 0)))
+    if min_kv > 0 and int(past_lens[:batch_size].min().item()) < min_kv:
+        return False
+    modes = workspace["group_mode"][:batch_size]
+    groups = int(modes.numel())
+    if groups == 0:
+        return False
+    missed = int((modes != 0).sum().item())
+    if missed < threshold * groups:
+        return False
+    if os.environ.get("MAC_ADAPTIVE_LOW_HIT_EJECT_LOG", "0").strip() == "1":
+        print(f"[mac_attention] low-hit ejection: {missed}/{groups} groups without a hit "
+              f"(threshold {threshold:.3f})", flush=True)
+    reqs = _host_req_ids(metadata, req_ids[:batch_size])
+    ejected = metadata.mac_low_hit_ejected_host
+    rows = len(metadata.mac_cache_ready_host) if metadata.mac_cache_ready_host is not None else 0
+    if ejected is None:
+        ejected = metadata.mac_low_hit_ejected_host = [False] * rows
+    elif len(ejected) < rows:
+        ejected.extend([False] * (rows - len(ejected)))
+    for r in reqs:
+        if 0 <= r < len(ejected):
+            ejected[r] = True
+    invalidate_persistent_ready(metadata, req_ids[:batch_size])
+    return True
+
+
+def clear_low_hit_ejection(metadata: MacMetadata, reqs: list[int]) -> None:
+    """A new prefill of these requests rebuilds their rings: they may use the
+    MAC path again (llama_hooks.py:905-918)."""
+    ejected = metadata.mac_low_hit_ejected_host
+    if ejected is None:
+        return
+    for r in reqs:
+        if 0 <= r < len(ejected):
+            ejected[r] = False
+
+
 def mark_persistent_ready(metadata: MacMetadata, req_ids: torch.Tensor) -> None:
     """flashinfer_hooks.py:1704-1738: the rings of ``req_ids`` now hold
     current rows (cache_epoch <- request_epoch, ready <- 1)."""
@@ -468,6 +535,7 @@ def try_persistent_decode(backend: Any, forward_batch: Any, config: Any, metadat
         metadata.mac_cache_ready if metadata.mac_cache_ready is not None else _empty(),
         metadata.mac_cache_epoch if metadata.mac_cache_epoch is not None else _empty(),
         metadata.request_epoch if metadata.request_epoch is not None else _empty())
+    eject_low_hit_requests(metadata, ws, batch, req_ids, past_lens)
     backend.mac_last_persistent_workspace = ws
     return out
 

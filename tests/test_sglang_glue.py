@@ -362,3 +362,40 @@ def test_mode_ids():
     assert persistent.candidate_mode_id("exclude_recent_right") == 1
     assert persistent.candidate_mode_id("last_M") == 0
     assert [persistent.bench_mode_id(x) for x in ("off", "synthetic-head", "synthetic_group")] == [0, 1, 2]
+
+
+def _ejection_meta(rows=6):
+    meta = persistent.MacMetadata(8, 2, 128)
+    meta.mac_cache_ready_host = [True] * rows  # host mirror only: no device vectors
+    meta.req_ids_host = None
+    return meta
+
+
+def test_low_hit_ejection_policy(monkeypatch):
+    """flashinfer_hooks.py:1500-1543: off unless the threshold is set; a step
+    with at least the threshold's share of non-hit groups takes its requests
+    off the MAC path (not ready, and not marked ready again) until their next
+    prefill; the minimum-context switch keeps short requests in."""
+    reqs = torch.tensor([1, 4], dtype=torch.int32)
+    past = torch.tensor([500, 900], dtype=torch.int32)
+    ws = {"group_mode": torch.tensor([[0, 1], [2, 1]], dtype=torch.int32)}  # 3 of 4 groups without a hit
+    meta = _ejection_meta()
+    monkeypatch.delenv("MAC_ADAPTIVE_LOW_HIT_EJECT_THRESHOLD", raising=False)
+    assert not persistent.eject_low_hit_requests(meta, ws, 2, reqs, past)  # off by default
+    monkeypatch.setenv("MAC_ADAPTIVE_LOW_HIT_EJECT_THRESHOLD", "0.8")
+    assert not persistent.eject_low_hit_requests(meta, ws, 2, reqs, past)  # 0.75 < 0.8
+    monkeypatch.setenv("MAC_ADAPTIVE_LOW_HIT_EJECT_THRESHOLD", "0.75")
+    monkeypatch.setenv("MAC_ADAPTIVE_LOW_HIT_EJECT_MIN_KV", "600")
+    assert not persistent.eject_low_hit_requests(meta, ws, 2, reqs, past)  # request 1 holds 500 < 600
+    monkeypatch.delenv("MAC_ADAPTIVE_LOW_HIT_EJECT_MIN_KV")
+    assert persistent.eject_low_hit_requests(meta, ws, 2, reqs, past)
+    assert meta.mac_low_hit_ejected_host == [False, True, False, False, True, False]
+    assert meta.mac_cache_ready_host == [True, False, True, True, False, True]
+    persistent.mark_persistent_ready(meta, reqs)  # a later ring update does not bring them back
+    assert meta.mac_cache_ready_host[1] is False and meta.mac_cache_ready_host[4] is False
+    meta.req_ids_host = [1, 4]
+    assert not persistent.persistent_ready(meta, reqs)
+    meta.req_ids_host = None
+    persistent.clear_low_hit_ejection(meta, [4])  # request 4 is prefilled again
+    persistent.mark_persistent_ready(meta, torch.tensor([4], dtype=torch.int32))
+    assert meta.mac_cache_ready_host[4] is True and meta.mac_cache_ready_host[1] is False
