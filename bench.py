@@ -302,7 +302,7 @@ def stream_read_peak(torch):
 
     from mac_attention.integrations.sglang import bridge
 
-    lib = bridge.load_library()
+    lib = bridge.load_bench_library()
     nbytes = 8 << 30
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     src = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").fill_(1)
@@ -314,7 +314,7 @@ def stream_read_peak(torch):
             rc = lib.mac_bench_stream_read(ctypes.c_void_p(src.data_ptr()), ctypes.c_int64(nbytes),
                                            ctypes.c_void_p(sink.data_ptr()), ctypes.c_int32(grid), stream)
             if rc != 0:
-                raise RuntimeError(lib.mac_last_error().decode())
+                raise RuntimeError(lib.mac_bench_last_error().decode())
 
         us = _time_us(torch, run, 10)
         if best is None or us < best[0]:

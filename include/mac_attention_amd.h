@@ -365,15 +365,6 @@ MAC_API int mac_decode_rope_preserve_q_bf16(void* q, int64_t q_stride0, void* k,
  * phase_cycles instead, DECODE:4751-4929). */
 MAC_API int mac_persistent_decode_bf16_timed(const MacDecodeArgs* args, void* stream, float* ms);
 
-/* Measurement helper, no reference counterpart: reads the first
- * floor(bytes / 16) 16-byte words of `src` (16-byte aligned) once with the
- * non-temporal policy the decode kernels stream K/V with, on a grid of
- * min(sink_len, 8 x CUs) workgroups, and stores one XOR word per workgroup
- * into sink[0 .. grid).  Timing it gives the rate a plain streaming read
- * reaches on the device, beside the HBM nameplate. */
-MAC_API int mac_bench_stream_read(const void* src, int64_t bytes, uint32_t* sink, int32_t sink_len,
-                                  void* stream);
-
 /* Message of the last failed call on this thread ("" if none).  No reference
  * counterpart: the reference raises through TORCH_CHECK instead. */
 MAC_API const char* mac_last_error(void);

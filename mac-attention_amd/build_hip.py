@@ -1,4 +1,5 @@
-"""Builds libmac_hip.so for gfx950 with hipcc (no CMake, no JIT)."""
+"""Builds libmac_hip.so (the decode library) and libmac_bench.so (a
+streaming-read measurement helper) for gfx950 with hipcc (no CMake, no JIT)."""
 
 from __future__ import annotations
 
@@ -8,8 +9,10 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
-SOURCES = [os.path.join(HERE, "csrc", f) for f in ("mac_decode.hip", "mac_cache_ops.hip", "mac_prefill.hip", "mac_rope.hip", "mac_bench.hip")]
+SOURCES = [os.path.join(HERE, "csrc", f) for f in ("mac_decode.hip", "mac_cache_ops.hip", "mac_prefill.hip", "mac_rope.hip")]
 OUTPUT = os.path.join(HERE, "libmac_hip.so")
+BENCH_SOURCES = [os.path.join(HERE, "csrc", "mac_bench.hip")]
+BENCH_OUTPUT = os.path.join(HERE, "libmac_bench.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [
@@ -30,8 +33,8 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False) -> str:
-    cmd = [HIPCC, *FLAGS, *SOURCES, "-o", OUTPUT]
+def _hipcc(sources: list[str], output: str, verbose: bool) -> str:
+    cmd = [HIPCC, *FLAGS, *sources, "-o", output]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -41,7 +44,13 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
-    return OUTPUT
+    return output
+
+
+def build(verbose: bool = False) -> str:
+    """Both libraries; returns the decode library's path."""
+    _hipcc(BENCH_SOURCES, BENCH_OUTPUT, verbose)
+    return _hipcc(SOURCES, OUTPUT, verbose)
 
 
 if __name__ == "__main__":

@@ -1,19 +1,28 @@
-// mac_bench.hip -- a measurement helper for MI355X (gfx950): the rate a plain
-// streaming read of HBM reaches on this GPU, as context for the decode
-// kernels' fractions of the 8 TB/s nameplate.  Not part of the decode path.
+// mac_bench.hip -- libmac_bench.so, a measurement helper for MI355X (gfx950):
+// the rate a plain streaming read of HBM reaches on this GPU, as context for
+// the decode kernels' fractions of the 8 TB/s nameplate.  Not part of the
+// decode path, so built as a library of its own.
 
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdarg>
 #include <cstdint>
+#include <cstdio>
 
-#include "mac_attention_amd.h"
-
-namespace mac {
-int fail(int code, const char* fmt, ...);
-}  // namespace mac
+#include "mac_bench.h"
 
 namespace {
+
+thread_local char g_bench_err[256] = "";
+
+int bench_fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_bench_err, sizeof(g_bench_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -53,7 +62,7 @@ extern "C" int mac_bench_stream_read(const void* src, int64_t bytes, uint32_t* s
                                      void* stream) {
   if (src == nullptr || sink == nullptr || bytes < 16 || sink_len <= 0 ||
       (reinterpret_cast<uintptr_t>(src) & 15) != 0)
-    return mac::fail(MAC_ERR_INVALID_ARGUMENT, "mac_bench_stream_read: invalid arguments");
+    return bench_fail(1, "mac_bench_stream_read: invalid arguments");
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess) {
     int v = 0;
@@ -63,6 +72,9 @@ extern "C" int mac_bench_stream_read(const void* src, int64_t bytes, uint32_t* s
   hipLaunchKernelGGL(stream_read_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<const u32x4_t*>(src), bytes / 16, sink);
   const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return mac::fail(MAC_ERR_HIP, "stream_read_kernel: %s", hipGetErrorString(e));
-  return MAC_OK;
+  if (e != hipSuccess) return bench_fail(2, "stream_read_kernel: %s", hipGetErrorString(e));
+  g_bench_err[0] = '\0';
+  return 0;
 }
+
+extern "C" const char* mac_bench_last_error(void) { return g_bench_err; }

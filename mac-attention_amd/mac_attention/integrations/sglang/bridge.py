@@ -83,7 +83,6 @@ EXPORTED_SYMBOLS = (
     "mac_prefill_window_attention_bf16",
     "mac_prefill_rectify_update_cache_bf16",
     "mac_decode_rope_preserve_q_bf16",
-    "mac_bench_stream_read",
     "mac_last_error",
     "mac_abi_version",
 )
@@ -157,12 +156,28 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i32, _p, _i32, _p, _i32,
         _i64, _i32, _i32, _i32, _i32, _p]
     lib.mac_decode_rope_preserve_q_bf16.restype = ctypes.c_int
-    lib.mac_bench_stream_read.argtypes = [_p, _i64, _p, _i32, _p]
-    lib.mac_bench_stream_read.restype = ctypes.c_int
     if lib.mac_abi_version() != ABI_VERSION:
         raise RuntimeError(
             f"{path} has ABI version {lib.mac_abi_version()}, binding expects {ABI_VERSION}"
         )
+    return lib
+
+
+BENCH_LIB_PATH = os.environ.get("MAC_BENCH_LIBRARY", os.path.join(_PKG_ROOT, "libmac_bench.so"))
+BENCH_EXPORTED_SYMBOLS = ("mac_bench_stream_read", "mac_bench_last_error")
+
+
+@lru_cache(maxsize=1)
+def load_bench_library(path: str | None = None) -> ctypes.CDLL:
+    """Open libmac_bench.so, the streaming-read measurement helper (not part
+    of the decode library)."""
+    path = path or BENCH_LIB_PATH
+    if not os.path.exists(path):
+        raise RuntimeError(f"measurement helper not found at {path}; build with __graft_entry__.build()")
+    lib = ctypes.CDLL(path)
+    lib.mac_bench_stream_read.argtypes = [_p, _i64, _p, _i32, _p]
+    lib.mac_bench_stream_read.restype = ctypes.c_int
+    lib.mac_bench_last_error.restype = ctypes.c_char_p
     return lib
 
 

@@ -12,11 +12,12 @@ import pytest
 from helpers import REPO
 
 HEADER = os.path.join(REPO, "include", "mac_attention_amd.h")
+BENCH_HEADER = os.path.join(REPO, "include", "mac_bench.h")
 
 
-def _declared():
-    text = open(HEADER).read()
-    return re.findall(r"MAC_API\s+[\w\s\*]+?\b(mac_\w+)\s*\(", text)
+def _declared(header=HEADER, api="MAC_API"):
+    text = open(header).read()
+    return re.findall(api + r"\s+[\w\s\*]+?\b(mac_\w+)\s*\(", text)
 
 
 @pytest.fixture(scope="module")
@@ -40,6 +41,20 @@ def test_library_exports_every_declared_symbol(bridge):
     exported = {l.split()[-1] for l in nm.splitlines() if " T " in l}
     assert exported == set(names)
     assert lib.mac_abi_version() == bridge.ABI_VERSION
+
+
+def test_measurement_library_is_separate(bridge):
+    """The streaming-read helper lives in libmac_bench.so, not in the decode
+    library, and exports exactly what include/mac_bench.h declares."""
+    names = _declared(BENCH_HEADER, "MAC_BENCH_API")
+    assert set(names) == set(bridge.BENCH_EXPORTED_SYMBOLS)
+    lib = bridge.load_bench_library()
+    for n in names:
+        assert hasattr(lib, n), n
+    nm = subprocess.run(["nm", "-D", "--defined-only", bridge.BENCH_LIB_PATH], capture_output=True,
+                        text=True, check=True).stdout
+    assert {l.split()[-1] for l in nm.splitlines() if " T " in l} == set(names)
+    assert not set(names) & set(bridge.EXPORTED_SYMBOLS)
 
 
 @pytest.mark.parametrize("struct", ["MacDecodeArgs", "MacWindowAttentionArgs", "MacRectifyArgs"])

@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 def _lib():
     from mac_attention.integrations.sglang import bridge
 
-    return bridge.load_library()
+    return bridge.load_bench_library()
 
 
 @pytest.mark.parametrize("nbytes,sink_len", [(16, 1), (64 << 20, 37), ((8 << 20) + 48, 300), ((256 << 20) + 16, 2048)])
@@ -30,7 +30,7 @@ def test_stream_read_reads_every_word(nbytes, sink_len):
     print(f"stream_read {nbytes} bytes, sink {sink_len}", flush=True)
     rc = lib.mac_bench_stream_read(ctypes.c_void_p(src.data_ptr()), ctypes.c_int64(nbytes),
                                    ctypes.c_void_p(sink.data_ptr()), ctypes.c_int32(sink_len), stream)
-    assert rc == 0, lib.mac_last_error()
+    assert rc == 0, lib.mac_bench_last_error()
     torch.cuda.synchronize()
     got = np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32))  # entries past the grid stay 0
     assert int(got) == int(np.bitwise_xor.reduce(words[: (nbytes // 16) * 4]))
