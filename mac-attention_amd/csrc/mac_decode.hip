@@ -1379,9 +1379,10 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* s_tmp, int& tota
 // Task granularity.  Workgroups fetch tasks dynamically, so about a dozen
 // tasks per workgroup bounds the end-of-kernel imbalance to a few percent,
 // while a task of at least kMinChunk tokens amortises its fixed cost (plan
-// lookup, Q staging, pipeline fill, partial write).
+// lookup, Q staging, pipeline fill, partial write) and keeps a long group's
+// partials few enough for merge_write to fetch in one or two rounds.
 constexpr int kTasksPerWorkgroup = 12;  // default of AttnParams::tasks_per_wg
-constexpr int kMinChunk = 2048;
+constexpr int kMinChunk = 3072;
 constexpr int kMaxChunk = 16384;
 constexpr int kFuseTokens = 1024;  // default of DecideParams::fuse_tokens
 
