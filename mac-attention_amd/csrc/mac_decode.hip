@@ -1969,24 +1969,28 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
   const bool stamp = p.phase_cycles != nullptr && g == 0 && h == 0 && tid == 0;
   if (stamp) p.phase_cycles[4] = static_cast<int64_t>(wall_clock64());
   if (g == 0 && h == 0 && tid == 0) *p.long_groups = 0;  // read by span_attention, set again by match_decide
-  if (p.group_fused[g] != 0) {  // finished by match_decide
-    if (stamp) p.phase_cycles[5] = static_cast<int64_t>(wall_clock64());
-    return;
-  }
+  // the group's descriptors are loaded with its finished flag (one round of
+  // loads, not two; a finished group does not use them)
   const int M = p.s.M;
   const int Hq = p.s.Hq;
   const int hq = hkv * G + h;
   const int64_t ho = static_cast<int64_t>(n) * Hq + hq;
+  const int fused = p.group_fused[g];
   const int P = p.past_lens[n];
   const int req = p.req_ids[n];
-  const bool ready = request_ready(p.cache_ready, p.cache_epoch, p.request_epoch, req, p.s.R);
-  const int dest = P % M;
-
   const int band_begin = p.group_rect_begin[g];
   const int new_end = p.group_rect_end[g];
   const int kv_len = p.group_tail_end[g];
-  const int sink_end = min(p.F, new_end);
   const int chunk = p.group_chunk[g];
+  const int hit = p.head_hit[ho];
+  const int mslot = p.head_match_slot[ho];
+  if (fused != 0) {  // finished by match_decide
+    if (stamp) p.phase_cycles[5] = static_cast<int64_t>(wall_clock64());
+    return;
+  }
+  const bool ready = request_ready(p.cache_ready, p.cache_epoch, p.request_epoch, req, p.s.R);
+  const int dest = P % M;
+  const int sink_end = min(p.F, new_end);
   const int n_sink = ceil_div(sink_end, chunk);
   const int n_band = ceil_div(new_end - band_begin, chunk);
   const int n_tail = ceil_div(kv_len - new_end, chunk);
@@ -2018,8 +2022,7 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
   // issued without waiting for them.  A non-finite lse is skipped.
   float entry_lse = -INFINITY;
   uint32_t entry_o = 0;
-  const int mslot = p.head_match_slot[ho];
-  if (wave == 0 && p.head_hit[ho] != 0 && mslot >= 0 && req >= 0 && req < p.s.R) {
+  if (wave == 0 && hit != 0 && mslot >= 0 && req >= 0 && req < p.s.R) {
     const int64_t rowi = (static_cast<int64_t>(req) * M + mslot) * Hq + hq;
     entry_lse = p.lse_cache[rowi];
     entry_o = *reinterpret_cast<const uint32_t*>(p.attn_cache + rowi * kHeadDim + d0);
