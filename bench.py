@@ -476,6 +476,18 @@ def measure_aux(torch):
 
     fused_us = _time_us(torch, fused, 20)
     comp_us = _time_us(torch, composed, 5)
+    # the window attention of every row on its own (the dominant call of the
+    # three): row i of a chunk attends keys max(0, i - S + 1) .. i.  Per launch
+    # it reads q (bf16) and every K/V row once and writes out (bf16) and lse
+    # (f32): 9.7 GB here against 2.2 TFLOP, so HBM, not MFMA, bounds it
+    # (4 D flop per (row, head, key) over 2 B per element is below the
+    # ridge of 2.5 PFLOP/s / 8 TB/s).
+    win_us = _time_us(torch, lambda: rect.window_attention_return_lse(q, k, v, qo, qo, idx, S - 1, scale, out=wo,
+                                                                      out_lse=wl), 5)
+    keys_per_chunk = sum(min(i + 1, S) for i in range(chunk))
+    win_flop = 4 * D * hq * B * keys_per_chunk
+    win_bytes = rows * hq * (2 * D * 2 + 4) + rows * hkv * 2 * D * 2 + rows * 4
+    hbm_s, mfma_s = win_bytes / 8e12, win_flop / 2.5e15
     # mac_prefill_update_cache alone (the last M rows of every chunk into the
     # ring): q and attention rows (2 * Hq * D bf16) + lse read and written per row
     upd_us = _time_us(torch, lambda: cache.mac_prefill_update_cache(qc, ac, lc, rl[:B], req, src_q, wo, wl, qo, lens,
@@ -495,7 +507,14 @@ def measure_aux(torch):
         "prefill_update_cache": {
             "workload": f"B={B} batch rows x {chunk} source rows, ring={M}, Hq={hq}",
             "us": round(upd_us, 2), "algorithmic_bytes": upd_bytes,
-            "gbs": round(upd_bytes / upd_us / 1e3, 1)}}
+            "gbs": round(upd_bytes / upd_us / 1e3, 1)},
+        "window_attention": {
+            "workload": f"every row of B={B} x {chunk}-token chunks, GQA-8 (Hq={hq}, Hkv={hkv}), window {S}",
+            "us": round(win_us, 1), "flop": win_flop, "algorithmic_bytes": win_bytes,
+            "bound": "hbm" if hbm_s >= mfma_s else "mfma",
+            "tflops": round(win_flop / win_us / 1e6, 1), "frac_bf16_peak": round(win_flop / win_us / 2.5e9, 4),
+            "gbs": round(win_bytes / win_us / 1e3, 1), "frac_hbm_peak": round(win_bytes / win_us / 8e6, 4),
+            "frac_roofline": round(max(hbm_s, mfma_s) / (win_us * 1e-6), 4)}}
     del k, v, q, src_q, o_full, wo
     torch.cuda.empty_cache()
 
