@@ -421,7 +421,7 @@ __device__ __forceinline__ void block_span(const BlockList& bl, int v, int& base
 // end in `st`.  pre0/pre1 (when not NULL): the req_to_token entries of the
 // wave's first two blocks, loaded by the caller; used for blocks outside
 // range 2.
-template <int G, bool kTwoClass>
+template <int G, bool kTwoClass, int W = kWaves>
 __device__ __forceinline__ void stream_blocks(const KvStream& ks, const BlockList& bl, int head_begin,
                                               float q_scale, const bf16x8_t (&qb)[4], uint4* s_kw,
                                               uint4* s_vw, WaveState& st, WaveState& ring,
@@ -450,9 +450,9 @@ __device__ __forceinline__ void stream_blocks(const KvStream& ks, const BlockLis
   {
     int b0, e0, b1, e1;
     block_span(bl, wave, b0, e0);
-    block_span(bl, wave + kWaves, b1, e1);
+    block_span(bl, wave + W, b1, e1);
     const bool use0 = pre0 != nullptr && (!kTwoClass || wave < bl.first2);
-    const bool use1 = pre1 != nullptr && (!kTwoClass || wave + kWaves < bl.first2);
+    const bool use1 = pre1 != nullptr && (!kTwoClass || wave + W < bl.first2);
 #pragma unroll
     for (int i = 0; i < 8; ++i) ph[i] = phys_ok(b0 + 8 * quad + i, e0, use0 ? pre0[i] : raw_row(b0 + 8 * quad + i));
 #pragma unroll
@@ -463,9 +463,9 @@ __device__ __forceinline__ void stream_blocks(const KvStream& ks, const BlockLis
   }
 
   bool switched = false;
-  const int my_blocks = wave < bl.nblk ? ceil_div(bl.nblk - wave, kWaves) : 0;
+  const int my_blocks = wave < bl.nblk ? ceil_div(bl.nblk - wave, W) : 0;
   for (int k = 0; k < my_blocks; ++k) {
-    const int v = wave + kWaves * k;
+    const int v = wave + W * k;
     if (kTwoClass && !switched && v >= bl.first2) {  // sink and tail done: st -> ring for the band
       ring = st;
       state_reset(st);
@@ -473,8 +473,8 @@ __device__ __forceinline__ void stream_blocks(const KvStream& ks, const BlockLis
     }
     int base, end_unused, b1, e1, b2, e2;
     block_span(bl, v, base, end_unused);
-    block_span(bl, v + kWaves, b1, e1);
-    block_span(bl, v + 2 * kWaves, b2, e2);
+    block_span(bl, v + W, b1, e1);
+    block_span(bl, v + 2 * W, b2, e2);
     const int hb = (kTwoClass ? v >= bl.first2 : v < bl.first1) ? head_begin : 0;
     int nph[8];
 #pragma unroll
@@ -631,15 +631,15 @@ __device__ __forceinline__ void state_to_lds(const WaveState& st, float* so, flo
 
 // Normalised (o[d], o[d+1], natural-log lse) of head h from the four wave
 // states in LDS; lse = -inf and o = 0 for an empty state.
-template <int G>
+template <int G, int W = kWaves>
 __device__ __forceinline__ void combine_waves(const float* so, const float* sml, int h, int d, float& o0,
                                               float& o1, float& lse) {
   float mm = kNegBig;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, sml[(w * G + h) * 2]);
+  for (int w = 0; w < W; ++w) mm = fmaxf(mm, sml[(w * G + h) * 2]);
   float ll = 0.0f, a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
+  for (int w = 0; w < W; ++w) {
     const float sc = fast_exp2(sml[(w * G + h) * 2] - mm);
     ll += sml[(w * G + h) * 2 + 1] * sc;
     a0 += so[(w * G + h) * kOPitch + d] * sc;
@@ -705,7 +705,7 @@ constexpr int kProbeSlots = 4;  // probe scan: slot pairs per lane batch and pas
 // per head its band start, the slot of a reusable cached entry (-1: none)
 // and that entry's lse; the group's band begin, new_end and whether
 // match_decide finishes the group itself.
-template <int G, int kMode>
+template <int G, int kMode, int W = kWaves>
 __device__ __forceinline__ void decide_group(const DecideParams& p, const float (*s_d)[kMaxGroup],
                                              const int (*s_p)[kMaxGroup], const int (*s_s)[kMaxGroup],
                                              const float (*s_lse)[kLsePrefetchSlots], bool lse_in_lds, int g,
@@ -720,7 +720,7 @@ __device__ __forceinline__ void decide_group(const DecideParams& p, const float 
   float bd = INFINITY;
   int bp = INT_MAX, bs = -1;
   if (head_lane) {
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < W; ++w) {
       if (better_pair(s_d[w][h], s_p[w][h], bd, bp)) {
         bd = s_d[w][h];
         bp = s_p[w][h];
@@ -922,16 +922,16 @@ __device__ __forceinline__ BlockList rest_blocks(int P, int new_end, int F) {
 // cached entry (+) band -> ring row at past_len % M (ready requests only);
 // out = ring state (+) sink (+) tail -- with no partials, no task and no
 // merge launch for the group.
-template <int G>
+template <int G, int W = kWaves>
 __device__ __forceinline__ void fused_group(const DecideParams& p, int n, int hkv, int P, int req, bool ready,
                                             int band_begin, int new_end, const int* s_rect,
                                             const int* s_mslot, const float* s_entry, uint4 qpost_w,
                                             const KvStream& ks, const int (&pre)[2][8]) {
-  constexpr int kPairs = (G * 64 + kBlock - 1) / kBlock;  // dim pairs per thread in the epilogue
-  __shared__ uint4 s_kv[2][kWaves][kTileU4];  // K and V tiles; the combine area afterwards
+  constexpr int kPairs = (G * 64 + (W * 64) - 1) / (W * 64);  // dim pairs per thread in the epilogue
+  __shared__ uint4 s_kv[2][W][kTileU4];  // K and V tiles; the combine area afterwards
   __shared__ uint4 s_q[16 * 16];
-  __shared__ float s_ml[2][kWaves][G][2];
-  static_assert(sizeof(float) * 2 * kWaves * G * kOPitch <= sizeof(s_kv), "combine area");
+  __shared__ float s_ml[2][W][G][2];
+  static_assert(sizeof(float) * 2 * W * G * kOPitch <= sizeof(s_kv), "combine area");
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = tid & 15;
@@ -939,13 +939,13 @@ __device__ __forceinline__ void fused_group(const DecideParams& p, int n, int hk
   const int M = p.s.M;
   const bool req_ok = req >= 0 && req < p.s.R;
 
-  s_q[tid] = qpost_w;
+  if (tid < 16 * 16) s_q[tid] = qpost_w;
   // the cached entries (hit heads) and the pre-RoPE query rows of the
   // epilogue, in flight during the stream
   uint32_t ent[kPairs], qpre[kPairs];
 #pragma unroll
   for (int i = 0; i < kPairs; ++i) {
-    const int e = tid + i * kBlock;
+    const int e = tid + i * (W * 64);
     ent[i] = 0;
     qpre[i] = 0;
     if (e < G * 64) {
@@ -969,24 +969,24 @@ __device__ __forceinline__ void fused_group(const DecideParams& p, int n, int hk
   WaveState rest, ring;
   state_reset(rest);
   state_reset(ring);
-  stream_blocks<G, true>(ks, bl, col < G ? s_rect[col] : 0, p.q_scale, qb, &s_kv[0][wave][0],
+  stream_blocks<G, true, W>(ks, bl, col < G ? s_rect[col] : 0, p.q_scale, qb, &s_kv[0][wave][0],
                          &s_kv[1][wave][0], rest, ring, pre[0], pre[1]);
   __syncthreads();  // every wave is done with its tiles
   float* so = reinterpret_cast<float*>(&s_kv[0][0][0]);
   state_to_lds<G>(ring, so, &s_ml[0][0][0][0]);
-  state_to_lds<G>(rest, so + kWaves * G * kOPitch, &s_ml[1][0][0][0]);
+  state_to_lds<G>(rest, so + W * G * kOPitch, &s_ml[1][0][0][0]);
   __syncthreads();
 
   const int dest = P % M;
 #pragma unroll
   for (int i = 0; i < kPairs; ++i) {
-    const int e = tid + i * kBlock;
+    const int e = tid + i * (W * 64);
     if (e >= G * 64) break;
     const int h = e >> 6, d0 = 2 * (e & 63), hq = hkv * G + h;
     const int64_t ho = static_cast<int64_t>(n) * Hq + hq;
     MergeState st{-INFINITY, {0.0f, 0.0f}};
     float o0, o1, l;
-    combine_waves<G>(so, &s_ml[0][0][0][0], h, d0, o0, o1, l);
+    combine_waves<G, W>(so, &s_ml[0][0][0][0], h, d0, o0, o1, l);
     merge_into(st, l, o0, o1);
     merge_into(st, s_entry[h], bf16_lo(ent[i]), bf16_hi(ent[i]));
     if (ready && P >= 0) {  // ring row (a negative past_len has no ring slot)
@@ -996,7 +996,7 @@ __device__ __forceinline__ void fused_group(const DecideParams& p, int n, int hk
       *reinterpret_cast<uint32_t*>(p.attn_cache + rowi * kHeadDim + d0) = valid ? pack_bf16x2(st.o[0], st.o[1]) : 0u;
       if (d0 == 0) p.ring_lse[rowi] = valid ? st.lse : -INFINITY;
     }
-    combine_waves<G>(so + kWaves * G * kOPitch, &s_ml[1][0][0][0], h, d0, o0, o1, l);
+    combine_waves<G, W>(so + W * G * kOPitch, &s_ml[1][0][0][0], h, d0, o0, o1, l);
     merge_into(st, l, o0, o1);
     const bool valid = isfinite(st.lse);
     *reinterpret_cast<uint32_t*>(p.out + ho * kHeadDim + d0) = valid ? pack_bf16x2(st.o[0], st.o[1]) : 0u;
@@ -1004,10 +1004,12 @@ __device__ __forceinline__ void fused_group(const DecideParams& p, int n, int hk
   }
 }
 
-template <int G, int kMode>
-__global__ void __launch_bounds__(kBlock, 2) match_decide_kernel(DecideParams p) {
+template <int G, int kMode, int W = kWaves>
+__global__ void __launch_bounds__(W * 64, W == kWaves ? 2 : 1) match_decide_kernel(DecideParams p) {
   constexpr int kPasses = (G + 3) / 4;
-  constexpr int kSlotBatch = 16 / kPasses;  // 16 row loads in flight per lane
+  // 16 row loads in flight per lane with four waves (eight with eight, which
+  // cover as many slots per batch)
+  constexpr int kSlotBatch = 16 / kPasses * kWaves / W;
   const int g = blockIdx.x;
   const int n = g / p.s.Hkv;
   const int hkv = g - n * p.s.Hkv;
@@ -1028,9 +1030,9 @@ __global__ void __launch_bounds__(kBlock, 2) match_decide_kernel(DecideParams p)
   if (p.candidate_mode == 1) cand_end = max(cand_begin, P - p.lookback_right);
   const bool cand_ok = P >= p.gen_min_limit && cand_end > cand_begin;
 
-  __shared__ float s_d[kWaves][kMaxGroup];
-  __shared__ int s_p[kWaves][kMaxGroup];
-  __shared__ int s_s[kWaves][kMaxGroup];
+  __shared__ float s_d[W][kMaxGroup];
+  __shared__ int s_p[W][kMaxGroup];
+  __shared__ int s_s[W][kMaxGroup];
   __shared__ float s_lse[kMaxGroup][kLsePrefetchSlots];  // lse of every slot (small rings)
 
   // Every load of the scan is independent of the readiness gate and of the
@@ -1080,7 +1082,7 @@ __global__ void __launch_bounds__(kBlock, 2) match_decide_kernel(DecideParams p)
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       int base, end;
-      block_span(rblk, wave + kWaves * u, base, end);
+      block_span(rblk, wave + W * u, base, end);
 #pragma unroll
       for (int i = 0; i < 8; ++i) pre[u][i] = ks.raw_row(base + 8 * row + i);
     }
@@ -1121,12 +1123,12 @@ __global__ void __launch_bounds__(kBlock, 2) match_decide_kernel(DecideParams p)
       qbw[ps] = *reinterpret_cast<const uint4*>(qp + 64);
     }
     const float thr_prune = p.thr_dist + fabsf(p.thr_dist) * 1e-4f + 1e-4f;
-    for (int s0 = s_lo + wave; s0 < s_hi; s0 += kWaves * 2 * kProbeBatch) {
+    for (int s0 = s_lo + wave; s0 < s_hi; s0 += W * 2 * kProbeBatch) {
       int pos[kProbeBatch], slot[kProbeBatch];
       bool in_window[kProbeBatch];
 #pragma unroll
       for (int u = 0; u < kProbeBatch; ++u) {
-        slot[u] = s0 + (2 * u + half) * kWaves;
+        slot[u] = s0 + (2 * u + half) * W;
         pos[u] = ring_slot_to_pos(P, M, slot[u]);
         in_window[u] = cand_ok && slot[u] < s_hi && pos[u] >= cand_begin && pos[u] < cand_end;
       }
@@ -1223,7 +1225,7 @@ __global__ void __launch_bounds__(kBlock, 2) match_decide_kernel(DecideParams p)
       bool in_window[kSlotBatch];
 #pragma unroll
       for (int u = 0; u < kSlotBatch; ++u) {
-        const int slot = s0 + u * kWaves;
+        const int slot = s0 + u * W;
         pos[u] = ring_slot_to_pos(P, M, slot);
         in_window[u] = cand_ok && slot < s_hi && pos[u] >= cand_begin && pos[u] < cand_end;
       }
@@ -1232,7 +1234,7 @@ __global__ void __launch_bounds__(kBlock, 2) match_decide_kernel(DecideParams p)
         const int hl = min(row + 4 * ps, G - 1);
 #pragma unroll
         for (int u = 0; u < kSlotBatch; ++u) {
-          const int slot = min(s0 + u * kWaves, s_hi - 1);  // past the range: re-reads its last row
+          const int slot = min(s0 + u * W, s_hi - 1);  // past the range: re-reads its last row
           const int64_t off = ((cache_req + slot) * Hq + hkv * G + hl) * kHeadDim + c * 8;
           w[ps][u] = load_stream16(p.query_cache + off);  // ring rows are read once per step
         }
@@ -1261,7 +1263,7 @@ __global__ void __launch_bounds__(kBlock, 2) match_decide_kernel(DecideParams p)
           if (in_window[u] && hl < G && better_pair(acc, pos[u], best_d[ps], best_p[ps])) {
             best_d[ps] = acc;
             best_p[ps] = pos[u];
-            best_s[ps] = s0 + u * kWaves;
+            best_s[ps] = s0 + u * W;
           }
         }
       }
@@ -1269,10 +1271,10 @@ __global__ void __launch_bounds__(kBlock, 2) match_decide_kernel(DecideParams p)
     // A ring that one batch per wave covers (32 slots with G = 8, 64 with
     // G <= 4) is scanned without a loop: the queries' unpacking then cannot
     // be hoisted in front of the ring loads, where its wait would hold them.
-    if (s_hi - s_lo <= kWaves * kSlotBatch) {
+    if (s_hi - s_lo <= W * kSlotBatch) {
       scan_batch(s_lo + wave);
     } else {
-      for (int s0 = s_lo + wave; s0 < s_hi; s0 += kWaves * kSlotBatch) scan_batch(s0);
+      for (int s0 = s_lo + wave; s0 < s_hi; s0 += W * kSlotBatch) scan_batch(s0);
     }
   }
 #pragma unroll
@@ -1296,7 +1298,7 @@ __global__ void __launch_bounds__(kBlock, 2) match_decide_kernel(DecideParams p)
   __shared__ int s_rect[kMaxGroup], s_mslot[kMaxGroup];
   __shared__ float s_entry[kMaxGroup];
   __shared__ int s_span[3];  // band begin, new_end, fused
-  if (wave == 0) decide_group<G, kMode>(p, s_d, s_p, s_s, s_lse, lse_in_lds, g, n, hkv, P, req, eligible,
+  if (wave == 0) decide_group<G, kMode, W>(p, s_d, s_p, s_s, s_lse, lse_in_lds, g, n, hkv, P, req, eligible,
                                         s_rect, s_mslot, s_entry, s_span);
   if constexpr (kMode != 1) {
     __syncthreads();
@@ -1309,7 +1311,7 @@ __global__ void __launch_bounds__(kBlock, 2) match_decide_kernel(DecideParams p)
                            : static_cast<int64_t>(cur_lo);
     ks.cur_row = (cl >= 0 && cl < p.s.pool_tokens) ? static_cast<int>(cl) : -1;
     if ((tid >> 4) >= G) qpost_w = make_uint4(0, 0, 0, 0);
-    fused_group<G>(p, n, hkv, P, req, ready, s_span[0], s_span[1], s_rect, s_mslot, s_entry, qpost_w, ks, pre);
+    fused_group<G, W>(p, n, hkv, P, req, ready, s_span[0], s_span[1], s_rect, s_mslot, s_entry, qpost_w, ks, pre);
   }
 }
 
@@ -2208,6 +2210,16 @@ int attn_residency(int dev, int G, int impl, size_t dyn_lds, int* cus, int* per_
   return MAC_OK;
 }
 
+// Waves per match_decide workgroup when a step has at most one group per CU
+// (MAC_AMD_MATCH_WAVES, read once: 8, the default, or 4).
+int match_waves() {
+  static const int v = [] {
+    const char* e = std::getenv("MAC_AMD_MATCH_WAVES");
+    return (e != nullptr && std::atoi(e) == 4) ? 4 : 8;
+  }();
+  return v;
+}
+
 // MAC_AMD_FUSE_POLICY (read per call): "auto" (default) applies
 // step_fuse_rule; "always" finishes every short group in match_decide.
 bool fuse_policy_always() {
@@ -2226,6 +2238,10 @@ int launch_all(const DecideParams& dp, const AttnParams& ap, const MergeParams& 
     DecideParams dp2 = dp;
     dp2.stamp_first = 0;  // the range scan recorded the step's start
     hipLaunchKernelGGL((match_decide_kernel<G, 2>), dim3(NG), dim3(kBlock), 0, stream, dp2);
+  } else if (NG <= dp.fuse_cus && match_waves() == 8) {
+    // at most one group per CU: eight waves per group stream a finished
+    // group's blocks in half the rounds
+    hipLaunchKernelGGL((match_decide_kernel<G, 0, 8>), dim3(NG), dim3(8 * 64), 0, stream, dp);
   } else {
     hipLaunchKernelGGL((match_decide_kernel<G, 0>), dim3(NG), dim3(kBlock), 0, stream, dp);
   }
