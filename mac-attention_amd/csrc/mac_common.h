@@ -69,14 +69,15 @@ __device__ __forceinline__ bf16x4_t lds_read_tr16(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_t*)(p));
 }
 
-// Maximum of finite or infinite floats (no NaN operands) with the plain
-// v_max3_f32: fmaxf makes the compiler quiet every operand first (an extra
-// v_max per operand) because it cannot rule out signalling NaNs in MFMA
-// results.
+// Maximum of finite or infinite floats (no NaN operands): one
+// v_maximum3_f32 (IEEE maximum, which needs no quieting of its operands,
+// unlike fmaxf's, for which the compiler adds a v_max per operand that may
+// come from an MFMA).  Not inline assembly: the compiler does not model an
+// inline-assembly instruction's wait for a matrix-core result it reads (the
+// window kernel's row maxima read the score MFMA's registers directly), so
+// such an instruction could read them before the MFMA had written them.
 __device__ __forceinline__ float max3_nonan(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
 __device__ __forceinline__ float max8_nonan(const float (&x)[8]) {
   return max3_nonan(max3_nonan(x[0], x[1], x[2]), max3_nonan(x[3], x[4], x[5]), max3_nonan(x[6], x[7], x[7]));
