@@ -170,6 +170,34 @@ def test_random_vs_oracle(cfg, fuse, ext, monkeypatch):
     _check_against_oracle(c, dev, out, out_lse, ws, res, what=str(cfg))
 
 
+@pytest.mark.parametrize("fuse", ["fused", "split"])
+@pytest.mark.parametrize("hkv", [8, 4])
+def test_decode_is_deterministic(hkv, fuse, ext, monkeypatch):
+    """A step on the same inputs gives the same bits on every call when the
+    short-group choice does not depend on history (fused: every short group
+    in match_decide; split: none): task order and timing never reach the
+    arithmetic.  Mixed hits, misses and long groups, 64 groups or fewer per
+    step (the eight-wave match_decide) and more (four waves)."""
+    _set_fuse(monkeypatch, fuse)
+    batch = 8 if hkv == 8 else 80
+    rng = np.random.default_rng(31)
+    kv_lens = rng.integers(300, 6000, batch).tolist()
+    print(f"decode determinism: Hkv={hkv} B={batch} fuse={fuse}", flush=True)
+    c = syn.random_case(batch=batch, hq=32, hkv=hkv, kv_lens=kv_lens, capacity=32, semantic_pos_ahead=64,
+                        front_sink_tokens=8, hit_rate=0.7, match_lag=16, seed=31)
+    runs = []
+    for _ in range(3):
+        dev = syn.to_device(torch, c)
+        out, out_lse, ws = syn.run_decode(torch, ext, dev, c, max_context=max(kv_lens) + 8, tile_tokens=16,
+                                          match_tile_slots=8)
+        torch.cuda.synchronize()
+        runs.append([out.view(torch.int16).clone(), out_lse.view(torch.int32).clone(),
+                     dev["attn_cache"].view(torch.int16).clone(), dev["lse_cache"].view(torch.int32).clone()])
+    for r in runs[1:]:
+        for a, b in zip(r, runs[0]):
+            assert torch.equal(a, b)
+
+
 def test_readiness_gate(ext):
     """Not-ready and epoch-mismatched requests run exact attention and leave
     their ring rows untouched (DECODE:208-230, :4487-4497)."""

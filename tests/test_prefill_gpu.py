@@ -351,6 +351,41 @@ def test_rectify_config4_chunk(rect_ext):
             assert np.isfinite(g["l"].cpu().numpy()).all()
 
 
+@pytest.mark.parametrize("hkv", [8, 4])
+def test_rectify_is_deterministic(rect_ext, hkv):
+    """The fused op gives the same ring rows and lengths on every call, for
+    both kernel instances (G = 4 and 8), with the front sink (F = 128, sink
+    mode 1) as its own key segment."""
+    B, chunk, hq, S, M, F, D = 4, 2048, 32, 256, 32, 128, 128
+    rows = B * chunk
+    print(f"rectify determinism: G={hq // hkv}", flush=True)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(9)
+    bf = torch.bfloat16
+    k = torch.randn(rows, hkv, D, device="cuda", dtype=bf, generator=g)
+    v = torch.randn_like(k)
+    q = torch.randn(rows, hq, D, device="cuda", dtype=bf, generator=g)
+    src_q = torch.randn(rows, hq, D, device="cuda", dtype=bf, generator=g)
+    o_full = torch.randn(rows, hq, D, device="cuda", dtype=bf, generator=g)
+    lse_full = torch.randn(rows, hq, device="cuda", generator=g) + 8.0
+    qo = torch.arange(0, rows + 1, chunk, device="cuda", dtype=torch.int32)
+    idx = torch.randperm(rows, device="cuda", generator=g).to(torch.int32)
+    req = torch.tensor([2, 0, 3, 1], device="cuda", dtype=torch.int32)
+    runs = []
+    for _ in range(3):
+        qc = torch.zeros(B, M, hq, D, device="cuda", dtype=bf)
+        ac = torch.zeros_like(qc)
+        lc = torch.zeros(B, M, hq, device="cuda")
+        rl = torch.tensor([0, 5, 31, 100], device="cuda", dtype=torch.int32)
+        rect_ext.mac_prefill_rectify_update_cache(q, src_q, o_full, lse_full, k, v, qo, qo, idx, qc, ac, lc, rl,
+                                                  req, S, F, 1.0 / math.sqrt(D), sink_mode=1)
+        torch.cuda.synchronize()
+        runs.append([qc.view(torch.int16), ac.view(torch.int16), lc.view(torch.int32), rl])
+    for r in runs[1:]:
+        for a, b in zip(r, runs[0]):
+            assert torch.equal(a, b)
+
+
 def test_window_attention_skips_requests_outside_the_buffers(rect_ext):
     """A request whose query range runs past total_q (or key range past
     kv_indices) is skipped: its rows stay untouched, the others are exact."""
