@@ -151,6 +151,10 @@ RANDOM_CASES = [
     (2, 32, 8, [3000, 3001], 32, 256, 128, 0.0, 17),
     (2, 10, 2, [900, 1500], 16, 64, 8, 0.6, 19),   # G = 5
     (2, 14, 2, [700, 2100], 32, 128, 0, 0.7, 20),  # G = 7
+    # rings of several scan batches per wave (the scan's loop; one group per
+    # CU or fewer, so the eight-wave decision kernel)
+    (2, 32, 4, [3000, 700], 256, 64, 8, 0.7, 21),   # G = 8, M = 256
+    (2, 16, 4, [900, 2500], 128, 32, 0, 0.6, 22),   # G = 4, M = 128
 ]
 
 
