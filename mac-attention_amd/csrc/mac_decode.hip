@@ -2211,13 +2211,11 @@ int attn_residency(int dev, int G, int impl, size_t dyn_lds, int* cus, int* per_
 }
 
 // Waves per match_decide workgroup when a step has at most one group per CU
-// (MAC_AMD_MATCH_WAVES, read once: 8, the default, or 4).
+// (MAC_AMD_MATCH_WAVES, read per call: 8, the default, or 4; the two give the
+// same results up to the order the waves' states are combined).
 int match_waves() {
-  static const int v = [] {
-    const char* e = std::getenv("MAC_AMD_MATCH_WAVES");
-    return (e != nullptr && std::atoi(e) == 4) ? 4 : 8;
-  }();
-  return v;
+  const char* e = std::getenv("MAC_AMD_MATCH_WAVES");
+  return (e != nullptr && std::atoi(e) == 4) ? 4 : 8;
 }
 
 // MAC_AMD_FUSE_POLICY (read per call): "auto" (default) applies

@@ -79,6 +79,12 @@ def test_reference_kat(builder, partial, fuse, ext, monkeypatch):
         monkeypatch.setenv(k, v)
     _set_fuse(monkeypatch, fuse)
     print(f"case={kat.name} partial={partial} fuse={fuse}", flush=True)
+    _run_kat(kat, partial, ext)
+
+
+def _run_kat(kat, partial, ext):
+    """One known-answer case on the GPU: the decisions it pins, its expected
+    outputs and ring rows, and the oracle on every output."""
     c = kat.case
     res = oracle_run(c)
     dev = syn.to_device(torch, c)
@@ -200,6 +206,34 @@ def test_decode_is_deterministic(hkv, fuse, ext, monkeypatch):
     for r in runs[1:]:
         for a, b in zip(r, runs[0]):
             assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("case", [f.__name__ for f in kat_cases.ALL + golden_cases.LOADERS]
+                         + [f"random_seed{c[-1]}" for c in RANDOM_CASES])
+def test_four_wave_decision_kernel(case, ext, monkeypatch):
+    """Steps of at most one group per CU run the eight-wave match_decide by
+    default; the four-wave form (the one larger steps run) is checked on the
+    same known-answer and random cases with MAC_AMD_MATCH_WAVES=4, every
+    short group finished inside it (its largest share of the work)."""
+    monkeypatch.setenv("MAC_AMD_MATCH_WAVES", "4")
+    _set_fuse(monkeypatch, "fused")
+    print(f"four-wave decision kernel: {case}", flush=True)
+    if case.startswith("random_seed"):
+        cfg = next(c for c in RANDOM_CASES if f"random_seed{c[-1]}" == case)
+        b, hq, hkv, kv_lens, m, s, f, hit_rate, seed = cfg
+        c = syn.random_case(batch=b, hq=hq, hkv=hkv, kv_lens=kv_lens, capacity=m, semantic_pos_ahead=s,
+                            front_sink_tokens=f, hit_rate=hit_rate, match_lag=m // 2, seed=seed)
+        dev = syn.to_device(torch, c)
+        out, out_lse, ws = syn.run_decode(torch, ext, dev, c, max_context=max(kv_lens) + 8, tile_tokens=16,
+                                          match_tile_slots=8)
+        torch.cuda.synchronize()
+        _check_against_oracle(c, dev, out, out_lse, ws, oracle_run(c), what=case)
+        return
+    builder = next(f for f in kat_cases.ALL + golden_cases.LOADERS if f.__name__ == case)
+    kat = builder()
+    for k, v in kat.env.items():
+        monkeypatch.setenv(k, v)
+    _run_kat(kat, "f32", ext)
 
 
 def test_readiness_gate(ext):
