@@ -30,10 +30,12 @@ extern "C" {
 
 #define MAC_ABI_VERSION 2
 
+#ifndef MAC_API
 #if defined(__GNUC__)
 #define MAC_API __attribute__((visibility("default")))
 #else
 #define MAC_API
+#endif
 #endif
 
 enum {
@@ -173,19 +175,9 @@ typedef struct MacDecodeArgs {
  * ([5]), group_mode ([15]) and task_counts ([22]). */
 MAC_API int mac_persistent_decode_bf16(const MacDecodeArgs* args, void* stream);
 
-/* No counterpart in the reference: for callers that cannot allocate device
- * memory or hand over workspaces (code under graph capture, tight serving
- * loops, harnesses that forbid allocation).  Same step and effects on the
- * caller's tensors as mac_persistent_decode_bf16 (out / out_lse, the ring row
- * at past_len % M, phase_cycles), with every workspace in one static device
- * array of the library (about 65 MiB per GPU, held until the process ends):
- * the workspace pointers and their sizes in `args` (match_*, head_*, group_*,
- * complete_task_*, task_counts, partial_*) are ignored and the decisions are
- * not returned.  Limits: N * Hq <= 4096 query heads, M <= 2048 ring slots;
- * larger steps are rejected with MAC_ERR_INVALID_ARGUMENT.  Calls allocate
- * nothing.  All calls on one GPU share its array: calls that overlap on one
- * GPU (different streams) race. */
-MAC_API int mac_persistent_decode_bf16_noalloc(const MacDecodeArgs* args, void* stream);
+/* The same step for callers that cannot allocate (no reference counterpart)
+ * is mac_persistent_decode_bf16_noalloc in libmac_noalloc.so, declared in
+ * mac_noalloc.h. */
 
 /* Replaces mac_prefill_update_cache (PREFILL:324-372, pybind PREFILL:500-502).
  * q_cache/attn_cache bf16 [R, M, H, D]; lse_cache f32 [R, M, H];
@@ -356,14 +348,6 @@ MAC_API int mac_decode_rope_preserve_q_bf16(void* q, int64_t q_stride0, void* k,
                                             int32_t positions_is_i64, const void* cache_locs,
                                             int32_t cache_locs_is_i64, int64_t N, int32_t Hq, int32_t Hkv,
                                             int32_t head_dim, int32_t is_neox, void* stream);
-
-/* Profiling variant of mac_persistent_decode_bf16: same arguments and effects,
- * plus HIP events on `stream` around each of the three kernels; synchronises
- * on the last event and stores the elapsed milliseconds of match_decide,
- * span_attention and merge_write in ms[0..2].  Not graph-capturable.  No
- * reference counterpart (the reference stamps clock64() phases into
- * phase_cycles instead, DECODE:4751-4929). */
-MAC_API int mac_persistent_decode_bf16_timed(const MacDecodeArgs* args, void* stream, float* ms);
 
 /* Message of the last failed call on this thread ("" if none).  No reference
  * counterpart: the reference raises through TORCH_CHECK instead. */

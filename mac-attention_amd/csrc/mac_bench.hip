@@ -1,7 +1,9 @@
-// mac_bench.hip -- libmac_bench.so, a measurement helper for MI355X (gfx950):
+// mac_bench.hip -- libmac_bench.so, measurement helpers for MI355X (gfx950):
 // the rate a plain streaming read of HBM reaches on this GPU, as context for
-// the decode kernels' fractions of the 8 TB/s nameplate.  Not part of the
-// decode path, so built as a library of its own.
+// the decode kernels' fractions of the 8 TB/s nameplate, and the decode step
+// timed kernel by kernel with HIP events (mac_decode.hip is compiled into
+// this library as well, with its C ABI hidden).  Not part of the decode path,
+// so built as a library of its own.
 
 #include <hip/hip_runtime.h>
 
@@ -75,6 +77,34 @@ extern "C" int mac_bench_stream_read(const void* src, int64_t bytes, uint32_t* s
   if (e != hipSuccess) return bench_fail(2, "stream_read_kernel: %s", hipGetErrorString(e));
   g_bench_err[0] = '\0';
   return 0;
+}
+
+namespace mac {
+int decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev);  // mac_decode.hip
+}
+extern "C" const char* mac_last_error(void);  // mac_decode.hip (not exported from this library)
+
+extern "C" int mac_bench_decode_timed(const MacDecodeArgs* a, void* stream, float* ms) {
+  if (ms == nullptr) return bench_fail(MAC_ERR_INVALID_ARGUMENT, "ms must not be NULL");
+  hipEvent_t ev[4];
+  for (int i = 0; i < 4; ++i) {
+    const hipError_t e = hipEventCreate(&ev[i]);
+    if (e != hipSuccess) {
+      for (int j = 0; j < i; ++j) (void)hipEventDestroy(ev[j]);
+      return bench_fail(MAC_ERR_HIP, "hipEventCreate: %s", hipGetErrorString(e));
+    }
+  }
+  int rc = mac::decode_impl(a, stream, ev);
+  if (rc != MAC_OK) {
+    bench_fail(rc, "%s", mac_last_error());
+  } else {
+    hipError_t e = hipEventSynchronize(ev[3]);
+    for (int i = 0; i < 3 && e == hipSuccess; ++i) e = hipEventElapsedTime(&ms[i], ev[i], ev[i + 1]);
+    if (e != hipSuccess) rc = bench_fail(MAC_ERR_HIP, "event timing: %s", hipGetErrorString(e));
+  }
+  for (int i = 0; i < 4; ++i) (void)hipEventDestroy(ev[i]);
+  if (rc == MAC_OK) g_bench_err[0] = '\0';
+  return rc;
 }
 
 extern "C" const char* mac_bench_last_error(void) { return g_bench_err; }

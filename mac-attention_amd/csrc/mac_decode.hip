@@ -59,6 +59,12 @@
 #include "mac_attention_amd.h"
 #include "mac_common.h"
 
+// No multiply-add contraction in this file: every product and sum rounds on
+// its own, so the same expression gives the same bits in every kernel it is
+// inlined into (a short group computed by match_decide and by span_attention
+// must agree bit for bit).
+#pragma clang fp contract(off)
+
 namespace mac {
 
 struct Shape {
@@ -163,9 +169,22 @@ struct AttnParams {
   const int32_t* group_fused;  // groups match_decide finished (no tasks here)
   const int32_t* long_groups;  // 0: match_decide finished every group
   uint32_t* fuse_sync;         // workgroup 0 leaves the step's counts for the next step's short-group rule
-  int fuse_tokens;             // (NULL: no rule) a group of at most fuse_tokens tokens is short
+  int fuse_tokens;             // a group of at most fuse_tokens tokens is short (0: none)
   int plan_bucket;             // groups per entry of the plan's LDS offset table
   int64_t* phase_cycles;
+  // short groups match_decide left here (one task each, short_group)
+  const uint16_t* q_pre;
+  uint16_t* ring_q;
+  uint16_t* attn_cache;
+  float* lse_cache;
+  uint16_t* out;
+  float* out_lse;
+  const uint8_t* cache_ready;
+  const int64_t* cache_epoch;
+  const int64_t* request_epoch;
+  const int32_t* head_hit;
+  const int32_t* head_match_slot;
+  int R;
 };
 
 struct MergeParams {
@@ -196,6 +215,7 @@ struct MergeParams {
   const int32_t* group_fused;
   int32_t* long_groups;  // cleared here for the next step
   int64_t* phase_cycles;
+  int fuse_tokens;  // short groups (at most this many tokens) have no partials: skipped
 };
 
 // Whether this step's short groups are finished here.  Finishing a short
@@ -260,6 +280,15 @@ __device__ __forceinline__ float clampf(float v, float lo, float hi) { return fm
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
+// threadIdx.x behind an empty asm statement: the addresses derived from it
+// inside a task body are then computed per task instead of being hoisted out
+// of span_attention's task loop and held in registers across every task.
+__device__ __forceinline__ int task_tid() {
+  int t = static_cast<int>(threadIdx.x);
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 // 16-byte non-temporal (streaming) global load.
 __device__ __forceinline__ uint4 load_stream16(const uint16_t* ptr) {
   return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(ptr)));
@@ -313,6 +342,7 @@ __device__ __forceinline__ int k_swz(int t) { return 4 * ((t >> 3) & 3) + (t & 3
 __device__ __forceinline__ int v_swz(int t) { return 2 * ((t & 3) | ((t >> 1) & 4)); }
 
 constexpr int kMfmaBlk = 32;  // tokens per wave block
+constexpr int kVirtualWaves = 4;  // a stream's blocks are dealt to four virtual waves
 constexpr int kTileU4 = kMfmaBlk * 16;  // uint4 per K or V tile
 
 // Softmax state of one lane: its head's running max m (log2 units) and sum l
@@ -413,25 +443,43 @@ __device__ __forceinline__ void block_span(const BlockList& bl, int v, int& base
   }
 }
 
-// Streams this wave's blocks of `bl` into `st`; qb: this lane's Q operands
-// (k-steps 0..3).  One class (kTwoClass false): range 0 is masked per head
-// from head_begin on (a band piece); ranges 1 and 2 are not.  Two classes:
-// range 2 is the band (masked per head), and its blocks -- the last ones of
-// every wave -- accumulate into `ring`, while ranges 0 and 1 (sink and tail)
-// end in `st`.  pre0/pre1 (when not NULL): the req_to_token entries of the
-// wave's first two blocks, loaded by the caller; used for blocks outside
-// range 2.
-template <int G, bool kTwoClass, int W = kWaves>
+// Streams one virtual wave's blocks of `bl` into `st`; qb: this lane's Q
+// operands (k-steps 0..3).  Blocks are dealt to four virtual waves, vw
+// taking every fourth one, so that the states a computation ends with do not
+// depend on how many hardware waves run it.  One class (kTwoClass false):
+// blocks vw, vw + 4, ... of the list; range 0 is masked per head from
+// head_begin on (a band piece), ranges 1 and 2 are not.  Two classes: blocks
+// [0, first2) (ranges 0 and 1: sink and tail) are the rest class and end in
+// `st`; blocks [first2, nblk) (range 2: the band, masked per head) are the
+// ring class and end in `ring`; each class is dealt to the virtual waves
+// separately (rest block j and band block j both go to virtual wave j % 4),
+// and do_rest / do_ring select the classes this hardware wave streams (a
+// four-wave workgroup streams both, rest first; an eight-wave one gives each
+// class its own four waves).  pre0/pre1 (when not NULL): the req_to_token
+// entries of the wave's first two rest blocks, loaded by the caller.
+template <int G, bool kTwoClass>
 __device__ __forceinline__ void stream_blocks(const KvStream& ks, const BlockList& bl, int head_begin,
                                               float q_scale, const bf16x8_t (&qb)[4], uint4* s_kw,
-                                              uint4* s_vw, WaveState& st, WaveState& ring,
+                                              uint4* s_vw, WaveState& st, WaveState& ring, int vw,
+                                              bool do_rest = true, bool do_ring = true,
                                               const int* pre0 = nullptr, const int* pre1 = nullptr) {
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+  const int lane = task_tid() & 63;
   const int quad = lane >> 4;
   const int col = lane & 15;
   const bool head_ok = col < G;
   const uint16_t* vtile = reinterpret_cast<const uint16_t*>(s_vw);
+  constexpr int kV = kVirtualWaves;
+  auto share = [&](int nb) { return nb > vw ? (nb - vw + kV - 1) / kV : 0; };
+  const int rest_end = kTwoClass ? bl.first2 : bl.nblk;
+  const int n_rest = do_rest ? share(rest_end) : 0;
+  const int n_ring = (kTwoClass && do_ring) ? share(bl.nblk - bl.first2) : 0;
+  const int my_blocks = n_rest + n_ring;
+  // list index of this wave's k-th block (past its last: an empty block)
+  auto vidx = [&](int k) -> int {
+    if (k < n_rest) return vw + kV * k;
+    if (k < my_blocks) return bl.first2 + vw + kV * (k - n_rest);
+    return bl.nblk + kV * (k - my_blocks);
+  };
 
   // raw_row() only issues the req_to_token load; phys_ok() checks it one
   // block later, so waiting for it never drains the K/V loads issued after it.
@@ -449,10 +497,10 @@ __device__ __forceinline__ void stream_blocks(const KvStream& ks, const BlockLis
   };
   {
     int b0, e0, b1, e1;
-    block_span(bl, wave, b0, e0);
-    block_span(bl, wave + W, b1, e1);
-    const bool use0 = pre0 != nullptr && (!kTwoClass || wave < bl.first2);
-    const bool use1 = pre1 != nullptr && (!kTwoClass || wave + W < bl.first2);
+    block_span(bl, vidx(0), b0, e0);
+    block_span(bl, vidx(1), b1, e1);
+    const bool use0 = pre0 != nullptr && n_rest > 0;
+    const bool use1 = pre1 != nullptr && n_rest > 1;
 #pragma unroll
     for (int i = 0; i < 8; ++i) ph[i] = phys_ok(b0 + 8 * quad + i, e0, use0 ? pre0[i] : raw_row(b0 + 8 * quad + i));
 #pragma unroll
@@ -463,18 +511,17 @@ __device__ __forceinline__ void stream_blocks(const KvStream& ks, const BlockLis
   }
 
   bool switched = false;
-  const int my_blocks = wave < bl.nblk ? ceil_div(bl.nblk - wave, W) : 0;
   for (int k = 0; k < my_blocks; ++k) {
-    const int v = wave + W * k;
-    if (kTwoClass && !switched && v >= bl.first2) {  // sink and tail done: st -> ring for the band
+    const int v = vidx(k);
+    if (kTwoClass && !switched && k == n_rest) {  // sink and tail done: st -> ring for the band
       ring = st;
       state_reset(st);
       switched = true;
     }
     int base, end_unused, b1, e1, b2, e2;
     block_span(bl, v, base, end_unused);
-    block_span(bl, v + W, b1, e1);
-    block_span(bl, v + 2 * W, b2, e2);
+    block_span(bl, vidx(k + 1), b1, e1);
+    block_span(bl, vidx(k + 2), b2, e2);
     const int hb = (kTwoClass ? v >= bl.first2 : v < bl.first1) ? head_begin : 0;
     int nph[8];
 #pragma unroll
@@ -602,19 +649,18 @@ __device__ __forceinline__ void stream_blocks(const KvStream& ks, const BlockLis
 // This lane's Q operands of the score MFMAs from the 16 x 128 Q tile in LDS
 // (rows g >= G zero): k-step s reads Q[col][8 (4 s + quad) .. + 8].
 __device__ __forceinline__ void load_q_operands(const uint4* s_q, bf16x8_t (&qb)[4]) {
-  const int lane = threadIdx.x & 63;
+  const int lane = task_tid() & 63;
   const int quad = lane >> 4, col = lane & 15;
 #pragma unroll
   for (int s = 0; s < 4; ++s) qb[s] = as_bf16x8(s_q[col * 16 + 4 * s + quad]);
 }
 
-// Stores this lane's part of a wave state into the LDS combine area:
-// so[wave][head][dim] (row pitch kOPitch floats), sml[wave][head] = (m, l).
+// Stores this lane's part of virtual wave vw's state into the LDS combine
+// area: so[vw][head][dim] (row pitch kOPitch floats), sml[vw][head] = (m, l).
 constexpr int kOPitch = kHeadDim + 4;  // padded: lanes of different heads hit different banks
 template <int G>
-__device__ __forceinline__ void state_to_lds(const WaveState& st, float* so, float* sml) {
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
+__device__ __forceinline__ void state_to_lds(const WaveState& st, float* so, float* sml, int wave) {
+  const int lane = task_tid() & 63;
   const int quad = lane >> 4, col = lane & 15;
   if (col < G) {
     float* row = so + (wave * G + col) * kOPitch;
@@ -701,7 +747,7 @@ constexpr int kLsePrefetchSlots = 64;
 constexpr int kProbeSlots = 4;  // probe scan: slot pairs per lane batch and pass
 
 // Per-head decisions and group spans of group g (wave 0; lanes 0..G-1 own a
-// head each), DECODE:1147-1402.  Publishes in LDS what fused_group needs:
+// head each), DECODE:1147-1402.  Publishes in LDS what short_group needs:
 // per head its band start, the slot of a reusable cached entry (-1: none)
 // and that entry's lse; the group's band begin, new_end and whether
 // match_decide finishes the group itself.
@@ -913,31 +959,50 @@ __device__ __forceinline__ BlockList rest_blocks(int P, int new_end, int F) {
   return bl;
 }
 
-// A group of few tokens (at most fuse_tokens: in practice the hit groups,
-// whose band is at most the ring capacity, and short requests) is finished
-// by the workgroup that decided it: its sink, band and tail are streamed by
-// the four waves (band blocks first, so each wave's band state is complete
-// when it reaches its first sink or tail block), the wave states are combined
-// in LDS, and the merge of DECODE:4280-4685 follows in place -- ring state =
-// cached entry (+) band -> ring row at past_len % M (ready requests only);
-// out = ring state (+) sink (+) tail -- with no partials, no task and no
-// merge launch for the group.
-template <int G, int W = kWaves>
-__device__ __forceinline__ void fused_group(const DecideParams& p, int n, int hkv, int P, int req, bool ready,
-                                            int band_begin, int new_end, const int* s_rect,
-                                            const int* s_mslot, const float* s_entry, uint4 qpost_w,
-                                            const KvStream& ks, const int (&pre)[2][8]) {
+// What a short group's computation reads and writes besides its K/V stream.
+struct ShortCtx {
+  const uint16_t* q_pre;
+  uint16_t* ring_q;      // query_cache
+  uint16_t* attn_cache;  // cached entries in, ring rows out
+  float* ring_lse;       // lse_cache
+  uint16_t* out;
+  float* out_lse;
+  int Hq, M, R, F;
+  float q_scale;
+};
+
+// The short-group computation (a group of at most fuse_tokens tokens: in
+// practice the hit groups, whose band is at most the ring capacity, and short
+// requests): its sink, tail and band are streamed by four virtual waves
+// (stream_blocks' two-class deal), the virtual waves' states are combined in
+// LDS, and the merge of DECODE:4280-4685 follows in place -- ring state =
+// band (+) cached entry -> ring row at past_len % M (ready requests only);
+// out = ring state (+) sink and tail -- with no partials and no merge
+// launch.  match_decide runs it for the groups it finishes (four or eight
+// hardware waves), span_attention as one task (four): the states, the
+// combine order and the merges are the same in every case, so a group's
+// results are bit for bit the same wherever it runs.
+//   s_rect / s_mslot / s_entry: per head its band start, the slot of a
+//   reusable cached entry (-1: none) and that entry's lse (LDS);
+//   s_kv: 2 x W K/V tiles (the combine area afterwards); s_q: 16 x 16 uint4;
+//   s_ml: [2][4][G][2] floats; pre: req_to_token entries of the wave's first
+//   two rest blocks (or NULL).
+template <int G, int W, bool kSeq>
+__device__ __forceinline__ void short_group(const ShortCtx& c, int n, int hkv, int P, int req, bool ready,
+                                            int band_begin, int new_end, const int* s_rect, const int* s_mslot,
+                                            const float* s_entry, uint4 qpost_w, const KvStream& ks,
+                                            const int (*pre)[8], uint4* s_kv, uint4* s_q, float* s_ml) {
+  static_assert(W == kVirtualWaves || W == 2 * kVirtualWaves, "four or eight waves");
+  static_assert(!kSeq || W == kVirtualWaves, "the sequential form runs on four waves");
+  constexpr int kV = kVirtualWaves;
   constexpr int kPairs = (G * 64 + (W * 64) - 1) / (W * 64);  // dim pairs per thread in the epilogue
-  __shared__ uint4 s_kv[2][W][kTileU4];  // K and V tiles; the combine area afterwards
-  __shared__ uint4 s_q[16 * 16];
-  __shared__ float s_ml[2][W][G][2];
-  static_assert(sizeof(float) * 2 * W * G * kOPitch <= sizeof(s_kv), "combine area");
-  const int tid = threadIdx.x;
+  const int tid = task_tid();
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int vw = wave & (kV - 1);
   const int col = tid & 15;
-  const int Hq = p.s.Hq;
-  const int M = p.s.M;
-  const bool req_ok = req >= 0 && req < p.s.R;
+  const int Hq = c.Hq;
+  const int M = c.M;
+  const bool req_ok = req >= 0 && req < c.R;
 
   if (tid < 16 * 16) s_q[tid] = qpost_w;
   // the cached entries (hit heads) and the pre-RoPE query rows of the
@@ -952,9 +1017,9 @@ __device__ __forceinline__ void fused_group(const DecideParams& p, int n, int hk
       const int h = e >> 6, d0 = 2 * (e & 63), hq = hkv * G + h;
       const int ms = s_mslot[h];
       if (ms >= 0 && req_ok)
-        ent[i] = *reinterpret_cast<const uint32_t*>(p.attn_cache +
+        ent[i] = *reinterpret_cast<const uint32_t*>(c.attn_cache +
                                                     ((static_cast<int64_t>(req) * M + ms) * Hq + hq) * kHeadDim + d0);
-      qpre[i] = *reinterpret_cast<const uint32_t*>(p.q_pre + (static_cast<int64_t>(n) * Hq + hq) * kHeadDim + d0);
+      qpre[i] = *reinterpret_cast<const uint32_t*>(c.q_pre + (static_cast<int64_t>(n) * Hq + hq) * kHeadDim + d0);
     }
   }
   __syncthreads();
@@ -962,20 +1027,73 @@ __device__ __forceinline__ void fused_group(const DecideParams& p, int n, int hk
   load_q_operands(s_q, qb);
 
   // blocks: sink [0, min(F, new_end)), tail [new_end, P + 1), band [band_begin, new_end)
-  BlockList bl = rest_blocks(P, new_end, p.F);
+  BlockList bl = rest_blocks(P, new_end, c.F);
   bl.begin2 = band_begin;
   bl.end2 = new_end;
   bl.nblk = bl.first2 + ceil_div(max(new_end - band_begin, 0), kMfmaBlk);
-  WaveState rest, ring;
-  state_reset(rest);
-  state_reset(ring);
-  stream_blocks<G, true, W>(ks, bl, col < G ? s_rect[col] : 0, p.q_scale, qb, &s_kv[0][wave][0],
-                         &s_kv[1][wave][0], rest, ring, pre[0], pre[1]);
-  __syncthreads();  // every wave is done with its tiles
-  float* so = reinterpret_cast<float*>(&s_kv[0][0][0]);
-  state_to_lds<G>(ring, so, &s_ml[0][0][0][0]);
-  state_to_lds<G>(rest, so + W * G * kOPitch, &s_ml[1][0][0][0]);
-  __syncthreads();
+  float* so = reinterpret_cast<float*>(s_kv);
+  float* so_rest = so + kV * G * kOPitch;
+  float* sml_rest = s_ml + kV * G * 2;
+  const int head_begin = col < G ? s_rect[col] : 0;
+  uint4* s_kw = s_kv + wave * kTileU4;
+  uint4* s_vw = s_kv + (W + wave) * kTileU4;
+  float rg[kPairs][3];  // the ring class combined: (o[d0], o[d0 + 1], lse) of each pair
+  if constexpr (kSeq) {
+    // one state at a time: the band (the ring class), combined into
+    // registers, then the sink and tail (the rest class).  Each class's
+    // blocks go to the same virtual waves, in the same order, as in the
+    // two-class stream, and the band's and the rest's block lists number
+    // their blocks as its ranges 2 and 0, 1 do.
+    WaveState st, unused;
+    state_reset(st);
+    stream_blocks<G, false>(ks, one_range(band_begin, new_end), head_begin, c.q_scale, qb, s_kw, s_vw, st,
+                            unused, vw);
+    __syncthreads();  // every wave is done with its tiles
+    state_to_lds<G>(st, so, s_ml, vw);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kPairs; ++i) {
+      const int e = tid + i * (W * 64);
+      rg[i][0] = rg[i][1] = 0.0f;
+      rg[i][2] = -INFINITY;
+      if (e < G * 64) combine_waves<G, kV>(so, s_ml, e >> 6, 2 * (e & 63), rg[i][0], rg[i][1], rg[i][2]);
+    }
+    __syncthreads();  // the combine area is the tiles again
+    BlockList rl;  // sink as range 1, tail as range 2 (range 0, the masked one, empty)
+    rl.begin0 = rl.end0 = 0;
+    rl.first1 = 0;
+    rl.begin1 = bl.begin0;
+    rl.end1 = bl.end0;
+    rl.first2 = bl.first1;
+    rl.begin2 = bl.begin1;
+    rl.end2 = bl.end1;
+    rl.nblk = bl.first2;
+    state_reset(st);
+    stream_blocks<G, false>(ks, rl, 0, c.q_scale, qb, s_kw, s_vw, st, unused, vw, true, true,
+                            pre != nullptr ? pre[0] : nullptr, pre != nullptr ? pre[1] : nullptr);
+    __syncthreads();
+    state_to_lds<G>(st, so_rest, sml_rest, vw);
+    __syncthreads();
+  } else {
+    WaveState rest, ring;
+    state_reset(rest);
+    state_reset(ring);
+    const bool do_rest = W == kV || wave < kV;
+    const bool do_ring = W == kV || wave >= kV;
+    stream_blocks<G, true>(ks, bl, head_begin, c.q_scale, qb, s_kw, s_vw, rest, ring, vw, do_rest, do_ring,
+                           pre != nullptr ? pre[0] : nullptr, pre != nullptr ? pre[1] : nullptr);
+    __syncthreads();  // every wave is done with its tiles
+    if (do_ring) state_to_lds<G>(ring, so, s_ml, vw);
+    if (do_rest) state_to_lds<G>(rest, so_rest, sml_rest, vw);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kPairs; ++i) {
+      const int e = tid + i * (W * 64);
+      rg[i][0] = rg[i][1] = 0.0f;
+      rg[i][2] = -INFINITY;
+      if (e < G * 64) combine_waves<G, kV>(so, s_ml, e >> 6, 2 * (e & 63), rg[i][0], rg[i][1], rg[i][2]);
+    }
+  }
 
   const int dest = P % M;
 #pragma unroll
@@ -986,21 +1104,20 @@ __device__ __forceinline__ void fused_group(const DecideParams& p, int n, int hk
     const int64_t ho = static_cast<int64_t>(n) * Hq + hq;
     MergeState st{-INFINITY, {0.0f, 0.0f}};
     float o0, o1, l;
-    combine_waves<G, W>(so, &s_ml[0][0][0][0], h, d0, o0, o1, l);
-    merge_into(st, l, o0, o1);
+    merge_into(st, rg[i][2], rg[i][0], rg[i][1]);
     merge_into(st, s_entry[h], bf16_lo(ent[i]), bf16_hi(ent[i]));
     if (ready && P >= 0) {  // ring row (a negative past_len has no ring slot)
       const int64_t rowi = (static_cast<int64_t>(req) * M + dest) * Hq + hq;
       const bool valid = isfinite(st.lse);
-      *reinterpret_cast<uint32_t*>(p.ring_q + rowi * kHeadDim + d0) = qpre[i];
-      *reinterpret_cast<uint32_t*>(p.attn_cache + rowi * kHeadDim + d0) = valid ? pack_bf16x2(st.o[0], st.o[1]) : 0u;
-      if (d0 == 0) p.ring_lse[rowi] = valid ? st.lse : -INFINITY;
+      *reinterpret_cast<uint32_t*>(c.ring_q + rowi * kHeadDim + d0) = qpre[i];
+      *reinterpret_cast<uint32_t*>(c.attn_cache + rowi * kHeadDim + d0) = valid ? pack_bf16x2(st.o[0], st.o[1]) : 0u;
+      if (d0 == 0) c.ring_lse[rowi] = valid ? st.lse : -INFINITY;
     }
-    combine_waves<G, W>(so + W * G * kOPitch, &s_ml[1][0][0][0], h, d0, o0, o1, l);
+    combine_waves<G, kV>(so_rest, sml_rest, h, d0, o0, o1, l);
     merge_into(st, l, o0, o1);
     const bool valid = isfinite(st.lse);
-    *reinterpret_cast<uint32_t*>(p.out + ho * kHeadDim + d0) = valid ? pack_bf16x2(st.o[0], st.o[1]) : 0u;
-    if (p.out_lse != nullptr && d0 == 0) p.out_lse[ho] = valid ? st.lse : -INFINITY;
+    *reinterpret_cast<uint32_t*>(c.out + ho * kHeadDim + d0) = valid ? pack_bf16x2(st.o[0], st.o[1]) : 0u;
+    if (c.out_lse != nullptr && d0 == 0) c.out_lse[ho] = valid ? st.lse : -INFINITY;
   }
 }
 
@@ -1078,13 +1195,15 @@ __global__ void __launch_bounds__(W * 64, W == kWaves ? 2 : 1) match_decide_kern
     cur_hi = ocl[p.s.out_cache_loc_is_i64 ? w0 + 1 : w0];
     ks = make_stream(p.req_to_token, p.s.r2t_rows, p.s.r2t_stride, req, P, -1, p.s.pool_tokens, p.k_buffer,
                      p.v_buffer, p.s.Hkv, hkv, c);
+    // (rest blocks of the wave's virtual wave; an eight-wave workgroup's
+    // waves 4..7 stream the band only)
     const BlockList rblk = rest_blocks(P, cache_end_for_pos(P, p.S), p.F);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       int base, end;
-      block_span(rblk, wave + W * u, base, end);
+      block_span(rblk, (wave & (kVirtualWaves - 1)) + kVirtualWaves * u, base, end);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) pre[u][i] = ks.raw_row(base + 8 * row + i);
+      for (int i = 0; i < 8; ++i) pre[u][i] = (W == kVirtualWaves || wave < kVirtualWaves) ? ks.raw_row(base + 8 * row + i) : 0;
     }
   }
   const bool req_ok = req >= 0 && req < p.s.R;
@@ -1311,7 +1430,14 @@ __global__ void __launch_bounds__(W * 64, W == kWaves ? 2 : 1) match_decide_kern
                            : static_cast<int64_t>(cur_lo);
     ks.cur_row = (cl >= 0 && cl < p.s.pool_tokens) ? static_cast<int>(cl) : -1;
     if ((tid >> 4) >= G) qpost_w = make_uint4(0, 0, 0, 0);
-    fused_group<G, W>(p, n, hkv, P, req, ready, s_span[0], s_span[1], s_rect, s_mslot, s_entry, qpost_w, ks, pre);
+    __shared__ uint4 s_kv[2][W][kTileU4];  // K and V tiles; the combine area afterwards
+    __shared__ uint4 s_q[16 * 16];
+    __shared__ float s_ml[2][kVirtualWaves][G][2];
+    static_assert(sizeof(float) * 2 * kVirtualWaves * G * kOPitch <= sizeof(s_kv), "combine area");
+    const ShortCtx sc{p.q_pre, p.ring_q, p.attn_cache, p.ring_lse, p.out, p.out_lse, p.s.Hq, p.s.M, p.s.R, p.F,
+                      p.q_scale};
+    short_group<G, W, false>(sc, n, hkv, P, req, ready, s_span[0], s_span[1], s_rect, s_mslot, s_entry, qpost_w, ks, pre,
+                      &s_kv[0][0][0], s_q, &s_ml[0][0][0][0]);
   }
 }
 
@@ -1353,6 +1479,21 @@ __device__ __forceinline__ GroupSpans load_spans(const int32_t* rect_begin, cons
 // last band piece can be shorter).
 __device__ __forceinline__ int full_band_pieces(const GroupSpans& s) {
   return (s.new_end - s.band_begin) / s.chunk;
+}
+
+// A group of at most fuse_tokens tokens is short: its whole computation is
+// short_group, wherever it runs (the same rule as match_decide's).
+__device__ __forceinline__ bool group_is_short(const GroupSpans& s, int fuse_tokens) {
+  return fuse_tokens > 0 && group_tokens(s.sink_end, s.band_begin, s.new_end, s.kv_len) <= fuse_tokens;
+}
+
+// Tasks of a group in class A (full band pieces) and class B (the rest): a
+// group match_decide finished has none, a short group one class-B task.
+__device__ __forceinline__ void group_task_counts(const GroupSpans& s, bool fused, int fuse_tokens, int& na,
+                                                  int& nb) {
+  const bool shrt = group_is_short(s, fuse_tokens);
+  na = (fused || shrt) ? 0 : full_band_pieces(s);
+  nb = fused ? 0 : (shrt ? 1 : s.n_sink + s.n_band + s.n_tail - na);
 }
 
 // Block-wide exclusive scan of per-thread values (256 threads).
@@ -1464,9 +1605,8 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
   int my_a = 0, my_b = 0;
   for (int g = g_lo; tok > 0 && g < g_hi; ++g) {
     GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, g, p.F, chunk, p.cap);
-    const bool fused = p.group_fused[g] != 0;
-    const int na = fused ? 0 : full_band_pieces(sp);
-    const int nb = fused ? 0 : sp.n_sink + sp.n_band + sp.n_tail - na;
+    int na, nb;
+    group_task_counts(sp, p.group_fused[g] != 0, p.fuse_tokens, na, nb);
     const int b = g / gpb;
     if (g % gpb == 0) {
       s_off[b] = 0;
@@ -1505,7 +1645,9 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
       else ++longs;
       units += static_cast<uint32_t>((t + 63) >> 6);
       p.group_chunk[g] = sp.chunk;
-      p.group_ntasks[g] = p.group_fused[g] != 0 ? 0 : sp.n_sink + sp.n_band + sp.n_tail;
+      int na, nb;
+      group_task_counts(sp, p.group_fused[g] != 0, p.fuse_tokens, na, nb);
+      p.group_ntasks[g] = na + nb;
       p.group_rect_tiles[g] = sp.n_band;
       p.group_tail_tiles[g] = sp.n_tail;
       const int mode = p.group_mode[g];
@@ -1592,6 +1734,7 @@ __device__ __forceinline__ int next_task(const AttnParams& p, int& s_task) {
 struct TaskInfo {
   int g, j, n, hkv, a, b;
   bool band;
+  bool shrt;  // the whole short group (short_group)
   int P, req;
   bool req_ok;
   int64_t cur_loc;
@@ -1616,9 +1759,9 @@ __device__ __forceinline__ TaskInfo decode_task(const AttnParams& p, const int* 
   int g = lo * gpb;
   GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, g, p.F, chunk, p.cap);
   for (; g + 1 < min((lo + 1) * gpb, NG); ++g) {
-    const bool fused = p.group_fused[g] != 0;
-    const int na = full_band_pieces(sp);
-    const int cnt = fused ? 0 : (class_a ? na : sp.n_sink + sp.n_band + sp.n_tail - na);
+    int na, nb;
+    group_task_counts(sp, p.group_fused[g] != 0, p.fuse_tokens, na, nb);
+    const int cnt = class_a ? na : nb;
     if (k < cnt) break;
     k -= cnt;
     sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, g + 1, p.F, chunk, p.cap);
@@ -1629,15 +1772,21 @@ __device__ __forceinline__ TaskInfo decode_task(const AttnParams& p, const int* 
   // piece index j of the group (sink pieces, band pieces, tail pieces), which
   // is also the partial's slot: class A takes the full band pieces, class B
   // the sink pieces, the band remainder and the tail pieces, in that order
+  ti.shrt = !class_a && group_is_short(sp, p.fuse_tokens);
   const int na = full_band_pieces(sp);
-  if (class_a)
+  if (ti.shrt)
+    ti.j = 0;
+  else if (class_a)
     ti.j = sp.n_sink + k;
   else if (k < sp.n_sink)
     ti.j = k;
   else
     ti.j = k + na;
   ti.band = false;
-  if (ti.j < sp.n_sink) {
+  if (ti.shrt) {
+    ti.a = sp.band_begin;
+    ti.b = sp.new_end;
+  } else if (ti.j < sp.n_sink) {
     ti.a = ti.j * sp.chunk;
     ti.b = min(ti.a + sp.chunk, sp.sink_end);
   } else if (ti.j < sp.n_sink + sp.n_band) {
@@ -1656,228 +1805,11 @@ __device__ __forceinline__ TaskInfo decode_task(const AttnParams& p, const int* 
   return ti;
 }
 
-// Combines the per-wave softmax states in LDS (unnormalised o, running max m
-// in log2 units, sum l) into one normalised partial (o, natural-log lse) per
-// head and stores it in slot j of group g.
-template <int G>
-__device__ __forceinline__ void write_partial(const AttnParams& p, int g, int j,
-                                              const float (*s_o)[G][kHeadDim],
-                                              const float (*s_ml)[G][2]) {
-  const int tid = threadIdx.x;
-  const int64_t slot = static_cast<int64_t>(g) * p.cap + j;
-  for (int e = tid; e < G * kHeadDim; e += kBlock) {
-    const int h = e / kHeadDim;
-    const int d = e - h * kHeadDim;
-    float mm = kNegBig;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, s_ml[w][h][0]);
-    float ll = 0.0f, oo = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float sc = fast_exp2(s_ml[w][h][0] - mm);
-      ll += s_ml[w][h][1] * sc;
-      oo += s_o[w][h][d] * sc;
-    }
-    const bool nonempty = ll > 0.0f;
-    const float ov = nonempty ? oo / ll : 0.0f;
-    const int64_t oi = static_cast<int64_t>(g) * p.o_group_stride + (static_cast<int64_t>(j) * G + h) * kHeadDim + d;
-    if (p.partial_bf16)
-      static_cast<uint16_t*>(p.partial_o)[oi] = f32_to_bf16(ov);
-    else
-      static_cast<float*>(p.partial_o)[oi] = ov;
-    if (d == 0) p.partial_lse[slot * G + h] = nonempty ? (mm + log2f(ll)) * kLn2 : -INFINITY;
-  }
-}
-
-template <int G>
-__global__ void __launch_bounds__(kBlock) span_attention_kernel(AttnParams p) {
-  constexpr int U = 2;                 // tokens per row per iteration
-  constexpr int kStep = kWaves * 4 * U;  // tokens per workgroup iteration
-  extern __shared__ int s_off[];  // 2 (NB + 1) bucket task offsets (dynamic)
-  __shared__ int s_tmp[kWaves];
-  __shared__ float s_o[kWaves][G][kHeadDim];
-  __shared__ float s_ml[kWaves][G][2];
-
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int row = lane >> 4;
-  const int c = lane & 15;
-  const int NG = p.s.N * p.s.Hkv;
-
-  if (p.phase_cycles != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
-    p.phase_cycles[2] = static_cast<int64_t>(wall_clock64());
-  int total_tasks = 0, chunk = 0, active_wgs = 0;
-  plan_tasks(p, s_off, s_tmp, total_tasks, chunk, active_wgs);
-  if (p.phase_cycles != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
-    p.phase_cycles[3] = static_cast<int64_t>(wall_clock64());
-  if (static_cast<int>(blockIdx.x) >= active_wgs) return;
-
-  // ---- tasks ----
-  const int Hq = p.s.Hq;
-  const int Hkv = p.s.Hkv;
-  const int my_tok = wave * 4 + row;  // token offset inside each 16-token sub-block
-  __shared__ int s_task;
-  for (int t = next_task(p, s_task); t < total_tasks; t = next_task(p, s_task)) {
-    const TaskInfo ti = decode_task(p, s_off, NG, chunk, t);
-    const int g = ti.g, j = ti.j, n = ti.n, hkv = ti.hkv, a = ti.a, b = ti.b, P = ti.P, req = ti.req;
-    const bool band = ti.band, req_ok = ti.req_ok;
-    const int64_t cur_loc = ti.cur_loc;
-    const int32_t* r2t = p.req_to_token + static_cast<int64_t>(req_ok ? req : 0) * p.s.r2t_stride;
-
-    // per-head band start (positions before it are masked for that head)
-    int mb[G];
-    float q[G][8];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const int hq = hkv * G + h;
-      mb[h] = band ? p.head_rect_start[static_cast<int64_t>(n) * Hq + hq] : 0;
-      const uint4 w = *reinterpret_cast<const uint4*>(p.q_post + (static_cast<int64_t>(n) * Hq + hq) * kHeadDim + c * 8);
-      unpack8(w, q[h]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) q[h][i] *= p.q_scale;
-    }
-    float m[G], l[G], o[G][8];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      m[h] = kNegBig;
-      l[h] = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[h][i] = 0.0f;
-    }
-
-    auto phys_of = [&](int pos) -> int64_t {
-      if (pos >= b || !req_ok || (pos != P && pos >= p.s.r2t_stride)) return -1;
-      const int64_t ph = pos == P ? cur_loc : static_cast<int64_t>(r2t[pos]);
-      return (ph >= 0 && ph < p.s.pool_tokens) ? ph : -1;
-    };
-    const int64_t kv_stride = static_cast<int64_t>(Hkv) * kHeadDim;
-    const uint16_t* kbase = p.k_buffer + static_cast<int64_t>(hkv) * kHeadDim + c * 8;
-    const uint16_t* vbase = p.v_buffer + static_cast<int64_t>(hkv) * kHeadDim + c * 8;
-
-    int64_t ph0[U], ph1[U];
-    uint4 k0[U], v0[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) ph0[u] = phys_of(a + u * 16 + my_tok);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      k0[u] = make_uint4(0, 0, 0, 0);
-      v0[u] = make_uint4(0, 0, 0, 0);
-      if (ph0[u] >= 0) {
-        k0[u] = *reinterpret_cast<const uint4*>(kbase + ph0[u] * kv_stride);
-        v0[u] = *reinterpret_cast<const uint4*>(vbase + ph0[u] * kv_stride);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) ph1[u] = phys_of(a + kStep + u * 16 + my_tok);
-
-    for (int base_pos = a; base_pos < b; base_pos += kStep) {
-      // prefetch the next iteration's rows and the one after's indices
-      uint4 k1[U], v1[U];
-      int64_t ph2[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        k1[u] = make_uint4(0, 0, 0, 0);
-        v1[u] = make_uint4(0, 0, 0, 0);
-        if (ph1[u] >= 0) {
-          k1[u] = *reinterpret_cast<const uint4*>(kbase + ph1[u] * kv_stride);
-          v1[u] = *reinterpret_cast<const uint4*>(vbase + ph1[u] * kv_stride);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) ph2[u] = phys_of(base_pos + 2 * kStep + u * 16 + my_tok);
-
-      float s[G][U];
-      float vf[U][8];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        float kf[8];
-        unpack8(k0[u], kf);
-        unpack8(v0[u], vf[u]);
-        const int pos = base_pos + u * 16 + my_tok;
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-          float acc = 0.0f;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) acc = fmaf(q[h][i], kf[i], acc);
-          acc = row16_sum(acc);
-          s[h][u] = (ph0[u] >= 0 && pos >= mb[h]) ? acc : -INFINITY;
-        }
-      }
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        float mx = s[h][0];
-#pragma unroll
-        for (int u = 1; u < U; ++u) mx = fmaxf(mx, s[h][u]);
-        const float m_new = fmaxf(m[h], mx);
-        const float alpha = fast_exp2(m[h] - m_new);
-        float pu[U];
-        float psum = 0.0f;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          pu[u] = fast_exp2(s[h][u] - m_new);
-          psum += pu[u];
-        }
-        l[h] = fmaf(l[h], alpha, psum);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float acc = o[h][i] * alpha;
-#pragma unroll
-          for (int u = 0; u < U; ++u) acc = fmaf(pu[u], vf[u][i], acc);
-          o[h][i] = acc;
-        }
-        m[h] = m_new;
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        k0[u] = k1[u];
-        v0[u] = v1[u];
-        ph0[u] = ph1[u];
-        ph1[u] = ph2[u];
-      }
-    }
-
-    // ---- combine the four rows of the wave, then the waves ----
-#pragma unroll
-    for (int msk = 16; msk <= 32; msk <<= 1) {
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float mo = __shfl_xor(m[h], msk);
-        const float lo2 = __shfl_xor(l[h], msk);
-        const float m_new = fmaxf(m[h], mo);
-        const float a1 = fast_exp2(m[h] - m_new);
-        const float a2 = fast_exp2(mo - m_new);
-        l[h] = l[h] * a1 + lo2 * a2;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float oo = __shfl_xor(o[h][i], msk);
-          o[h][i] = o[h][i] * a1 + oo * a2;
-        }
-        m[h] = m_new;
-      }
-    }
-    if (row == 0) {
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) s_o[wave][h][c * 8 + i] = o[h][i];
-        if (c == 0) {
-          s_ml[wave][h][0] = m[h];
-          s_ml[wave][h][1] = l[h];
-        }
-      }
-    }
-    __syncthreads();
-    write_partial<G>(p, g, j, s_o, s_ml);  // next_task's barrier closes the task
-  }
-}
-
 // ------------------------------------------------- MFMA span attention ----
 //
-// Same plan and task list as span_attention_kernel; a task is one range of
-// the block stream above (band pieces mask each head's positions before its
-// own band start).  The four waves' states are combined through LDS into one
-// normalised partial per head.
+// A task is one range of the block stream above (band pieces mask each
+// head's positions before its own band start).  The four waves' states are
+// combined through LDS into one normalised partial per head.
 template <int G>
 __device__ __forceinline__ void mfma_task(const AttnParams& p, const TaskInfo& ti, uint4 (*s_kv)[kWaves][kTileU4],
                                           uint4* s_q, float (*s_ml)[G][2]) {
@@ -1903,11 +1835,11 @@ __device__ __forceinline__ void mfma_task(const AttnParams& p, const TaskInfo& t
   WaveState st, unused;
   state_reset(st);
   stream_blocks<G, false>(ks, one_range(ti.a, ti.b), head_begin, p.q_scale, qb, &s_kv[0][wave][0],
-                          &s_kv[1][wave][0], st, unused);
+                          &s_kv[1][wave][0], st, unused, wave);
   // ---- wave results -> LDS (over the tiles), then combine the four waves ----
   __syncthreads();  // every wave is done with its tiles
   float* so = reinterpret_cast<float*>(&s_kv[0][0][0]);
-  state_to_lds<G>(st, so, &s_ml[0][0][0]);
+  state_to_lds<G>(st, so, &s_ml[0][0][0], wave);
   __syncthreads();
   const int64_t slot = static_cast<int64_t>(ti.g) * p.cap + ti.j;
   for (int e = tid; e < G * 64; e += kBlock) {
@@ -1924,14 +1856,49 @@ __device__ __forceinline__ void mfma_task(const AttnParams& p, const TaskInfo& t
   // next_task's barrier closes the task
 }
 
+// A short group left to this kernel: the whole group as one task, computed by
+// short_group exactly as match_decide computes the groups it finishes (the
+// same four virtual waves, combine and merges), so that where a short group
+// runs never changes its results.  Writes out, out_lse and the ring row.
+template <int G>
+__device__ __forceinline__ void short_task(const AttnParams& p, const TaskInfo& ti, uint4* s_kv, uint4* s_q,
+                                           float* s_ml, int* s_rect, int* s_mslot, float* s_entry) {
+  const int tid = task_tid();
+  const int n = ti.n, hkv = ti.hkv;
+  const int Hq = p.s.Hq;
+  const bool ready = request_ready(p.cache_ready, p.cache_epoch, p.request_epoch, ti.req, p.R);
+  if (tid < G) {
+    const int64_t ho = static_cast<int64_t>(n) * Hq + hkv * G + tid;
+    const int hit = p.head_hit[ho];
+    const int ms = p.head_match_slot[ho];
+    const bool reuse = hit != 0 && ms >= 0 && ti.req >= 0 && ti.req < p.R;
+    s_rect[tid] = p.head_rect_start[ho];
+    s_mslot[tid] = hit != 0 ? ms : -1;
+    s_entry[tid] = reuse ? p.lse_cache[(static_cast<int64_t>(ti.req) * p.s.M + ms) * Hq + hkv * G + tid] : -INFINITY;
+  }
+  uint4 qpost_w = make_uint4(0, 0, 0, 0);
+  if ((tid >> 4) < G)
+    qpost_w = *reinterpret_cast<const uint4*>(p.q_post + (static_cast<int64_t>(n) * Hq + hkv * G + (tid >> 4)) * kHeadDim +
+                                              (tid & 15) * 8);
+  const KvStream ks = make_stream(p.req_to_token, p.s.r2t_rows, p.s.r2t_stride, ti.req, ti.P, ti.cur_loc,
+                                  p.s.pool_tokens, p.k_buffer, p.v_buffer, p.s.Hkv, hkv, tid & 15);
+  const ShortCtx sc{p.q_pre, p.ring_q, p.attn_cache, p.lse_cache, p.out, p.out_lse, Hq, p.s.M, p.R, p.F, p.q_scale};
+  __syncthreads();  // s_rect / s_mslot / s_entry
+  short_group<G, kVirtualWaves, true>(sc, n, hkv, ti.P, ti.req, ready, ti.a, ti.b, s_rect, s_mslot, s_entry, qpost_w, ks,
+                                nullptr, s_kv, s_q, s_ml);
+}
+
 template <int G>
 __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnParams p) {
   extern __shared__ int s_off[];  // 2 (NB + 1) bucket task offsets (dynamic)
   __shared__ int s_tmp[kWaves];
   __shared__ uint4 s_kv[2][kWaves][kTileU4];
   __shared__ uint4 s_q[16 * 16];
-  __shared__ float s_ml[kWaves][G][2];
-  static_assert(sizeof(float) * kWaves * G * kOPitch <= sizeof(s_kv), "combine area");
+  __shared__ float s_ml[2][kWaves][G][2];
+  __shared__ int s_rect[kMaxGroup], s_mslot[kMaxGroup];
+  __shared__ float s_entry[kMaxGroup];
+  static_assert(sizeof(float) * 2 * kWaves * G * kOPitch <= sizeof(s_kv), "combine area");
+  static_assert(kWaves == kVirtualWaves, "a short task runs short_group on four waves");
 
   if (p.phase_cycles != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
     p.phase_cycles[2] = static_cast<int64_t>(wall_clock64());
@@ -1943,8 +1910,13 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
   if (static_cast<int>(blockIdx.x) >= active_wgs) return;
 
   __shared__ int s_task;
-  for (int t = next_task(p, s_task); t < total_tasks; t = next_task(p, s_task))
-    mfma_task<G>(p, decode_task(p, s_off, NG, chunk, t), s_kv, s_q, s_ml);
+  for (int t = next_task(p, s_task); t < total_tasks; t = next_task(p, s_task)) {
+    const TaskInfo ti = decode_task(p, s_off, NG, chunk, t);
+    if (ti.shrt)
+      short_task<G>(p, ti, &s_kv[0][0][0], s_q, &s_ml[0][0][0][0], s_rect, s_mslot, s_entry);
+    else
+      mfma_task<G>(p, ti, s_kv, s_q, s_ml[0]);
+  }
 }
 
 // ============================================================ 3. merge ====
@@ -1986,13 +1958,14 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
   const int chunk = p.group_chunk[g];
   const int hit = p.head_hit[ho];
   const int mslot = p.head_match_slot[ho];
-  if (fused != 0) {  // finished by match_decide
+  const int sink_end = min(p.F, new_end);
+  const bool shrt = p.fuse_tokens > 0 && group_tokens(sink_end, band_begin, new_end, kv_len) <= p.fuse_tokens;
+  if (fused != 0 || shrt) {  // finished by match_decide or by a short task
     if (stamp) p.phase_cycles[5] = static_cast<int64_t>(wall_clock64());
     return;
   }
   const bool ready = request_ready(p.cache_ready, p.cache_epoch, p.request_epoch, req, p.s.R);
   const int dest = P % M;
-  const int sink_end = min(p.F, new_end);
   const int n_sink = ceil_div(sink_end, chunk);
   const int n_band = ceil_div(new_end - band_begin, chunk);
   const int n_tail = ceil_div(kv_len - new_end, chunk);
@@ -2107,8 +2080,6 @@ int fail(int code, const char* fmt, ...) {
     if (e_ != hipSuccess) return fail(MAC_ERR_HIP, "%s: %s", #call, hipGetErrorString(e_)); \
   } while (0)
 
-// MAC_AMD_ATTN_IMPL=valu selects the VALU span-attention kernel; the default
-// is the MFMA kernel.  Read once per process.
 // Target tasks per workgroup (MAC_AMD_TASKS_PER_WG, read once; 4..64).
 int tasks_per_wg() {
   static const int v = [] {
@@ -2159,27 +2130,18 @@ int fuse_tokens() {
   return x < 0 ? 0 : x;
 }
 
-int attn_impl() {
-  static const int impl = [] {
-    const char* e = std::getenv("MAC_AMD_ATTN_IMPL");
-    return (e != nullptr && std::strcmp(e, "valu") == 0) ? 0 : 1;
-  }();
-  return impl;
-}
-
 template <int G>
-void* attn_kernel_ptr(int impl) {
-  return impl ? reinterpret_cast<void*>(&span_attention_mfma_kernel<G>)
-              : reinterpret_cast<void*>(&span_attention_kernel<G>);
+void* attn_kernel_ptr() {
+  return reinterpret_cast<void*>(&span_attention_mfma_kernel<G>);
 }
 
 // Compute units of the device and resident span-attention workgroups per CU
 // for a given kernel and dynamic LDS size, cached per process.
 std::mutex g_dev_mu;
-std::map<std::tuple<int, int, int, size_t>, int> g_blocks_per_cu;
+std::map<std::tuple<int, int, size_t>, int> g_blocks_per_cu;
 std::map<int, int> g_cus;
 
-int attn_residency(int dev, int G, int impl, size_t dyn_lds, int* cus, int* per_cu) {
+int attn_residency(int dev, int G, size_t dyn_lds, int* cus, int* per_cu) {
   std::lock_guard<std::mutex> lk(g_dev_mu);
   auto ci = g_cus.find(dev);
   if (ci == g_cus.end()) {
@@ -2187,19 +2149,19 @@ int attn_residency(int dev, int G, int impl, size_t dyn_lds, int* cus, int* per_
     MAC_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
     ci = g_cus.emplace(dev, n).first;
   }
-  const auto key = std::make_tuple(dev, G, impl, dyn_lds);
+  const auto key = std::make_tuple(dev, G, dyn_lds);
   auto bi = g_blocks_per_cu.find(key);
   if (bi == g_blocks_per_cu.end()) {
     void* fn = nullptr;
     switch (G) {
-      case 1: fn = attn_kernel_ptr<1>(impl); break;
-      case 2: fn = attn_kernel_ptr<2>(impl); break;
-      case 3: fn = attn_kernel_ptr<3>(impl); break;
-      case 4: fn = attn_kernel_ptr<4>(impl); break;
-      case 5: fn = attn_kernel_ptr<5>(impl); break;
-      case 6: fn = attn_kernel_ptr<6>(impl); break;
-      case 7: fn = attn_kernel_ptr<7>(impl); break;
-      default: fn = attn_kernel_ptr<8>(impl); break;
+      case 1: fn = attn_kernel_ptr<1>(); break;
+      case 2: fn = attn_kernel_ptr<2>(); break;
+      case 3: fn = attn_kernel_ptr<3>(); break;
+      case 4: fn = attn_kernel_ptr<4>(); break;
+      case 5: fn = attn_kernel_ptr<5>(); break;
+      case 6: fn = attn_kernel_ptr<6>(); break;
+      case 7: fn = attn_kernel_ptr<7>(); break;
+      default: fn = attn_kernel_ptr<8>(); break;
     }
     int blocks = 0;
     MAC_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kBlock, dyn_lds));
@@ -2227,7 +2189,7 @@ bool fuse_policy_always() {
 
 template <int G>
 int launch_all(const DecideParams& dp, const AttnParams& ap, const MergeParams& mp, int attn_grid,
-               int impl, hipStream_t stream, hipEvent_t* ev) {
+               hipStream_t stream, hipEvent_t* ev) {
   const int NG = dp.s.N * dp.s.Hkv;
   if (ev) MAC_HIP(hipEventRecord(ev[0], stream));
   if (dp.splits > 1) {
@@ -2246,10 +2208,7 @@ int launch_all(const DecideParams& dp, const AttnParams& ap, const MergeParams& 
   MAC_HIP(hipGetLastError());
   if (ev) MAC_HIP(hipEventRecord(ev[1], stream));
   const size_t plan_lds = 2 * sizeof(int) * (static_cast<size_t>(ceil_div(NG, ap.plan_bucket)) + 1);
-  if (impl)
-    hipLaunchKernelGGL(span_attention_mfma_kernel<G>, dim3(attn_grid), dim3(kBlock), plan_lds, stream, ap);
-  else
-    hipLaunchKernelGGL(span_attention_kernel<G>, dim3(attn_grid), dim3(kBlock), plan_lds, stream, ap);
+  hipLaunchKernelGGL(span_attention_mfma_kernel<G>, dim3(attn_grid), dim3(kBlock), plan_lds, stream, ap);
   MAC_HIP(hipGetLastError());
   if (ev) MAC_HIP(hipEventRecord(ev[2], stream));
   hipLaunchKernelGGL(merge_write_kernel<G>, dim3(NG, G), dim3(kBlock), 0, stream, mp);
@@ -2271,21 +2230,6 @@ int decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev);
 
 extern "C" int mac_persistent_decode_bf16(const MacDecodeArgs* a, void* stream_ptr) {
   return mac::decode_impl(a, stream_ptr, nullptr);
-}
-
-extern "C" int mac_persistent_decode_bf16_timed(const MacDecodeArgs* a, void* stream_ptr, float* ms) {
-  g_err[0] = '\0';
-  MAC_REQUIRE(ms != nullptr, "ms must not be NULL");
-  hipEvent_t ev[4];
-  for (int i = 0; i < 4; ++i) MAC_HIP(hipEventCreate(&ev[i]));
-  int rc = mac::decode_impl(a, stream_ptr, ev);
-  if (rc == MAC_OK) {
-    hipError_t e = hipEventSynchronize(ev[3]);
-    for (int i = 0; i < 3 && e == hipSuccess; ++i) e = hipEventElapsedTime(&ms[i], ev[i], ev[i + 1]);
-    if (e != hipSuccess) rc = fail(MAC_ERR_HIP, "event timing: %s", hipGetErrorString(e));
-  }
-  for (int i = 0; i < 4; ++i) (void)hipEventDestroy(ev[i]);
-  return rc;
 }
 
 int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
@@ -2336,12 +2280,11 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   int dev = 0;
   MAC_HIP(hipGetDevice(&dev));
   int cus = 0, per_cu = 0;
-  const int impl = attn_impl();
   // The planner's LDS table has one entry per bucket of plan_bucket groups
   // (one group per entry up to kMaxPlanBuckets groups).
   const int plan_bucket = ceil_div(N * Hkv, kMaxPlanBuckets);
   const size_t plan_lds = 2 * sizeof(int) * (static_cast<size_t>(ceil_div(N * Hkv, plan_bucket)) + 1);
-  int rc = attn_residency(dev, G, impl, plan_lds, &cus, &per_cu);
+  int rc = attn_residency(dev, G, plan_lds, &cus, &per_cu);
   if (rc != MAC_OK) return rc;
 
   Shape s{};
@@ -2417,7 +2360,7 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
                      ? reinterpret_cast<uint32_t*>(a->complete_task_go + 2 * static_cast<int64_t>(N) * Hkv + 2)
                      : nullptr;
   dp.fuse_cus = cus;
-  dp.narrow_min_tokens = impl ? narrow_min_tokens() : LLONG_MAX;
+  dp.narrow_min_tokens = narrow_min_tokens();
   dp.q_post = static_cast<const uint16_t*>(a->q_post);
   dp.k_buffer = static_cast<const uint16_t*>(a->k_buffer);
   dp.v_buffer = static_cast<const uint16_t*>(a->v_buffer);
@@ -2465,7 +2408,7 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   ap.tile_tokens = a->tile_tokens;
   ap.tasks_per_wg = tasks_per_wg();
   ap.min_chunk = min_chunk();
-  ap.narrow_grid = impl ? cus : INT_MAX;  // the VALU kernel is instruction-bound: every resident workgroup
+  ap.narrow_grid = cus;
   ap.narrow_min_tokens = narrow_min_tokens();
   ap.group_fused = dp.group_fused;
   ap.fuse_sync = const_cast<uint32_t*>(dp.fuse_sync);
@@ -2473,6 +2416,18 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   ap.plan_bucket = plan_bucket;
   ap.long_groups = dp.long_groups;
   ap.phase_cycles = stamps;
+  ap.q_pre = dp.q_pre;
+  ap.ring_q = dp.ring_q;
+  ap.attn_cache = dp.attn_cache;
+  ap.lse_cache = a->lse_cache;
+  ap.out = dp.out;
+  ap.out_lse = dp.out_lse;
+  ap.cache_ready = dp.cache_ready;
+  ap.cache_epoch = dp.cache_epoch;
+  ap.request_epoch = dp.request_epoch;
+  ap.head_hit = a->head_hit;
+  ap.head_match_slot = a->head_match_slot;
+  ap.R = a->R;
 
   MergeParams mp{};
   mp.s = s;
@@ -2502,6 +2457,7 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   mp.group_fused = dp.group_fused;
   mp.long_groups = dp.long_groups;
   mp.phase_cycles = stamps;
+  mp.fuse_tokens = dp.fuse_tokens;
 
   // Persistent grid: what the device keeps resident, but no more workgroups
   // than the largest task count the caller's max_context allows.
@@ -2513,124 +2469,13 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   if (grid < 1) grid = 1;
 
   switch (G) {
-    case 1: return launch_all<1>(dp, ap, mp, static_cast<int>(grid), impl, stream, ev);
-    case 2: return launch_all<2>(dp, ap, mp, static_cast<int>(grid), impl, stream, ev);
-    case 3: return launch_all<3>(dp, ap, mp, static_cast<int>(grid), impl, stream, ev);
-    case 4: return launch_all<4>(dp, ap, mp, static_cast<int>(grid), impl, stream, ev);
-    case 5: return launch_all<5>(dp, ap, mp, static_cast<int>(grid), impl, stream, ev);
-    case 6: return launch_all<6>(dp, ap, mp, static_cast<int>(grid), impl, stream, ev);
-    case 7: return launch_all<7>(dp, ap, mp, static_cast<int>(grid), impl, stream, ev);
-    default: return launch_all<8>(dp, ap, mp, static_cast<int>(grid), impl, stream, ev);
+    case 1: return launch_all<1>(dp, ap, mp, static_cast<int>(grid), stream, ev);
+    case 2: return launch_all<2>(dp, ap, mp, static_cast<int>(grid), stream, ev);
+    case 3: return launch_all<3>(dp, ap, mp, static_cast<int>(grid), stream, ev);
+    case 4: return launch_all<4>(dp, ap, mp, static_cast<int>(grid), stream, ev);
+    case 5: return launch_all<5>(dp, ap, mp, static_cast<int>(grid), stream, ev);
+    case 6: return launch_all<6>(dp, ap, mp, static_cast<int>(grid), stream, ev);
+    case 7: return launch_all<7>(dp, ap, mp, static_cast<int>(grid), stream, ev);
+    default: return launch_all<8>(dp, ap, mp, static_cast<int>(grid), stream, ev);
   }
-}
-
-// ============================================= no-allocation entry point ====
-//
-// mac_persistent_decode_bf16_noalloc runs the same three kernels with every
-// workspace (decisions, task table, partial (o, lse) results, counters) in
-// one file-scope device array instead of caller memory.  Its limits size the
-// array: at most kNoAllocMaxHeads decode query heads (N * Hq), rings of at
-// most 256 * kNoAllocMatchTiles slots, and kNoAllocPartialSlots partial slots
-// per group (the task plan enlarges a long group's chunks to fit them).
-// Every call on a device shares that device's array: calls that overlap on
-// one GPU (different streams) race.  Nothing in it needs clearing between
-// calls: match_decide zeroes the task counter and rewrites every per-group
-// field a later kernel reads.
-
-namespace mac {
-
-constexpr int kNoAllocMaxHeads = 4096;
-constexpr int kNoAllocPartialSlots = 32;
-constexpr int kNoAllocMatchTiles = 8;
-
-constexpr size_t up256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
-
-struct ScratchLayout {  // byte offsets into the scratch array
-  static constexpr size_t H = kNoAllocMaxHeads;
-  static constexpr size_t kMatch = up256(H * kNoAllocMatchTiles * 4);  // one match array
-  static constexpr size_t kHead = up256(H * 4);                        // one head_* / group_* array
-  static constexpr size_t kTask = up256((2 * H + kTaskExtra) * 4);     // complete_task_go / _tile
-  static constexpr size_t match_dist = 0;
-  static constexpr size_t match_pos = match_dist + kMatch;
-  static constexpr size_t match_slot = match_pos + kMatch;
-  static constexpr size_t head0 = match_slot + kMatch;                 // 6 head arrays
-  static constexpr size_t group0 = head0 + 6 * kHead;                  // 7 group arrays (groups <= heads)
-  static constexpr size_t task_go = group0 + 7 * kHead;
-  static constexpr size_t task_tile = task_go + kTask;
-  static constexpr size_t task_counts = task_tile + kTask;
-  static constexpr size_t partial_lse = task_counts + 256;
-  static constexpr size_t partial_o = partial_lse + up256(H * kNoAllocPartialSlots * 4);
-  static constexpr size_t bytes = partial_o + up256(H * kNoAllocPartialSlots * kHeadDim * 4);
-};
-constexpr size_t kScratchBytes = ScratchLayout::bytes;  // ~65 MiB
-
-}  // namespace mac
-
-static __device__ __align__(256) unsigned char scratch[mac::kScratchBytes];
-
-namespace mac {
-
-std::mutex g_scratch_mu;
-std::map<int, unsigned char*> g_scratch;
-
-// Device address of this device's scratch array (looked up once per device,
-// with that device current).
-int scratch_base(int dev, unsigned char** out) {
-  std::lock_guard<std::mutex> lk(g_scratch_mu);
-  auto it = g_scratch.find(dev);
-  if (it == g_scratch.end()) {
-    unsigned char* ptr = nullptr;
-    MAC_HIP(hipGetSymbolAddress(reinterpret_cast<void**>(&ptr), HIP_SYMBOL(scratch)));
-    if (ptr == nullptr) return fail(MAC_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
-    it = g_scratch.emplace(dev, ptr).first;
-  }
-  *out = it->second;
-  return MAC_OK;
-}
-
-}  // namespace mac
-
-extern "C" int mac_persistent_decode_bf16_noalloc(const MacDecodeArgs* a, void* stream_ptr) {
-  g_err[0] = '\0';
-  MAC_REQUIRE(a != nullptr, "args must not be NULL");
-  MAC_REQUIRE(a->struct_size == sizeof(MacDecodeArgs) && a->abi_version == MAC_ABI_VERSION,
-              "MacDecodeArgs size/version mismatch (got %u/%u, library expects %zu/%d)",
-              a->struct_size, a->abi_version, sizeof(MacDecodeArgs), MAC_ABI_VERSION);
-  const int64_t heads = static_cast<int64_t>(a->N) * a->Hq;
-  MAC_REQUIRE(heads <= kNoAllocMaxHeads,
-              "no-allocation decode supports at most %d query heads per step (N * Hq = %lld)", kNoAllocMaxHeads,
-              static_cast<long long>(heads));
-  MAC_REQUIRE(a->M <= 256 * kNoAllocMatchTiles, "no-allocation decode supports rings of at most %d slots (M = %d)",
-              256 * kNoAllocMatchTiles, a->M);
-  MAC_REQUIRE(a->max_context > 0, "max_context must be positive");
-  int dev = 0;
-  MAC_HIP(hipGetDevice(&dev));
-  unsigned char* base = nullptr;
-  int rc = scratch_base(dev, &base);
-  if (rc != MAC_OK) return rc;
-  using L = ScratchLayout;
-  MacDecodeArgs w = *a;
-  auto i32 = [&](size_t off) { return reinterpret_cast<int32_t*>(base + off); };
-  w.match_dist = reinterpret_cast<float*>(base + L::match_dist);
-  w.match_pos = i32(L::match_pos);
-  w.match_slot = i32(L::match_slot);
-  int32_t** heads_ws[6] = {&w.head_hit, &w.head_match_slot, &w.head_match_pos,
-                           &w.head_prefix_end, &w.head_rect_start, &w.head_new_end};
-  for (int i = 0; i < 6; ++i) *heads_ws[i] = i32(L::head0 + i * L::kHead);
-  int32_t** groups_ws[7] = {&w.group_rect_begin, &w.group_rect_end, &w.group_rect_tiles, &w.group_tail_begin,
-                            &w.group_tail_end, &w.group_tail_tiles, &w.group_mode};
-  for (int i = 0; i < 7; ++i) *groups_ws[i] = i32(L::group0 + i * L::kHead);
-  w.complete_task_go = i32(L::task_go);
-  w.complete_task_tile = i32(L::task_tile);
-  w.task_counts = i32(L::task_counts);
-  w.partial_lse = reinterpret_cast<float*>(base + L::partial_lse);
-  w.partial_o = base + L::partial_o;
-  w.partial_o_is_bf16 = 0;
-  w.max_match_tiles = kNoAllocMatchTiles;
-  w.match_tile_slots = 256;
-  w.max_tiles_context = kNoAllocPartialSlots;
-  w.tile_tokens = (a->max_context + kNoAllocPartialSlots - 1) / kNoAllocPartialSlots;
-  w.complete_task_len = 2 * static_cast<int64_t>(a->N) * (a->Hkv > 0 ? a->Hkv : 1) + kTaskExtra;
-  w.workspace_rows = a->N;
-  return mac::decode_impl(&w, stream_ptr, nullptr);
 }

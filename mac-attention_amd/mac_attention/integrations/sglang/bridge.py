@@ -73,8 +73,6 @@ class MacDecodeArgs(ctypes.Structure):
 
 EXPORTED_SYMBOLS = (
     "mac_persistent_decode_bf16",
-    "mac_persistent_decode_bf16_timed",
-    "mac_persistent_decode_bf16_noalloc",
     "mac_prefill_update_cache",
     "mac_mark_persistent_ready",
     "mac_invalidate_persistent_ready",
@@ -131,11 +129,6 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.mac_abi_version.restype = ctypes.c_int
     lib.mac_persistent_decode_bf16.argtypes = [ctypes.POINTER(MacDecodeArgs), _p]
     lib.mac_persistent_decode_bf16.restype = ctypes.c_int
-    lib.mac_persistent_decode_bf16_timed.argtypes = [
-        ctypes.POINTER(MacDecodeArgs), _p, ctypes.POINTER(ctypes.c_float)]
-    lib.mac_persistent_decode_bf16_timed.restype = ctypes.c_int
-    lib.mac_persistent_decode_bf16_noalloc.argtypes = [ctypes.POINTER(MacDecodeArgs), _p]
-    lib.mac_persistent_decode_bf16_noalloc.restype = ctypes.c_int
     lib.mac_prefill_update_cache.argtypes = [
         _p, _p, _p, _p, _i32, _p, _i32, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i32, _p, _p,
     ]
@@ -164,20 +157,40 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
 
 
 BENCH_LIB_PATH = os.environ.get("MAC_BENCH_LIBRARY", os.path.join(_PKG_ROOT, "libmac_bench.so"))
-BENCH_EXPORTED_SYMBOLS = ("mac_bench_stream_read", "mac_bench_last_error")
+BENCH_EXPORTED_SYMBOLS = ("mac_bench_stream_read", "mac_bench_decode_timed", "mac_bench_last_error")
+NOALLOC_LIB_PATH = os.environ.get("MAC_NOALLOC_LIBRARY", os.path.join(_PKG_ROOT, "libmac_noalloc.so"))
+NOALLOC_EXPORTED_SYMBOLS = ("mac_persistent_decode_bf16_noalloc", "mac_noalloc_last_error")
 
 
 @lru_cache(maxsize=1)
 def load_bench_library(path: str | None = None) -> ctypes.CDLL:
-    """Open libmac_bench.so, the streaming-read measurement helper (not part
-    of the decode library)."""
+    """Open libmac_bench.so, the measurement helpers (not part of the decode
+    library): the streaming read and the decode step timed per kernel."""
     path = path or BENCH_LIB_PATH
     if not os.path.exists(path):
         raise RuntimeError(f"measurement helper not found at {path}; build with __graft_entry__.build()")
     lib = ctypes.CDLL(path)
     lib.mac_bench_stream_read.argtypes = [_p, _i64, _p, _i32, _p]
     lib.mac_bench_stream_read.restype = ctypes.c_int
+    lib.mac_bench_decode_timed.argtypes = [ctypes.POINTER(MacDecodeArgs), _p, ctypes.POINTER(ctypes.c_float)]
+    lib.mac_bench_decode_timed.restype = ctypes.c_int
     lib.mac_bench_last_error.restype = ctypes.c_char_p
+    return lib
+
+
+@lru_cache(maxsize=1)
+def load_noalloc_library(path: str | None = None) -> ctypes.CDLL:
+    """Open libmac_noalloc.so (the decode step with its workspaces in a static
+    device array; no reference counterpart).  It links against libmac_hip.so
+    in the same directory."""
+    path = path or NOALLOC_LIB_PATH
+    if not os.path.exists(path):
+        raise RuntimeError(f"no-allocation library not found at {path}; build with __graft_entry__.build()")
+    load_library()  # the decode library it links against, with its ABI version checked
+    lib = ctypes.CDLL(path)
+    lib.mac_persistent_decode_bf16_noalloc.argtypes = [ctypes.POINTER(MacDecodeArgs), _p]
+    lib.mac_persistent_decode_bf16_noalloc.restype = ctypes.c_int
+    lib.mac_noalloc_last_error.restype = ctypes.c_char_p
     return lib
 
 
@@ -220,6 +233,10 @@ def _env_flag(name: str, default: int) -> int:
         return 0
 
 
+# MacDecodeArgs fields of the 30 workspace tensors (prefixes)
+_WORKSPACE_FIELDS = ("match_", "head_", "group_", "complete_task_", "task_counts", "partial_")
+
+
 def _ptr(t: torch.Tensor | None) -> int | None:
     if t is None or t.numel() == 0:
         return None
@@ -250,25 +267,32 @@ class PersistentDecodeExtension:
         _raise_on(self._lib, rc)
 
     def mac_persistent_decode_bf16_noalloc(self, *args) -> None:
-        """The same step through the library's no-allocation entry point
-        (no reference counterpart): the 68 arguments are checked as above,
-        the workspace tensors are then ignored (the library's static device
-        array holds them) and the decisions are not returned.  At most 4096
-        query heads per step and 2048 ring slots."""
-        a, device = self._marshal(*args)
+        """The same step through libmac_noalloc.so's entry point (no reference
+        counterpart): the same 68 positional arguments, but the 30 workspace
+        tensors and phase_cycles may be None -- they are neither checked nor
+        used (the library's static device array holds the workspaces), and
+        the decisions are not returned.  At most 4096 query heads per step
+        and 2048 ring slots."""
+        a, device = self._marshal(*args, use_workspaces=False)
+        lib = load_noalloc_library()
         with torch.cuda.device(device):
-            rc = self._lib.mac_persistent_decode_bf16_noalloc(ctypes.byref(a), _stream(device))
-        _raise_on(self._lib, rc)
+            rc = lib.mac_persistent_decode_bf16_noalloc(ctypes.byref(a), _stream(device))
+        if rc != 0:
+            msg = lib.mac_noalloc_last_error().decode(errors="replace")
+            raise RuntimeError(msg or f"MAC HIP call failed with code {rc}")
 
     def phase_times_ms(self, *args) -> tuple[float, float, float]:
-        """Runs the same step eagerly with HIP events around each kernel and
-        returns (match_decide, span_attention, merge_write) milliseconds.
+        """Runs the same step eagerly through libmac_bench.so's timed copy of
+        the decode step (HIP events around each kernel) and returns
+        (decision kernel, span_attention, merge_write) milliseconds.
         Synchronises; profiling only (no reference counterpart)."""
         a, device = self._marshal(*args)
+        lib = load_bench_library()
         ms = (ctypes.c_float * 3)()
         with torch.cuda.device(device):
-            rc = self._lib.mac_persistent_decode_bf16_timed(ctypes.byref(a), _stream(device), ms)
-        _raise_on(self._lib, rc)
+            rc = lib.mac_bench_decode_timed(ctypes.byref(a), _stream(device), ms)
+        if rc != 0:
+            raise RuntimeError(lib.mac_bench_last_error().decode(errors="replace") or f"code {rc}")
         return float(ms[0]), float(ms[1]), float(ms[2])
 
     def _marshal(
@@ -289,9 +313,12 @@ class PersistentDecodeExtension:
         bench_hit_rate, bench_hit_rate_std, bench_skip_ratio, bench_skip_ratio_std,
         bench_match_lag_mean, bench_match_lag_std, bench_seed, bench_miss_mask, bench_layer_id,
         query_post_cache, mac_cache_ready, mac_cache_epoch, mac_request_epoch,
+        use_workspaces: bool = True,
     ) -> tuple[MacDecodeArgs, torch.device]:
         """Checks the 68 arguments like the reference launcher
-        (mac_decode_persistent.cu:5031-5175) and fills the C argument block."""
+        (mac_decode_persistent.cu:5031-5175) and fills the C argument block.
+        With use_workspaces False (the no-allocation entry point) the
+        workspace tensors and phase_cycles are neither checked nor passed."""
         bf16, f32, i32, i64 = torch.bfloat16, torch.float32, torch.int32, torch.int64
         _check_tensor(q_post, "q_post", bf16, 3)
         _check_tensor(q_pre, "q_pre", bf16, 3)
@@ -314,9 +341,71 @@ class PersistentDecodeExtension:
         _check(optional_lse.is_contiguous(), "optional_lse must be contiguous")
         _check(optional_lse.numel() == 0 or optional_lse.dtype == f32,
                "optional_lse must be empty or float32")
-        _check(phase_cycles.is_cuda, "phase_cycles must be CUDA")
-        _check(phase_cycles.dtype == i64, "phase_cycles must be int64")
-        _check(phase_cycles.numel() >= 6, "phase_cycles must have at least 6 elements")
+        if use_workspaces or phase_cycles is not None:
+            _check(phase_cycles.is_cuda, "phase_cycles must be CUDA")
+            _check(phase_cycles.dtype == i64, "phase_cycles must be int64")
+            _check(phase_cycles.numel() >= 6, "phase_cycles must have at least 6 elements")
+        _check_tensor(q_post, "q_post", bf16, 3)  # (the shape checks below read it)
+        N, Hq, D = (int(x) for x in q_post.shape)
+        Hkv = int(k_buffer.shape[1])
+        if use_workspaces:
+            self._check_workspaces(
+                N, Hq, Hkv, query_cache, max_context, tile_tokens, match_tile_slots, semantic_pos_ahead,
+                bench_mode, match_dist, match_pos, match_slot, head_hit, head_match_slot,
+                head_match_pos, head_prefix_end, head_rect_start, head_new_end, group_rect_begin,
+                group_rect_end, group_rect_tiles, group_tail_begin, group_tail_end, group_tail_tiles,
+                group_mode, complete_task_go, complete_task_tile, tail_task_go, tail_task_tile,
+                hit_tail_task_ho, hit_tail_task_tile, task_counts, partial_rect_o, partial_rect_lse,
+                partial_rect_reduced_o, partial_rect_reduced_lse, partial_tail_o, partial_tail_lse)
+        else:
+            _check(int(bench_mode) in (0, 1, 2), "unsupported synthetic MAC bench mode")
+        _check(D == _HEAD_DIM, "persistent decode v1 supports D=128 only")
+        _check(tuple(q_pre.shape) == tuple(q_post.shape), "q_pre/q_post shape mismatch")
+        _check(tuple(v_buffer.shape) == tuple(k_buffer.shape), "k/v shape mismatch")
+        _check(int(k_buffer.shape[2]) == D, "k/v head_dim mismatch")
+        _check(Hkv > 0 and Hq % Hkv == 0, "Hq must be divisible by Hkv")
+        G = Hq // Hkv
+        _check(0 < G <= _MAX_GROUP, "unsupported GQA group size")
+        _check(req_ids.shape[0] >= N and past_lens.shape[0] >= N and out_cache_loc.shape[0] >= N,
+               "batch metadata too small")
+        _check(tuple(out.shape) == tuple(q_post.shape), "out shape mismatch")
+        _check(optional_lse.numel() == 0 or optional_lse.numel() >= N * Hq,
+               "optional_lse too small")
+        R, M = int(query_cache.shape[0]), int(query_cache.shape[1])
+        _check(query_cache.shape[2] == Hq and query_cache.shape[3] == D,
+               "query_cache shape mismatch")
+        _check(tuple(attn_cache.shape) == tuple(query_cache.shape), "attn_cache shape mismatch")
+        _check(tuple(lse_cache.shape) == (R, M, Hq), "lse_cache shape mismatch")
+        return self._fill(
+            N, Hq, Hkv, D, M, R, q_post, q_pre, k_buffer, v_buffer, req_to_token, req_ids, past_lens,
+            out_cache_loc, query_cache, attn_cache, lse_cache, out, optional_lse,
+            match_dist, match_pos, match_slot,
+            head_hit, head_match_slot, head_match_pos, head_prefix_end, head_rect_start, head_new_end,
+            group_rect_begin, group_rect_end, group_rect_tiles, group_tail_begin, group_tail_end,
+            group_tail_tiles, group_mode, complete_task_go, complete_task_tile, task_counts,
+            partial_rect_o, partial_rect_lse, phase_cycles,
+            max_context, tile_tokens, match_tile_slots, semantic_pos_ahead, front_sink_tokens,
+            gen_min_limit, lookback_right, candidate_mode, threshold, sm_scale, debug_enabled, bench_mode,
+            bench_hit_rate, bench_hit_rate_std, bench_skip_ratio, bench_skip_ratio_std,
+            bench_match_lag_mean, bench_match_lag_std, bench_seed, bench_miss_mask, bench_layer_id,
+            mac_cache_ready, mac_cache_epoch, mac_request_epoch, use_workspaces)
+
+    @staticmethod
+    def _check_workspaces(
+        N, Hq, Hkv, query_cache, max_context, tile_tokens, match_tile_slots, semantic_pos_ahead,
+        bench_mode, match_dist, match_pos, match_slot, head_hit, head_match_slot, head_match_pos,
+        head_prefix_end, head_rect_start, head_new_end, group_rect_begin, group_rect_end,
+        group_rect_tiles, group_tail_begin, group_tail_end, group_tail_tiles, group_mode,
+        complete_task_go, complete_task_tile, tail_task_go, tail_task_tile, hit_tail_task_ho,
+        hit_tail_task_tile, task_counts, partial_rect_o, partial_rect_lse, partial_rect_reduced_o,
+        partial_rect_reduced_lse, partial_tail_o, partial_tail_lse,
+    ) -> None:
+        """The reference launcher's workspace checks (mac_decode_persistent.cu:5090-5153),
+        plus the complete-task minimum this build's kernels need."""
+        f32, i32 = torch.float32, torch.int32
+        D = _HEAD_DIM
+        G = Hq // Hkv if Hkv > 0 and Hq % Hkv == 0 else 1
+        M = int(query_cache.shape[1])
         _check_tensor(match_dist, "match_dist", f32, 3)
         _check_tensor(match_pos, "match_pos", i32, 3)
         _check_tensor(match_slot, "match_slot", i32, 3)
@@ -344,25 +433,6 @@ class PersistentDecodeExtension:
                and partial_tail_o.dtype == partial_rect_o.dtype,
                "all partial output workspaces must use the same dtype")
 
-        N, Hq, D = (int(x) for x in q_post.shape)
-        Hkv = int(k_buffer.shape[1])
-        _check(D == _HEAD_DIM, "persistent decode v1 supports D=128 only")
-        _check(tuple(q_pre.shape) == tuple(q_post.shape), "q_pre/q_post shape mismatch")
-        _check(tuple(v_buffer.shape) == tuple(k_buffer.shape), "k/v shape mismatch")
-        _check(int(k_buffer.shape[2]) == D, "k/v head_dim mismatch")
-        _check(Hkv > 0 and Hq % Hkv == 0, "Hq must be divisible by Hkv")
-        G = Hq // Hkv
-        _check(0 < G <= _MAX_GROUP, "unsupported GQA group size")
-        _check(req_ids.shape[0] >= N and past_lens.shape[0] >= N and out_cache_loc.shape[0] >= N,
-               "batch metadata too small")
-        _check(tuple(out.shape) == tuple(q_post.shape), "out shape mismatch")
-        _check(optional_lse.numel() == 0 or optional_lse.numel() >= N * Hq,
-               "optional_lse too small")
-        R, M = int(query_cache.shape[0]), int(query_cache.shape[1])
-        _check(query_cache.shape[2] == Hq and query_cache.shape[3] == D,
-               "query_cache shape mismatch")
-        _check(tuple(attn_cache.shape) == tuple(query_cache.shape), "attn_cache shape mismatch")
-        _check(tuple(lse_cache.shape) == (R, M, Hq), "lse_cache shape mismatch")
         max_match_tiles = int(match_dist.shape[2])
         mtc = int(partial_rect_lse.shape[2])
         mtr = int(partial_rect_reduced_lse.shape[2])
@@ -411,7 +481,27 @@ class PersistentDecodeExtension:
                   group_tail_end, group_tail_tiles, group_mode):
             _check(t.shape[1] == Hkv, "group workspace must have Hkv columns")
         _check(ws_rows >= N, "head/group workspace has fewer rows than the batch")
+        # this build's kernels keep per-group flags and the task counter there
+        _check(complete_task_go.numel() >= 2 * N * Hkv + 6,
+               "complete task workspace too small: needs at least 2 * N * Hkv + 6 entries")
 
+    @staticmethod
+    def _fill(
+        N, Hq, Hkv, D, M, R, q_post, q_pre, k_buffer, v_buffer, req_to_token, req_ids, past_lens,
+        out_cache_loc, query_cache, attn_cache, lse_cache, out, optional_lse,
+        match_dist, match_pos, match_slot,
+        head_hit, head_match_slot, head_match_pos, head_prefix_end, head_rect_start, head_new_end,
+        group_rect_begin, group_rect_end, group_rect_tiles, group_tail_begin, group_tail_end,
+        group_tail_tiles, group_mode, complete_task_go, complete_task_tile, task_counts,
+        partial_rect_o, partial_rect_lse, phase_cycles,
+        max_context, tile_tokens, match_tile_slots, semantic_pos_ahead, front_sink_tokens,
+        gen_min_limit, lookback_right, candidate_mode, threshold, sm_scale, debug_enabled, bench_mode,
+        bench_hit_rate, bench_hit_rate_std, bench_skip_ratio, bench_skip_ratio_std,
+        bench_match_lag_mean, bench_match_lag_std, bench_seed, bench_miss_mask, bench_layer_id,
+        mac_cache_ready, mac_cache_epoch, mac_request_epoch, use_workspaces,
+    ) -> tuple[MacDecodeArgs, torch.device]:
+        """The readiness-gate checks and the C argument block."""
+        bf16, i64 = torch.bfloat16, torch.int64
         ready = epoch = req_epoch = None
         if mac_cache_ready is not None and mac_cache_ready.numel() > 0:
             _check(mac_cache_ready.is_cuda, "mac_cache_ready must be CUDA")
@@ -450,20 +540,25 @@ class PersistentDecodeExtension:
                         ("partial_o", partial_rect_o), ("partial_lse", partial_rect_lse),
                         ("cache_ready", ready), ("cache_epoch", epoch),
                         ("request_epoch", req_epoch)):
-            setattr(a, name, _ptr(t))
+            if use_workspaces or not name.startswith(_WORKSPACE_FIELDS):
+                setattr(a, name, _ptr(t))
         a.N, a.Hq, a.Hkv, a.D, a.M, a.R = N, Hq, Hkv, D, M, R
         a.pool_tokens = int(k_buffer.shape[0])
         a.req_to_token_rows = int(req_to_token.shape[0])
         a.req_to_token_stride = int(req_to_token.shape[1])
         a.out_cache_loc_is_i64 = 1 if out_cache_loc.dtype == i64 else 0
-        a.max_match_tiles = max_match_tiles
-        a.max_tiles_context = mtc
-        a.partial_o_is_bf16 = 1 if partial_rect_o.dtype == bf16 else 0
-        a.complete_task_len = int(complete_task_go.numel())
-        a.workspace_rows = ws_rows
+        if use_workspaces:
+            a.max_match_tiles = int(match_dist.shape[2])
+            a.max_tiles_context = int(partial_rect_lse.shape[2])
+            a.partial_o_is_bf16 = 1 if partial_rect_o.dtype == bf16 else 0
+            a.complete_task_len = int(complete_task_go.numel())
+            a.workspace_rows = min(int(t.shape[0]) for t in (
+                head_hit, head_match_slot, head_match_pos, head_prefix_end, head_rect_start,
+                head_new_end, group_rect_begin, group_rect_end, group_rect_tiles, group_tail_begin,
+                group_tail_end, group_tail_tiles, group_mode, match_dist, match_pos, match_slot))
         a.max_context = int(max_context)
-        a.tile_tokens = tile_tokens
-        a.match_tile_slots = match_tile_slots
+        a.tile_tokens = int(tile_tokens)
+        a.match_tile_slots = int(match_tile_slots)
         a.semantic_pos_ahead = int(semantic_pos_ahead)
         a.front_sink_tokens = int(front_sink_tokens)
         a.gen_min_limit = int(gen_min_limit)
@@ -484,8 +579,9 @@ class PersistentDecodeExtension:
         a.bench_layer_id = int(bench_layer_id)
         a.mixed_group_fallback = _env_flag("MAC_PERSISTENT_MIXED_GROUP_FALLBACK", 1)
         a.bench_exact_quota = _env_flag("MAC_BENCH_EXACT_QUOTA", 1)
-        a.phase_cycles = _ptr(phase_cycles)
-        a.phase_cycles_len = int(phase_cycles.numel())
+        if phase_cycles is not None:
+            a.phase_cycles = _ptr(phase_cycles)
+            a.phase_cycles_len = int(phase_cycles.numel())
         return a, q_post.device
 
 

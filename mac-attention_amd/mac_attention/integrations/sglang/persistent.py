@@ -415,7 +415,9 @@ def ensure_persistent_workspace(backend: Any, metadata: MacMetadata, config: Any
     for name in ("rect_begin", "rect_end", "rect_tiles", "tail_begin", "tail_end", "tail_tiles", "mode"):
         ws["group_" + name] = e(max_running, hkv)
     ws.update({
-        "complete_task_go": e(max_running * hq * tiles_ctx), "complete_task_tile": e(max_running * hq * tiles_ctx),
+        # the reference's size, at least the 2 N Hkv + 6 entries this build's kernels use
+        "complete_task_go": e(max(max_running * hq * tiles_ctx, 2 * max_running * hkv + 6)),
+        "complete_task_tile": e(max(max_running * hq * tiles_ctx, 2 * max_running * hkv + 6)),
         "tail_task_go": e(max_running * hkv * tiles_tail), "tail_task_tile": e(max_running * hkv * tiles_tail),
         "hit_tail_task_ho": e(max_running * hq * tiles_tail), "hit_tail_task_tile": e(max_running * hq * tiles_tail),
         "task_counts": e(9),

@@ -277,7 +277,8 @@ def workspace(torch, *, batch, hq, hkv, capacity, max_context, tile_tokens, matc
         *[e(batch, hq, dt=i32) for _ in range(6)],
         *[e(batch, hkv, dt=i32) for _ in range(6)],
         e(batch, hkv, dt=i32),
-        e(batch * hq * mtc, dt=i32), e(batch * hq * mtc, dt=i32),
+        e(max(batch * hq * mtc, 2 * batch * hkv + 6), dt=i32),
+        e(max(batch * hq * mtc, 2 * batch * hkv + 6), dt=i32),
         e(batch * hkv * mtt, dt=i32), e(batch * hkv * mtt, dt=i32),
         e(batch * hq * mtt, dt=i32), e(batch * hq * mtt, dt=i32),
         e(9, dt=i32),

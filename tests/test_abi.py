@@ -13,6 +13,7 @@ from helpers import REPO
 
 HEADER = os.path.join(REPO, "include", "mac_attention_amd.h")
 BENCH_HEADER = os.path.join(REPO, "include", "mac_bench.h")
+NOALLOC_HEADER = os.path.join(REPO, "include", "mac_noalloc.h")
 
 
 def _declared(header=HEADER, api="MAC_API"):
@@ -44,8 +45,10 @@ def test_library_exports_every_declared_symbol(bridge):
 
 
 def test_measurement_library_is_separate(bridge):
-    """The streaming-read helper lives in libmac_bench.so, not in the decode
-    library, and exports exactly what include/mac_bench.h declares."""
+    """The measurement helpers (streaming read, per-kernel timed decode step)
+    live in libmac_bench.so, not in the decode library, and it exports
+    exactly what include/mac_bench.h declares -- none of the decode
+    library's entry points, although it compiles the decode source too."""
     names = _declared(BENCH_HEADER, "MAC_BENCH_API")
     assert set(names) == set(bridge.BENCH_EXPORTED_SYMBOLS)
     lib = bridge.load_bench_library()
@@ -55,6 +58,37 @@ def test_measurement_library_is_separate(bridge):
                         text=True, check=True).stdout
     assert {l.split()[-1] for l in nm.splitlines() if " T " in l} == set(names)
     assert not set(names) & set(bridge.EXPORTED_SYMBOLS)
+
+
+def test_noalloc_library_is_separate(bridge):
+    """The no-allocation entry point and its static device array live in
+    libmac_noalloc.so (so only processes that load it reserve the array),
+    which exports exactly what include/mac_noalloc.h declares and links
+    against libmac_hip.so in its own directory."""
+    names = _declared(NOALLOC_HEADER)
+    assert set(names) == set(bridge.NOALLOC_EXPORTED_SYMBOLS)
+    lib = bridge.load_noalloc_library()
+    for n in names:
+        assert hasattr(lib, n), n
+    nm = subprocess.run(["nm", "-D", "--defined-only", bridge.NOALLOC_LIB_PATH], capture_output=True,
+                        text=True, check=True).stdout
+    assert {l.split()[-1] for l in nm.splitlines() if " T " in l} == set(names)
+    assert not set(names) & set(bridge.EXPORTED_SYMBOLS)
+    needed = subprocess.run(["readelf", "-d", bridge.NOALLOC_LIB_PATH], capture_output=True, text=True,
+                            check=True).stdout
+    assert "libmac_hip.so" in needed and "$ORIGIN" in needed
+    # no device array in the decode library
+    syms = subprocess.run(["nm", bridge.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    assert "scratch" not in syms
+    a = bridge.MacDecodeArgs()
+    a.struct_size = ctypes.sizeof(a)
+    a.abi_version = bridge.ABI_VERSION
+    a.N, a.Hq, a.Hkv, a.D, a.M, a.R, a.max_context = 200, 32, 8, 128, 32, 200, 1024
+    assert lib.mac_persistent_decode_bf16_noalloc(ctypes.byref(a), None) == 1
+    assert b"at most 4096 query heads" in lib.mac_noalloc_last_error()
+    a.N, a.M = 4, 4096
+    assert lib.mac_persistent_decode_bf16_noalloc(ctypes.byref(a), None) == 1
+    assert b"rings of at most 2048" in lib.mac_noalloc_last_error()
 
 
 @pytest.mark.parametrize("struct", ["MacDecodeArgs", "MacWindowAttentionArgs", "MacRectifyArgs"])

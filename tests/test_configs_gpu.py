@@ -221,48 +221,86 @@ def config3(request):
     torch.cuda.empty_cache()
 
 
-@pytest.fixture
-def pinned_fusion(monkeypatch):
-    """Tests that compare two decode calls bit for bit pin the short-group
-    rule: by default it follows the previous call's counts, and the fused and
-    split paths agree only to rounding."""
-    monkeypatch.setenv("MAC_AMD_FUSE_POLICY", "always")
-
-
 def _restore(dev, pristine):
     for k in RING_ROWS:
         dev[k].copy_(pristine[k])
 
 
-@pytest.mark.parametrize("hit", [0.0, 0.25, 0.5, 0.75, 0.9, 1.0])
-def test_config3_hit_sweep(ext, config3, hit, pinned_fusion):
-    """Every hit ratio bench.py times at the headline shape, GQA-4 and GQA-8:
-    ring copies planted where the bench's synthetic_head override puts its
-    hits, decided by the real ring scan and checked against the oracle on two
-    requests; then the override itself (bench_mode 1, what the bench runs)
-    must make the same decisions for all 64 requests and give the same
-    output bit for bit."""
-    hkv, dev, pristine = config3
-    S = 256
+def _expected_fused(ws, n_groups, hkv, fuse_tokens=1024, narrow_tokens=8 << 20):
+    """The short-group rule restated (mac_decode.hip step_fuse_rule) from the
+    previous step's counts, which span_attention leaves in complete_task_go
+    [2 NG + 2 .. + 4]: per group, whether match_decide finishes it."""
+    go = _np(ws[16])
+    n_short, n_long, units = (int(x) for x in go[2 * n_groups + 2:2 * n_groups + 5])
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if n_short + n_long != n_groups or n_long == 0:
+        fuse = True
+    else:
+        fuse = units * 64 >= narrow_tokens and 2 * n_short > cus
+    sink = 0
+    tokens = sink + (_np(ws[10]) - _np(ws[9])) + (_np(ws[13]) - _np(ws[10]))
+    return (tokens <= fuse_tokens) & fuse
+
+
+def _bench_step(ext, dev, pristine, hit, S, max_context, ws=None):
+    """One step of what bench.py times at a sweep point (the synthetic_head
+    override, bench_mode 1, on the planted ring); the ring is restored first."""
     _restore(dev, pristine)
     syn.plant_synthetic_hits(torch, dev, hit_rate=hit, bench_mode=1, semantic_pos_ahead=S)
-    check = [0, 37]
-    print(f"config3 sweep hkv={hkv} hit={hit}", flush=True)
+    return _run(ext, dev, S=S, F=0, max_context=max_context, ws=ws,
+                bench=dict(bench_mode=1, bench_hit_rate=hit, bench_match_lag_mean=64.0))
+
+
+def _timed_path_point(ext, dev, pristine, hit, check, what, S=256, max_context=131072):
+    """The exact path bench.py times at one sweep point, with its default
+    short-group rule in its steady state: a warm-up step on the workspace
+    leaves the counts the rule reads, as the bench's warm-up replays do.
+    Then (1) the real ring scan (copies planted where the override puts its
+    hits) on that workspace, checked against the oracle on `check` requests,
+    with the rule's choice asserted per group; (2) the override itself on the
+    same workspace (what the bench replays) must make the same decisions,
+    finish the same groups in match_decide and give the same bits for all
+    requests."""
+    n, hq, _ = dev["q_post"].shape
+    hkv = dev["k"].shape[1]
+    _, _, ws = _bench_step(ext, dev, pristine, hit, S, max_context)  # warm-up (counts for the rule)
+    torch.cuda.synchronize()
+    expected = _expected_fused(ws, n * hkv, hkv)
+    _restore(dev, pristine)
+    syn.plant_synthetic_hits(torch, dev, hit_rate=hit, bench_mode=1, semantic_pos_ahead=S)
     sub = host_subset(torch, dev, check, semantic_pos_ahead=S)
     res = oracle_run(sub)
-    out, out_lse, ws = _run(ext, dev, S=S, F=0, max_context=131072)
+    out, out_lse, ws = _run(ext, dev, S=S, F=0, max_context=max_context, ws=ws)
     torch.cuda.synchronize()
-    _check_subset(dev, out, out_lse, ws, sub, res, check, f"config3 hkv {hkv} hit {hit}")
-    assert int(ws[3].sum()) == round(hit * 64 * 32)
+    _check_subset(dev, out, out_lse, ws, sub, res, check, what)
+    assert int(ws[3].sum()) == round(hit * n * hq)
+    ng = n * hkv
+    fused = _np(ws[16])[ng:2 * ng].reshape(n, hkv) != 0
+    np.testing.assert_array_equal(fused, expected, err_msg=f"{what}: groups finished in match_decide")
+    print(f"{what}: {int(fused.sum())}/{ng} groups finished in match_decide", flush=True)
     scan = {i: ws[i].clone() for i in (3, 5, 9, 10, 13, 15)}
-    scan_out = out.clone()
-    _restore(dev, pristine)
-    out2, _, ws2 = _run(ext, dev, S=S, F=0, max_context=131072,
-                        bench=dict(bench_mode=1, bench_hit_rate=hit, bench_match_lag_mean=64.0))
+    scan_out, scan_lse = out.clone(), out_lse.clone()
+    scan_ring = {k: dev[k].clone() for k in RING_ROWS}
+    out2, lse2, ws2 = _bench_step(ext, dev, pristine, hit, S, max_context, ws=ws)
     torch.cuda.synchronize()
     for i, t in scan.items():
         assert torch.equal(ws2[i], t), f"workspace [{i}] of the override differs from the scan's"
-    assert torch.equal(out2, scan_out)
+    np.testing.assert_array_equal(_np(ws2[16])[ng:2 * ng].reshape(n, hkv) != 0, fused)
+    assert torch.equal(out2, scan_out) and torch.equal(lse2.view(torch.int32), scan_lse.view(torch.int32))
+    for k in RING_ROWS:
+        assert torch.equal(dev[k].view(torch.int16 if dev[k].dtype == torch.bfloat16 else torch.int32),
+                           scan_ring[k].view(torch.int16 if dev[k].dtype == torch.bfloat16 else torch.int32)), k
+
+
+@pytest.mark.parametrize("hit", [0.0, 0.25, 0.5, 0.75, 0.8, 0.9, 1.0])
+def test_config3_hit_sweep(ext, config3, hit):
+    """Every hit ratio bench.py times at the headline shape, GQA-4 and GQA-8,
+    through the path the bench times (its default short-group rule in steady
+    state, see _timed_path_point): the real scan against the oracle on two
+    requests, then the override bit for bit on all 64."""
+    hkv, dev, pristine = config3
+    print(f"config3 sweep hkv={hkv} hit={hit}", flush=True)
+    _timed_path_point(ext, dev, pristine, hit, [0, 37], f"config3 hkv {hkv} hit {hit}")
 
 
 @pytest.fixture(scope="module", params=[8, 4], ids=["gqa4", "gqa8"])
@@ -277,30 +315,15 @@ def ring2048(request):
     torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("hit", [0.0, 1.0])
-def test_reference_shape_hit_ends(ext, ring2048, hit, pinned_fusion):
-    """The ends of bench.py's reference_shape sweep (ring 2048: the
-    range-split, probe-pruned scan): scan decisions against the oracle on two
-    requests, and the override's decisions equal to the scan's."""
+@pytest.mark.parametrize("hit", [0.0, 0.5, 0.8, 0.9, 1.0])
+def test_reference_shape_hit_sweep(ext, ring2048, hit):
+    """Every hit ratio of bench.py's reference_shape leg (ring 2048: the
+    range-split, probe-pruned scan) through the path the bench times: scan
+    decisions and values against the oracle on two requests, the override's
+    decisions, placement and bits equal to the scan's."""
     hkv, dev, pristine = ring2048
-    S = 256
-    _restore(dev, pristine)
-    syn.plant_synthetic_hits(torch, dev, hit_rate=hit, bench_mode=1, semantic_pos_ahead=S)
-    check = [5, 60]
     print(f"ring2048 hkv={hkv} hit={hit}", flush=True)
-    sub = host_subset(torch, dev, check, semantic_pos_ahead=S)
-    res = oracle_run(sub)
-    out, out_lse, ws = _run(ext, dev, S=S, F=0, max_context=131072)
-    torch.cuda.synchronize()
-    _check_subset(dev, out, out_lse, ws, sub, res, check, f"ring2048 hkv {hkv} hit {hit}")
-    assert int(ws[3].sum()) == round(hit * 64 * 32)
-    scan = {i: ws[i].clone() for i in (3, 5, 9, 15)}
-    _restore(dev, pristine)
-    _, _, ws2 = _run(ext, dev, S=S, F=0, max_context=131072,
-                     bench=dict(bench_mode=1, bench_hit_rate=hit, bench_match_lag_mean=64.0))
-    torch.cuda.synchronize()
-    for i, t in scan.items():
-        assert torch.equal(ws2[i], t), f"workspace [{i}] of the override differs from the scan's"
+    _timed_path_point(ext, dev, pristine, hit, [5, 60], f"ring2048 hkv {hkv} hit {hit}")
 
 
 # ------------------------------------------------------------- config 4 ----
@@ -376,7 +399,7 @@ def test_config4_ragged_serving_mix(ext, cache_ext):
     _check_subset(dev, out2, out_lse2, ws2, sub2, res2, check2, "config4 step2")
 
 
-def test_config4_graph_replays_follow_host_flips(ext, cache_ext, pinned_fusion):
+def test_config4_graph_replays_follow_host_flips(ext, cache_ext):
     """Config 4's serving mix captured once in a hipGraph and replayed while
     the host changes what the readiness gate sees between replays
     (DECODE:208-230, the in-graph demotion the serving path relies on):
@@ -569,7 +592,7 @@ def test_near_threshold_decisions_are_logged(ext):
 # ------------------------------------------------------------ hipGraph ----
 
 
-def test_graph_replay_matches_eager(ext, pinned_fusion):
+def test_graph_replay_matches_eager(ext):
     """The decode step captured in a graph and replayed (with eager work and
     synchronisation between replays) gives the eager result every time,
     including the ring-row writes and the readiness gate."""

@@ -53,11 +53,13 @@ def _check_against_oracle(case, dev, out, out_lse, ws, res, tol=1e-2, what=""):
     assert_close(lc, res.lse_cache, 3e-2, f"{what} lse_cache")
 
 
-# Groups of at most MAC_AMD_FUSE_TOKENS tokens may be finished inside
-# match_decide (attention, merge and ring row in one workgroup).  "fused":
-# every such group is (MAC_AMD_FUSE_POLICY=always); "split": none is, every
-# group goes through span_attention and merge_write; "auto": the default
-# step-wide rule decides.  All must give the oracle's results.
+# Groups of at most MAC_AMD_FUSE_TOKENS tokens are short: one computation
+# (short_group) finishes each of them, inside match_decide or as one task of
+# span_attention.  "fused": match_decide finishes every short group
+# (MAC_AMD_FUSE_POLICY=always); "split": no group is short, every group goes
+# through span_attention's pieces and merge_write; "auto": the default
+# step-wide rule places the short groups.  All must give the oracle's
+# results; "fused" and "auto" give the same bits.
 FUSE = {"fused": ("always", None), "split": (None, "0"), "auto": (None, None)}
 
 
@@ -180,32 +182,72 @@ def test_random_vs_oracle(cfg, fuse, ext, monkeypatch):
     _check_against_oracle(c, dev, out, out_lse, ws, res, what=str(cfg))
 
 
-@pytest.mark.parametrize("fuse", ["fused", "split"])
+def _bits(dev, out, out_lse):
+    return [out.view(torch.int16).clone(), out_lse.view(torch.int32).clone(),
+            dev["attn_cache"].view(torch.int16).clone(), dev["lse_cache"].view(torch.int32).clone(),
+            dev["query_cache"].view(torch.int16).clone()]
+
+
 @pytest.mark.parametrize("hkv", [8, 4])
-def test_decode_is_deterministic(hkv, fuse, ext, monkeypatch):
-    """A step on the same inputs gives the same bits on every call when the
-    short-group choice does not depend on history (fused: every short group
-    in match_decide; split: none): task order and timing never reach the
-    arithmetic.  Mixed hits, misses and long groups, 64 groups or fewer per
-    step (the eight-wave match_decide) and more (four waves)."""
-    _set_fuse(monkeypatch, fuse)
+def test_decode_is_deterministic(hkv, ext, monkeypatch):
+    """A step's results depend on its inputs only, with the default
+    short-group rule: after a fresh workspace, after a step of another shape
+    on the same workspace, after steps with other hits (which move the short
+    groups between match_decide and span_attention), with every short group
+    pinned to match_decide, and with the four- and eight-wave decision
+    kernels, the outputs and ring rows are the same bits.  Mixed hits,
+    misses and long groups; 64 groups or fewer per step (the eight-wave
+    match_decide) and more (four waves)."""
+    _set_fuse(monkeypatch, "auto")
     batch = 8 if hkv == 8 else 80
     rng = np.random.default_rng(31)
     kv_lens = rng.integers(300, 6000, batch).tolist()
-    print(f"decode determinism: Hkv={hkv} B={batch} fuse={fuse}", flush=True)
-    c = syn.random_case(batch=batch, hq=32, hkv=hkv, kv_lens=kv_lens, capacity=32, semantic_pos_ahead=64,
-                        front_sink_tokens=8, hit_rate=0.7, match_lag=16, seed=31)
-    runs = []
-    for _ in range(3):
-        dev = syn.to_device(torch, c)
-        out, out_lse, ws = syn.run_decode(torch, ext, dev, c, max_context=max(kv_lens) + 8, tile_tokens=16,
-                                          match_tile_slots=8)
+    max_context = 20008
+    print(f"decode determinism: Hkv={hkv} B={batch}", flush=True)
+
+    def case(hit, seed, lens=kv_lens):
+        return syn.random_case(batch=len(lens), hq=32, hkv=hkv, kv_lens=lens, capacity=32, semantic_pos_ahead=64,
+                               front_sink_tokens=8, hit_rate=hit, match_lag=16, seed=seed)
+
+    c = case(0.7, 31)
+    ws = syn.workspace(torch, batch=batch, hq=32, hkv=hkv, capacity=32, max_context=max_context, tile_tokens=64,
+                       match_tile_slots=8, semantic_pos_ahead=64, front_sink_tokens=8, device="cuda")
+    ng = batch * hkv
+
+    def step(cc, ws_=ws):
+        dev = syn.to_device(torch, cc)
+        out, out_lse, w = syn.run_decode(torch, ext, dev, cc, max_context=max_context, tile_tokens=64,
+                                         match_tile_slots=8, ws=ws_)
         torch.cuda.synchronize()
-        runs.append([out.view(torch.int16).clone(), out_lse.view(torch.int32).clone(),
-                     dev["attn_cache"].view(torch.int16).clone(), dev["lse_cache"].view(torch.int32).clone()])
-    for r in runs[1:]:
-        for a, b in zip(r, runs[0]):
-            assert torch.equal(a, b)
+        return _bits(dev, out, out_lse), _np(w[16])[ng:2 * ng].copy()
+
+    ws[16].zero_()  # no history
+    ref, placed_first = step(c)
+    runs = {"no history": ref}
+    runs["repeat"], placed_repeat = step(c)
+    step(case(0.7, 31, [40] * (batch // 2)))  # a smaller batch on the same workspace
+    runs["after another shape"], _ = step(c)
+    step(case(0.0, 32, [20000] * batch))  # all long: the next step leaves its short groups to span_attention
+    runs["after long steps"], placed_after_long = step(c)
+    step(case(1.0, 33))
+    runs["after all-hit steps"], _ = step(c)
+    _set_fuse(monkeypatch, "fused")
+    runs["all in match_decide"], placed_fused = step(c)
+    monkeypatch.setenv("MAC_AMD_MATCH_WAVES", "4")
+    runs["four-wave decisions"], _ = step(c)
+    monkeypatch.delenv("MAC_AMD_MATCH_WAVES")
+    # the placements differ (so both places ran short groups) ...
+    assert placed_fused.sum() > 0 and placed_after_long.sum() < placed_fused.sum(), \
+        (placed_fused.sum(), placed_after_long.sum())
+    # ... and the bits do not
+    for name, r in runs.items():
+        for i, (a, b) in enumerate(zip(r, ref)):
+            assert torch.equal(a, b), f"{name}: tensor {i} differs from the first step's"
+    # and they are the oracle's
+    dev = syn.to_device(torch, c)
+    out, out_lse, w = syn.run_decode(torch, ext, dev, c, max_context=max_context, tile_tokens=64, match_tile_slots=8)
+    torch.cuda.synchronize()
+    _check_against_oracle(c, dev, out, out_lse, w, oracle_run(c), what=f"determinism Hkv={hkv}")
 
 
 @pytest.mark.parametrize("case", [f.__name__ for f in kat_cases.ALL + golden_cases.LOADERS]
