@@ -17,7 +17,10 @@ Targets, by group:
     Qwen classes are optional);
   * FlashInfer backend: settings at construction, the ring marks kept on the
     backend (init_forward_metadata), the ring update after each prefill
-    chunk (forward_extend) and the fused MAC decode step (forward_decode).
+    chunk (forward_extend) and the fused MAC decode step (forward_decode);
+  * the ROCm backends (AiterAttnBackend, TritonAttnBackend; optional): the
+    same four targets, with the ring update computing the kept rows' full
+    prefill state itself, since these backends return no lse.
 Profiling-only and CUDA-graph-trace hooks of the reference are not part of
 this build, nor its decode-graph metadata skipping and the wait for
 side-stream ring updates before a graph replay: the ring update here runs
@@ -46,6 +49,12 @@ _MODEL_CLASSES = (
     ("sglang.srt.models.qwen3_moe", "Qwen3MoeModel", True),
 )
 _FLASHINFER = "sglang.srt.layers.attention.flashinfer_backend:FlashInferAttnBackend"
+# the attention backends SGLang runs on ROCm (optional: an SGLang build has
+# the ones its platform supports)
+_ROCM_BACKENDS = (
+    "sglang.srt.layers.attention.aiter_backend:AiterAttnBackend",
+    "sglang.srt.layers.attention.triton_backend:TritonAttnBackend",
+)
 
 
 @dataclass(frozen=True)
@@ -86,6 +95,13 @@ def iter_hook_specs() -> Iterable[HookSpec]:
                    "around")
     yield HookSpec(f"{_FLASHINFER}.forward_extend", model_hooks.flashinfer_forward_extend_around, "around")
     yield HookSpec(f"{_FLASHINFER}.forward_decode", flashinfer_forward_decode_around, "around")
+
+    for backend in _ROCM_BACKENDS:
+        yield HookSpec(f"{backend}.__init__", model_hooks.flashinfer_backend_init_after, "after", True)
+        yield HookSpec(f"{backend}.init_forward_metadata", model_hooks.flashinfer_init_forward_metadata_around,
+                       "around", True)
+        yield HookSpec(f"{backend}.forward_extend", model_hooks.rocm_forward_extend_around, "around", True)
+        yield HookSpec(f"{backend}.forward_decode", flashinfer_forward_decode_around, "around", True)
 
 
 def _resolve_target(target: str) -> tuple[Any, str]:

@@ -325,3 +325,144 @@ def flashinfer_forward_extend_around(original_fn: Any, self: Any, q: torch.Tenso
     lse = lse_log2 * _LN2  # FlashInfer returns log2; the ring stores natural-log lse
     update_rings_after_prefill(self, forward_batch, config, meta, q_input, k_buffer, v_buffer, o, lse, layer)
     return o.view(-1, layer.tp_q_head_num * layer.head_dim)
+
+
+# ----------------------------------------------- ROCm attention backends ----
+#
+# SGLang on ROCm serves attention with AiterAttnBackend (when aiter is
+# installed) or TritonAttnBackend, not FlashInfer.  The hooks below attach
+# the same MAC path to them: construction and init_forward_metadata as for
+# FlashInfer (backend_init_after, flashinfer_init_forward_metadata_around are
+# backend-agnostic), the fused MAC step on decode
+# (persistent.flashinfer_forward_decode_around, also backend-agnostic), and
+# on extend the backend's own prefill attention followed by the ring update.
+# These backends return no lse, so the full prefill state (o, lse) of the
+# rows the ring keeps -- at most M per request -- comes from this build's
+# window-attention kernel with no window (causal attention over [0, pos]),
+# the role FlashInfer's forward_return_lse plays in flashinfer_hooks.py:2847-3010.
+
+
+def _req_to_token(backend: Any, forward_batch: Any) -> Optional[torch.Tensor]:
+    """The request-to-token table: FlashInfer keeps it on its index updaters,
+    the Triton and aiter backends as ``req_to_token``, SGLang's forward batch
+    on its ``req_to_token_pool``."""
+    for owner in (getattr(backend, "indices_updater_prefill", None), getattr(backend, "indices_updater_decode", None),
+                  backend, getattr(forward_batch, "req_to_token_pool", None)):
+        t = getattr(owner, "req_to_token", None) if owner is not None else None
+        if torch.is_tensor(t):
+            return t
+    return None
+
+
+def _ring_rows(forward_batch: Any, b: int, total_q: int, capacity: int):
+    """The chunk rows the ring keeps: the scheduler's marked suffix of each
+    request (every row without marks), cut to its last ``capacity`` rows
+    (mac_prefill_update_cache keeps no more, PREFILL:201-269).  Returns the
+    plan (None without marks) and per kept segment (batch row, first chunk
+    row, absolute position of that row, rows, request kv length), or None
+    when the chunk's lengths are not on the host."""
+    from .prefill_suffix import PrefillSuffixSegment
+
+    plan = build_prefill_suffix_plan(forward_batch, b, total_q)
+    if plan is not None:
+        segs = list(plan.segments)
+    else:
+        ext = _host_ints(getattr(forward_batch, "extend_seq_lens_cpu", None), b)
+        pre = _host_ints(getattr(forward_batch, "extend_prefix_lens_cpu", None), b) or [0] * b
+        if ext is None or sum(ext) != total_q:
+            return plan, None
+        segs, q_base, kv_base = [], 0, 0
+        for i in range(b):
+            if ext[i] > 0:
+                segs.append(PrefillSuffixSegment(i, q_base, pre[i], ext[i], kv_base, pre[i] + ext[i]))
+            q_base += ext[i]
+            kv_base += pre[i] + ext[i]
+    kept = []
+    for s in segs:
+        n = min(s.length, capacity)
+        skip = s.length - n
+        kept.append((s.batch_index, s.source_start + skip, s.update_start + skip, n, s.kv_len))
+    return plan, kept
+
+
+def _src_rows(meta: Any, plan: Any, kept: list, rows: int) -> Optional[list[int]]:
+    """Indices into the preserved pre-RoPE rows of the kept chunk rows, or
+    None when they were not kept (persistent.preserve_q_before_rope keeps
+    every row, the plan's rows compacted in plan order, or a tail)."""
+    src = meta.cur_q_before_rope
+    if src is None:
+        return None
+    idx = []
+    if not meta.cur_q_before_rope_compacted:
+        for _, first, _, n, _ in kept:
+            idx.extend(range(first, first + n))
+    elif plan is not None and int(src.shape[0]) == int(plan.total_len):
+        where, off = {}, 0
+        for s in plan.segments:
+            where[s.batch_index] = (s.source_start, off)
+            off += s.length
+        for bi, first, _, n, _ in kept:
+            start, o = where[bi]
+            idx.extend(range(o + first - start, o + first - start + n))
+    else:  # a preserved tail of the chunk
+        base = int(meta.cur_q_before_rope_local_start)
+        for _, first, _, n, _ in kept:
+            if first < base:
+                return None
+            idx.extend(range(first - base, first - base + n))
+    return idx if all(0 <= i < int(src.shape[0]) for i in idx) else None
+
+
+def update_rings_from_own_prefill(backend: Any, forward_batch: Any, config: Any, meta: Any, q_input: torch.Tensor,
+                                  k_buffer: torch.Tensor, v_buffer: torch.Tensor, layer: Any) -> None:
+    """Ring update after a prefill chunk whose attention backend returned no
+    lse: the kept rows' full prefill state from the window-attention kernel
+    (no window), then the fused rectification (persistent.offload_prefill_cache)
+    and the ready marks."""
+    b = int(forward_batch.batch_size)
+    dev = q_input.device
+    req_ids = meta.req_ids[:b]
+    capacity = int(meta.unified_query_cache.shape[1])
+    plan, kept = _ring_rows(forward_batch, b, int(q_input.shape[0]), capacity)
+    if plan is not None and plan.total_len <= 0:
+        return  # the scheduler kept no row of this chunk
+    r2t = _req_to_token(backend, forward_batch)
+    src_idx = _src_rows(meta, plan, kept, int(q_input.shape[0])) if kept is not None else None
+    if kept is None or not kept or r2t is None or src_idx is None:
+        persistent.invalidate_persistent_ready(meta, req_ids)
+        return
+    reqs = meta.req_ids_host or [int(x) for x in forward_batch.req_pool_indices[:b].tolist()]
+    i32 = dict(dtype=torch.int32, device=dev)
+    rows = torch.tensor([r for _, first, _, n, _ in kept for r in range(first, first + n)], dtype=torch.long,
+                        device=dev)
+    qo = torch.tensor([0] + list(_cumsum(n for _, _, _, n, _ in kept)), **i32)
+    kv_indptr = torch.tensor([0] + list(_cumsum(kv for *_, kv in kept)), **i32)
+    kv_indices = torch.cat([r2t[reqs[bi], :kv] for bi, _, _, _, kv in kept]).to(torch.int32).contiguous()
+    ids = req_ids.index_select(0, torch.tensor([bi for bi, *_ in kept], dtype=torch.long, device=dev)).contiguous()
+    prefix = torch.tensor([pos for _, _, pos, _, _ in kept], **i32)
+    q_rows = q_input.index_select(0, rows).contiguous()
+    o_full, lse_full = meta.rect_ext.window_attention_return_lse(q_rows, k_buffer, v_buffer, qo, kv_indptr,
+                                                                 kv_indices, -1, float(layer.scaling))
+    meta.cur_q_before_rope = meta.cur_q_before_rope.index_select(
+        0, torch.tensor(src_idx, dtype=torch.long, device=dev)).contiguous()
+    meta.cur_q_before_rope_compacted = True
+    persistent.offload_prefill_cache(meta, config, q_post=q_rows, o_full=o_full, lse_full=lse_full,
+                                     k_buffer=k_buffer, v_buffer=v_buffer, qo_indptr=qo, kv_indptr=kv_indptr,
+                                     kv_indices=kv_indices, req_ids=ids, prefix_lens=prefix,
+                                     sm_scale=float(layer.scaling))
+
+
+def rocm_forward_extend_around(original_fn: Any, self: Any, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                               layer: Any, forward_batch: Any, save_kv_cache: bool = True, **kwargs: Any) -> Any:
+    """Around-hook of AiterAttnBackend / TritonAttnBackend.forward_extend: the
+    backend's own prefill attention (its output is the layer's, and it writes
+    the chunk's K/V), then the ring update of the rows the ring keeps."""
+    config = getattr(layer, "mac_config", None) or getattr(self, "mac_config", None) or get_mac_config()
+    out = original_fn(self, q, k, v, layer, forward_batch, save_kv_cache=save_kv_cache, **kwargs)
+    if not persistent.supports_mac_backend(self, layer, forward_batch, config):
+        return out
+    meta = layer.mac_metadata
+    q_input = q.contiguous().view(-1, layer.tp_q_head_num, layer.head_dim)
+    k_buffer, v_buffer = forward_batch.token_to_kv_pool.get_kv_buffer(layer.layer_id)
+    update_rings_from_own_prefill(self, forward_batch, config, meta, q_input, k_buffer, v_buffer, layer)
+    return out

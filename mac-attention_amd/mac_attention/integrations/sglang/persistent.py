@@ -493,7 +493,12 @@ def try_persistent_decode(backend: Any, forward_batch: Any, config: Any, metadat
         return None
     if getattr(layer, "k_scale_float", None) is not None or getattr(layer, "v_scale_float", None) is not None:
         return None
-    req_to_token = getattr(getattr(backend, "indices_updater_decode", None), "req_to_token", None)
+    req_to_token = None  # FlashInfer: on its decode index updater; Triton / aiter: on the backend
+    for owner in (getattr(backend, "indices_updater_decode", None), backend,
+                  getattr(forward_batch, "req_to_token_pool", None)):
+        req_to_token = getattr(owner, "req_to_token", None) if owner is not None else None
+        if torch.is_tensor(req_to_token):
+            break
     if not torch.is_tensor(req_to_token) or req_to_token.dtype != torch.int32 or not req_to_token.is_contiguous():
         return None
     req_ids = metadata.req_ids[:batch]
@@ -564,8 +569,9 @@ def flashinfer_forward_decode_around(original_fn: Any, self: Any, q: torch.Tenso
                                      v: torch.Tensor, layer: Any, forward_batch: Any,
                                      save_kv_cache: bool = True, **kwargs: Any) -> Any:
     """Around-hook of FlashInferAttnBackend.forward_decode
-    (flashinfer_hooks.py:2614-2735): write K/V, try the fused MAC step, else
-    invalidate the batch's rings and run the backend's own decode."""
+    (flashinfer_hooks.py:2614-2735), and of the ROCm backends'
+    (AiterAttnBackend, TritonAttnBackend): write K/V, try the fused MAC step,
+    else invalidate the batch's rings and run the backend's own decode."""
     from .config import get_mac_config
 
     config = getattr(layer, "mac_config", None) or getattr(self, "mac_config", None) or get_mac_config()

@@ -6,8 +6,12 @@ classes that have the attributes and call structure the hooks rely on:
 ServerArgs, ScheduleBatch, ForwardBatch, LlamaAttention (qkv projection,
 rotary embedding, RadixAttention, output projection), FlashInferAttnBackend
 (its own extend / decode are recorded so a test can tell whether the MAC
-path took over) and the scheduler-process launch sites.  The numeric parts
-(projections, RoPE, the paged prefill wrapper) are supplied by the GPU test.
+path took over), the ROCm backends TritonAttnBackend and AiterAttnBackend
+(their own extend writes the chunk's K/V and runs a prefill attention the
+test supplies, without lse; their own decode must not run) and the
+scheduler-process launch sites.  The numeric parts (projections, RoPE, the
+paged prefill wrapper, the ROCm backends' prefill attention) are supplied by
+the GPU test.
 """
 
 from __future__ import annotations
@@ -33,8 +37,9 @@ def _module(monkeypatch, name):
     return mod
 
 
-def install(monkeypatch):
-    """Registers the stand-in modules; returns them by short name."""
+def install(monkeypatch, rocm: bool = True):
+    """Registers the stand-in modules (the ROCm attention backends' modules
+    only with ``rocm``); returns them by short name."""
     mods = {}
     for name in ("sglang", "sglang.srt", "sglang.srt.managers", "sglang.srt.model_executor", "sglang.srt.models",
                  "sglang.srt.layers", "sglang.srt.layers.attention", "sglang.srt.entrypoints"):
@@ -149,6 +154,42 @@ def install(monkeypatch):
 
     fi.FlashInferAttnBackend = FlashInferAttnBackend
 
+    rocm_backends = {}
+    for module, cls_name in (("sglang.srt.layers.attention.triton_backend", "TritonAttnBackend"),
+                             ("sglang.srt.layers.attention.aiter_backend", "AiterAttnBackend")):
+        if not rocm:
+            break
+        mod = _module(monkeypatch, module)
+
+        def make(cls_name=cls_name):
+            class RocmAttnBackend:
+                """SGLang's ROCm backends keep the request-to-token table as
+                ``req_to_token`` and return no lse from forward_extend."""
+
+                def __init__(self, **kw):
+                    self.__dict__.update(kw)
+
+                def init_forward_metadata(self, forward_batch):
+                    calls.append(f"{cls_name}.init_forward_metadata (SGLang's own)")
+                    self.forward_metadata = types.SimpleNamespace(forward_batch=forward_batch)
+
+                def forward_extend(self, q, k, v, layer, forward_batch, save_kv_cache=True):
+                    calls.append(f"{cls_name}.forward_extend (SGLang's own)")
+                    if save_kv_cache:
+                        forward_batch.token_to_kv_pool.set_kv_buffer(layer, forward_batch.out_cache_loc, k, v,
+                                                                     layer.k_scale, layer.v_scale)
+                    return self.prefill_attention(q, layer, forward_batch)
+
+                def forward_decode(self, q, k, v, layer, forward_batch, save_kv_cache=True):
+                    calls.append(f"{cls_name}.forward_decode (SGLang's own)")
+                    raise AssertionError("the MAC decode path was expected")
+
+            RocmAttnBackend.__name__ = RocmAttnBackend.__qualname__ = cls_name
+            return RocmAttnBackend
+
+        rocm_backends[cls_name] = make()
+        setattr(mod, cls_name, rocm_backends[cls_name])
+
     scheduler = _module(monkeypatch, "sglang.srt.managers.scheduler")
 
     def run_scheduler_process(*args, **kwargs):
@@ -180,4 +221,6 @@ def install(monkeypatch):
     return types.SimpleNamespace(ServerArgs=ServerArgs, ScheduleBatch=ScheduleBatch, ForwardBatch=ForwardBatch,
                                  LlamaAttention=LlamaAttention, LlamaModel=LlamaModel,
                                  FlashInferAttnBackend=FlashInferAttnBackend,
+                                 TritonAttnBackend=rocm_backends.get("TritonAttnBackend"),
+                                 AiterAttnBackend=rocm_backends.get("AiterAttnBackend"),
                                  engine=engine, http=http, dpc=dpc, scheduler=scheduler, calls=calls)

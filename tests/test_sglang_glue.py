@@ -399,3 +399,37 @@ def test_low_hit_ejection_policy(monkeypatch):
     persistent.clear_low_hit_ejection(meta, [4])  # request 4 is prefilled again
     persistent.mark_persistent_ready(meta, torch.tensor([4], dtype=torch.int32))
     assert meta.mac_cache_ready_host[4] is True and meta.mac_cache_ready_host[1] is False
+
+
+def test_rocm_extend_ring_rows_are_the_last_capacity_rows():
+    """The ROCm extend hook computes the full prefill state only for the rows
+    the ring keeps: the scheduler's marked suffix (every row without marks),
+    cut to its last M rows, at the absolute positions the ring indexes them
+    by; the preserved pre-RoPE rows are found for every layout the attention
+    hook leaves (all rows, the plan's rows compacted, a tail)."""
+    import types
+
+    from mac_attention.integrations.sglang import model_hooks
+
+    M = 4
+    fb = types.SimpleNamespace(extend_seq_lens_cpu=[10, 3, 6], extend_prefix_lens_cpu=[5, 0, 2],
+                               mac_prefill_cache_update_starts=[7, -1, 2])
+    plan, kept = model_hooks._ring_rows(fb, 3, 19, M)
+    # request 0: marked from position 7 = chunk row 2 (rows 2..9), last 4 -> rows 6..9 at positions 11..14
+    # request 1: unmarked (-1) -> no rows; request 2: from position 2 = chunk row 0 (6 rows) -> last 4
+    assert kept == [(0, 6, 11, 4, 15), (2, 15, 4, 4, 8)]
+    fb_nomarks = types.SimpleNamespace(extend_seq_lens_cpu=[10, 3], extend_prefix_lens_cpu=[5, 0])
+    plan2, kept2 = model_hooks._ring_rows(fb_nomarks, 2, 13, M)
+    assert plan2 is None and kept2 == [(0, 6, 11, 4, 15), (1, 10, 0, 3, 3)]
+    meta = types.SimpleNamespace(cur_q_before_rope=torch.zeros(19, 1, 1), cur_q_before_rope_compacted=False,
+                                 cur_q_before_rope_local_start=0)
+    assert model_hooks._src_rows(meta, plan, kept, 19) == [6, 7, 8, 9, 15, 16, 17, 18]
+    # compacted in plan order: request 0's 8 marked rows, then request 2's 6
+    meta.cur_q_before_rope = torch.zeros(14, 1, 1)
+    meta.cur_q_before_rope_compacted = True
+    assert model_hooks._src_rows(meta, plan, kept, 19) == [4, 5, 6, 7, 10, 11, 12, 13]
+    # a preserved tail of the last 5 chunk rows cannot serve request 0's rows
+    meta.cur_q_before_rope = torch.zeros(5, 1, 1)
+    meta.cur_q_before_rope_local_start = 14
+    assert model_hooks._src_rows(meta, plan, kept, 19) is None
+    assert model_hooks._src_rows(meta, plan, [kept[1]], 19) == [1, 2, 3, 4]

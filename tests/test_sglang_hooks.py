@@ -35,6 +35,9 @@ REQUIRED = {
     "sglang.srt.layers.attention.flashinfer_backend:FlashInferAttnBackend.forward_extend",
     "sglang.srt.layers.attention.flashinfer_backend:FlashInferAttnBackend.forward_decode",
 }
+ROCM = {f"sglang.srt.layers.attention.{m}:{c}.{attr}"
+        for m, c in (("triton_backend", "TritonAttnBackend"), ("aiter_backend", "AiterAttnBackend"))
+        for attr in ("__init__", "init_forward_metadata", "forward_extend", "forward_decode")}
 CHILD_SITES = {
     "sglang.srt.entrypoints.engine:run_scheduler_process",
     "sglang.srt.entrypoints.http_server:run_scheduler_process",
@@ -56,11 +59,21 @@ def sg(monkeypatch):
 def test_install_wraps_every_serving_target(sg):
     done = set(hook_installer.install_hooks(strict=True))
     assert REQUIRED <= done, REQUIRED - done
+    assert ROCM <= done, ROCM - done  # the ROCm attention backends this SGLang has
     assert CHILD_SITES <= done, CHILD_SITES - done
     assert not any("qwen" in t for t in done)  # optional classes this SGLang lacks are skipped
     assert getattr(sg.LlamaAttention.forward, "__mac_attention_hooked__", False)
     assert hook_installer.install_hooks(strict=True) == ()  # idempotent
     assert hook_installer.is_installed()
+
+
+def test_rocm_backends_are_optional(monkeypatch):
+    """An SGLang without the ROCm attention backends (a CUDA build) installs
+    every required hook and skips theirs."""
+    monkeypatch.setattr(hook_installer, "_INSTALLED", [])
+    sglang_standin.install(monkeypatch, rocm=False)
+    done = set(hook_installer.install_hooks(strict=True))
+    assert REQUIRED <= done and not done & ROCM
 
 
 def test_scheduler_process_installs_hooks_then_runs_sglang(sg, monkeypatch):
@@ -95,7 +108,7 @@ def test_plugin_registers_with_sglang_hook_registry(sg, monkeypatch):
     monkeypatch.setitem(sys.modules, "sglang.srt.plugins.hook_registry", mod)
     plugin.register_plugin()
     targets = {t for t, _, _ in registered}
-    assert REQUIRED <= targets and not any("qwen" in t for t in targets)
+    assert REQUIRED <= targets and ROCM <= targets and not any("qwen" in t for t in targets)
     kinds = {t: k for t, _, k in registered}
     assert kinds["sglang.srt.models.llama:LlamaAttention.forward"] is HookType.AROUND
     assert kinds["sglang.srt.server_args:ServerArgs.__post_init__"] is HookType.AFTER

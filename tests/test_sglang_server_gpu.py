@@ -10,9 +10,12 @@ marks the requests ready, and on decode the attention hook's fused RoPE and
 the forward_decode hook's MAC step produce the output.  Request 0's heads
 0-3 repeat a query of their prompt, so the decode step must hit; decisions,
 output and the written ring rows are checked against the CPU oracle run on
-the ring state the prefill left.  The paged prefill attention FlashInfer
-would compute (full causal attention with its lse) comes from this build's
-window-attention kernel with no window.
+the ring state the prefill left.  Three attention backends: FlashInfer,
+whose paged prefill attention with its lse comes from this build's
+window-attention kernel with no window; and the backends SGLang runs on ROCm
+(TritonAttnBackend, AiterAttnBackend), whose own prefill attention returns no
+lse (here a float32 torch attention), so the extend hook computes the kept
+rows' full prefill state itself.
 """
 
 import math
@@ -40,7 +43,27 @@ def _rope_neox(positions, x, heads, cos_sin):
     return torch.cat([x0 * c - x1 * s, x1 * c + x0 * s], dim=-1).to(x.dtype).view(x.shape[0], heads * D)
 
 
-def test_prefill_populates_rings_and_decode_hits_through_installed_hooks(monkeypatch):
+def _torch_prefill(q, fb, req_to_token, k_buf, v_buf, sm_scale):
+    """Causal prefill attention of a chunk in float32 (the ROCm backends'
+    own extend attention in the stand-in): rows of request i at positions
+    prefix_i + j attend the pool rows of positions [0, prefix_i + j]."""
+    qv = q.view(-1, HQ, D).float()
+    outs, off = [], 0
+    for i, r in enumerate(fb.req_pool_indices.tolist()):
+        ext, pre = int(fb.extend_seq_lens_cpu[i]), int(fb.extend_prefix_lens_cpu[i])
+        rows = req_to_token[r, : pre + ext].long()
+        kx = k_buf[rows].float().repeat_interleave(HQ // HKV, dim=1)
+        vx = v_buf[rows].float().repeat_interleave(HQ // HKV, dim=1)
+        sc = torch.einsum("thd,shd->hts", qv[off: off + ext], kx) * sm_scale
+        pos = pre + torch.arange(ext, device=q.device)
+        sc = sc.masked_fill(torch.arange(pre + ext, device=q.device)[None, :] > pos[:, None], float("-inf"))
+        outs.append(torch.einsum("hts,shd->thd", torch.softmax(sc, dim=-1), vx))
+        off += ext
+    return torch.cat(outs).to(torch.bfloat16).reshape(-1, HQ * D)
+
+
+@pytest.mark.parametrize("backend_name", ["FlashInferAttnBackend", "TritonAttnBackend", "AiterAttnBackend"])
+def test_prefill_populates_rings_and_decode_hits_through_installed_hooks(monkeypatch, backend_name):
     from mac_attention.integrations.sglang import bridge, hook_installer
 
     for key, val in (("MAC_ATTENTION_ENABLE", "1"), ("MAC_LOOKBACK_TOKENS_LEFT", str(M)),
@@ -91,10 +114,17 @@ def test_prefill_populates_rings_and_decode_hits_through_installed_hooks(monkeyp
             return o, lse / math.log(2.0)
 
     wrapper = PrefillWrapper()
-    backend = sg.FlashInferAttnBackend(
-        forward_metadata=types.SimpleNamespace(use_ragged=False, prefill_wrappers=[wrapper]),
-        indices_updater_decode=types.SimpleNamespace(req_to_token=req_to_token),
-        indices_updater_prefill=types.SimpleNamespace(req_to_token=req_to_token))
+    if backend_name == "FlashInferAttnBackend":
+        backend = sg.FlashInferAttnBackend(
+            forward_metadata=types.SimpleNamespace(use_ragged=False, prefill_wrappers=[wrapper]),
+            indices_updater_decode=types.SimpleNamespace(req_to_token=req_to_token),
+            indices_updater_prefill=types.SimpleNamespace(req_to_token=req_to_token))
+    else:
+        backend = getattr(sg, backend_name)(
+            req_to_token=req_to_token,
+            prefill_attention=lambda q, layer, fb: _torch_prefill(q, fb, req_to_token, k_buf, v_buf, sm_scale))
+    assert backend.mac_config.enable_mac  # the __init__ hook ran
+    print(f"served through {backend_name}", flush=True)
 
     class RadixAttention:
         layer_id, tp_q_head_num, head_dim, scaling, logit_cap = 0, HQ, D, sm_scale, 0
@@ -138,8 +168,12 @@ def test_prefill_populates_rings_and_decode_hits_through_installed_hooks(monkeyp
     wrapper.kv_indices = locs.to(torch.int32)
     hidden = torch.randn(total, width, device=dev, generator=g).to(torch.bfloat16)
     q_pre_prefill = hidden[:, : HQ * D].clone().view(total, HQ, D)
-    layer.forward(positions, hidden, fb)
+    prefill_out = layer.forward(positions, hidden, fb)
     torch.cuda.synchronize()
+    if backend_name != "FlashInferAttnBackend":  # the backend's own prefill ran and gave the layer's output
+        assert f"{backend_name}.forward_extend (SGLang's own)" in sg.calls
+        q_rot = _rope_neox(positions, hidden[:, : HQ * D], HQ, cos_sin)
+        torch.testing.assert_close(prefill_out, _torch_prefill(q_rot, fb, req_to_token, k_buf, v_buf, sm_scale))
     meta = layer.mac_metadata
     assert meta is not None and rope_calls == [total]
     lse = meta.unified_lse_cache.cpu().numpy()
