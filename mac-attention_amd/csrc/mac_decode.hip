@@ -147,12 +147,7 @@ struct AttnParams {
   const int32_t* group_rect_begin;
   const int32_t* group_rect_end;
   const int32_t* group_tail_end;
-  const int32_t* group_mode;
-  int32_t* group_rect_tiles;
-  int32_t* group_tail_tiles;
-  int32_t* group_chunk;   // complete_task_go
-  int32_t* group_ntasks;  // complete_task_tile
-  int32_t* task_counts;
+  int32_t* task_counts;   // [0] tasks and [4] the plan's chunk (workgroup 0)
   int32_t* task_counter;   // complete_task_tile[N * Hkv]; zeroed by match_decide
   void* partial_o;
   float* partial_lse;
@@ -160,7 +155,6 @@ struct AttnParams {
   int64_t o_group_stride;  // elements of partial_o per group
   int cap;                 // task slots per group
   int F;
-  int tile_tokens;  // the caller's tile size (task_counts[3] only)
   int tasks_per_wg;  // target tasks per workgroup of the plan
   int narrow_grid;                // workgroups that take tasks when a step has
   long long narrow_min_tokens;    // at least this many tokens (the others return)
@@ -168,7 +162,6 @@ struct AttnParams {
   float q_scale;  // sm_scale * log2(e)
   const int32_t* group_fused;  // groups match_decide finished (no tasks here)
   const int32_t* long_groups;  // 0: match_decide finished every group
-  uint32_t* fuse_sync;         // workgroup 0 leaves the step's counts for the next step's short-group rule
   int fuse_tokens;             // a group of at most fuse_tokens tokens is short (0: none)
   int plan_bucket;             // groups per entry of the plan's LDS offset table
   int64_t* phase_cycles;
@@ -205,7 +198,6 @@ struct MergeParams {
   const int32_t* group_rect_begin;
   const int32_t* group_rect_end;
   const int32_t* group_tail_end;
-  const int32_t* group_chunk;
   const void* partial_o;
   const float* partial_lse;
   int partial_bf16;
@@ -216,6 +208,15 @@ struct MergeParams {
   int32_t* long_groups;  // cleared here for the next step
   int64_t* phase_cycles;
   int fuse_tokens;  // short groups (at most this many tokens) have no partials: skipped
+  // the counting workgroup's outputs (publish_counts)
+  const int32_t* group_mode;
+  int32_t* group_chunk_out;  // complete_task_go
+  int32_t* group_ntasks;     // complete_task_tile
+  int32_t* group_rect_tiles;
+  int32_t* group_tail_tiles;
+  int32_t* task_counts;      // [0] and [4] come from span_attention
+  uint32_t* fuse_sync;       // the next step's short-group rule (NULL: no rule)
+  int tile_tokens;
 };
 
 // Whether this step's short groups are finished here.  Finishing a short
@@ -236,8 +237,7 @@ struct MergeParams {
 // different orders), so two calls on the same inputs can differ in the last
 // bits when their previous steps differed (MAC_AMD_FUSE_POLICY=always pins
 // the choice).
-__device__ __forceinline__ int step_fuse_rule(const DecideParams& p) {
-  const uint32_t* c = p.fuse_sync;
+__device__ __forceinline__ int step_fuse_rule(const DecideParams& p, const uint32_t (&c)[3]) {
   const uint32_t n_short = c[0], n_long = c[1];
   const long long all_tokens = static_cast<long long>(c[2]) << 6;
   // counts of a different batch shape (or none yet: a workspace's first
@@ -755,7 +755,8 @@ template <int G, int kMode, int W = kWaves>
 __device__ __forceinline__ void decide_group(const DecideParams& p, const float (*s_d)[kMaxGroup],
                                              const int (*s_p)[kMaxGroup], const int (*s_s)[kMaxGroup],
                                              const float (*s_lse)[kLsePrefetchSlots], bool lse_in_lds, int g,
-                                             int n, int hkv, int P, int req, bool eligible, int* s_rect,
+                                             int n, int hkv, int P, int req, bool eligible,
+                                             const uint32_t (&rule_counts)[3], int* s_rect,
                                              int* s_mslot, float* s_entry, int* s_span) {
   const int lane = threadIdx.x & 63;
   const int M = p.s.M;
@@ -922,7 +923,7 @@ __device__ __forceinline__ void decide_group(const DecideParams& p, const float 
   const long long tokens = static_cast<long long>(fs_begin) + (new_end - rb) + max(P + 1 - new_end, 0);
   const bool is_short = p.fuse_tokens > 0 && tokens <= p.fuse_tokens;
   int fused = is_short ? 1 : 0;
-  if (is_short && p.fuse_sync != nullptr && lane == 0) fused = step_fuse_rule(p);
+  if (is_short && p.fuse_sync != nullptr) fused = step_fuse_rule(p, rule_counts);
   if (head_lane) {
     s_rect[h] = rect_start;
     s_mslot[h] = hit ? mslot : -1;
@@ -1140,8 +1141,32 @@ __global__ void __launch_bounds__(W * 64, W == kWaves ? 2 : 1) match_decide_kern
 
   const int P = p.past_lens[n];
   const int req = p.req_ids[n];
-  // DECODE:974-981; the readiness gate (a load of its own) is applied after
-  // the scan's loads are in flight
+  // The words the decision reads besides the scan's results -- the readiness
+  // gate and the previous step's counts for the short-group rule -- are
+  // loaded here, with the scan's round, and used only after the scan.  They
+  // are vector loads (`zero` is a vector register the compiler cannot see
+  // through) from always-valid addresses, with no branch: a uniform load
+  // would be moved to a scalar register at once, and a branch on a pointer
+  // would join the loaded value before its use, either of which waits for
+  // the load before the scan's loads are issued.
+  int zero = 0;
+  asm volatile("" : "+v"(zero));
+  const bool req_in = req >= 0 && req < p.s.R;
+  const int req_c = req_in ? req : 0;
+  const bool have_ready = p.cache_ready != nullptr;
+  const bool have_epochs = have_ready && p.cache_epoch != nullptr && p.request_epoch != nullptr;
+  const bool have_rule = kMode != 1 && p.fuse_sync != nullptr;
+  const void* any_valid = p.q_pre;  // (8-byte aligned, at least 32 bytes)
+  const uint8_t* ready_at = have_ready ? p.cache_ready + req_c : static_cast<const uint8_t*>(any_valid);
+  const int64_t* epoch_c_at = have_epochs ? p.cache_epoch + req_c : static_cast<const int64_t*>(any_valid);
+  const int64_t* epoch_r_at = have_epochs ? p.request_epoch + req_c : static_cast<const int64_t*>(any_valid);
+  const uint32_t* rule_at = have_rule ? p.fuse_sync : static_cast<const uint32_t*>(any_valid);
+  const uint32_t ready_word = ready_at[zero];
+  const int64_t epoch_c = epoch_c_at[zero], epoch_r = epoch_r_at[zero];
+  uint32_t rule_counts[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) rule_counts[i] = rule_at[i + zero];
+  // DECODE:974-981; the readiness gate is applied after the scan
   const int cand_begin = max(0, P - M);
   int cand_end = P;
   if (p.candidate_mode == 1) cand_end = max(cand_begin, P - p.lookback_right);
@@ -1409,7 +1434,8 @@ __global__ void __launch_bounds__(W * 64, W == kWaves ? 2 : 1) match_decide_kern
 #pragma unroll
     for (int hh = 0; hh < G; ++hh) s_lse[hh][lane] = lse_reg[hh];
   }
-  const bool ready = request_ready(p.cache_ready, p.cache_epoch, p.request_epoch, req, p.s.R);
+  // DECODE:221-230, request_ready's rule on the words loaded at the start
+  const bool ready = req_in && (!have_ready || (ready_word != 0 && (!have_epochs || epoch_c == epoch_r)));
   const bool eligible = cand_ok && ready;
   __syncthreads();
   if (kMode != 1 && p.phase_cycles != nullptr && g == 0 && tid == 0)
@@ -1418,7 +1444,7 @@ __global__ void __launch_bounds__(W * 64, W == kWaves ? 2 : 1) match_decide_kern
   __shared__ float s_entry[kMaxGroup];
   __shared__ int s_span[3];  // band begin, new_end, fused
   if (wave == 0) decide_group<G, kMode, W>(p, s_d, s_p, s_s, s_lse, lse_in_lds, g, n, hkv, P, req, eligible,
-                                        s_rect, s_mslot, s_entry, s_span);
+                                        rule_counts, s_rect, s_mslot, s_entry, s_span);
   if constexpr (kMode != 1) {
     __syncthreads();
     if (s_span[2] == 0) return;
@@ -1541,8 +1567,7 @@ constexpr int kFuseTokens = 1024;  // default of DecideParams::fuse_tokens
 // plan_bucket consecutive groups (NB buckets; one group per bucket for up to
 // kMaxPlanBuckets groups), s_off[NB+1 .. 2NB+1] those of the B counts;
 // decode_task finds a task's bucket in the table and its group from the
-// bucket's spans.  Workgroup 0 also publishes the per-group chunk and task
-// counts for merge_write and the task counters.
+// bucket's spans.  Workgroup 0 also publishes the chunk and the task count.
 __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& total_tasks_out,
                            int& chunk_out, int& active_wgs_out) {
   const int tid = threadIdx.x;
@@ -1555,7 +1580,7 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
   const int g_lo = min(tid * per_thread, NG);
   const int g_hi = min(g_lo + per_thread, NG);
   // match_decide finished every group: only workgroup 0 stays, to publish
-  // the per-group descriptors and the counters
+  // the chunk and the task count
   const bool any_long = *p.long_groups != 0;
   if (!any_long && blockIdx.x != 0) {
     total_tasks_out = 0;
@@ -1634,83 +1659,12 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
   }
   __syncthreads();
 
-  if (blockIdx.x == 0) {
-    // descriptors for merge_write and the reference's task counters
-    int nonhit = 0, ff = 0, red = 0, max_ff = 0, max_mixed = 0, tails = 0, shorts = 0, longs = 0;
-    uint32_t units = 0;  // tokens / 64 of all groups, for the next step's short-group rule
-    for (int g = tid; g < NG; g += kBlock) {
-      GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, g, p.F, chunk, p.cap);
-      const int t = group_tokens(sp.sink_end, sp.band_begin, sp.new_end, sp.kv_len);
-      if (t <= p.fuse_tokens) ++shorts;
-      else ++longs;
-      units += static_cast<uint32_t>((t + 63) >> 6);
-      p.group_chunk[g] = sp.chunk;
-      int na, nb;
-      group_task_counts(sp, p.group_fused[g] != 0, p.fuse_tokens, na, nb);
-      p.group_ntasks[g] = na + nb;
-      p.group_rect_tiles[g] = sp.n_band;
-      p.group_tail_tiles[g] = sp.n_tail;
-      const int mode = p.group_mode[g];
-      if (p.group_fused[g] == 0) tails += sp.n_tail;
-      if (mode != MAC_GROUP_MAC_HIT) {
-        ++nonhit;
-        // the reference's reduce condition with its default threshold: the
-        // band spans more than one tile of tile_tokens
-        if (sp.new_end - sp.band_begin > p.tile_tokens) ++red;
-      }
-      if (mode == MAC_GROUP_FULL_FALLBACK) {
-        ++ff;
-        max_ff = max(max_ff, sp.n_band);
-      }
-      if (mode == MAC_GROUP_MIXED) max_mixed = max(max_mixed, sp.n_band);
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      nonhit += __shfl_xor(nonhit, off);
-      ff += __shfl_xor(ff, off);
-      red += __shfl_xor(red, off);
-      tails += __shfl_xor(tails, off);
-      shorts += __shfl_xor(shorts, off);
-      longs += __shfl_xor(longs, off);
-      units += __shfl_xor(units, off);
-      max_ff = max(max_ff, __shfl_xor(max_ff, off));
-      max_mixed = max(max_mixed, __shfl_xor(max_mixed, off));
-    }
-    __shared__ int s_cnt[kWaves][9];
-    if (lane == 0) {
-      s_cnt[wave][0] = nonhit;
-      s_cnt[wave][1] = ff;
-      s_cnt[wave][2] = red;
-      s_cnt[wave][3] = tails;
-      s_cnt[wave][4] = max_ff;
-      s_cnt[wave][5] = max_mixed;
-      s_cnt[wave][6] = shorts;
-      s_cnt[wave][7] = longs;
-      s_cnt[wave][8] = static_cast<int>(units);
-    }
-    __syncthreads();
-    if (tid == 0) {
-      int a[6] = {0, 0, 0, 0, 0, 0};
-      uint32_t f[3] = {0, 0, 0};
-      for (int w = 0; w < kWaves; ++w) {
-        for (int i = 0; i < 4; ++i) a[i] += s_cnt[w][i];
-        a[4] = max(a[4], s_cnt[w][4]);
-        a[5] = max(a[5], s_cnt[w][5]);
-        for (int i = 0; i < 3; ++i) f[i] += static_cast<uint32_t>(s_cnt[w][6 + i]);
-      }
-      if (p.fuse_sync != nullptr) {
-        for (int i = 0; i < 3; ++i) p.fuse_sync[i] = f[i];
-      }
-      p.task_counts[0] = total_tasks;
-      p.task_counts[1] = a[3];
-      p.task_counts[2] = 0;
-      p.task_counts[3] = a[2];
-      p.task_counts[4] = chunk;
-      p.task_counts[5] = a[0];
-      p.task_counts[6] = a[1];
-      p.task_counts[7] = a[4];
-      p.task_counts[8] = a[5];
-    }
+  if (blockIdx.x == 0 && tid == 0) {
+    // the plan's chunk, from which merge_write derives every group's chunk,
+    // and the task total (the reference's counters [4] and [0]; the others
+    // are counted by merge_write's workgroup 0, off this kernel's critical path)
+    p.task_counts[0] = total_tasks;
+    p.task_counts[4] = chunk;
   }
 
   total_tasks_out = total_tasks;
@@ -1929,10 +1883,105 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
 // ring state = cached entry (hit heads) (+) band partials -> ring row (ready
 // requests only); out / out_lse = ring state (+) sink and tail partials.  An empty partial (lse = -inf) has weight 0,
 // the reference's skip rule (DECODE:866-890).
+// The per-group descriptors (chunk, task, band and tail task counts) and the
+// reference's task counters of the step (DECODE:1406-1530), counted by one
+// extra workgroup of merge_write, where they overlap that launch instead of
+// delaying span_attention's end; also the step's counts for the next step's
+// short-group rule (step_fuse_rule) and the cleared long-group flag.
+__device__ void publish_counts(const MergeParams& p) {
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int NG = p.s.N * p.s.Hkv;
+  const int chunk = p.task_counts[4];
+  if (tid == 0) *p.long_groups = 0;  // read by span_attention, set again by match_decide
+  int nonhit = 0, ff = 0, red = 0, max_ff = 0, max_mixed = 0, tails = 0, shorts = 0, longs = 0;
+  uint32_t units = 0;  // tokens / 64 of all groups, for the next step's short-group rule
+  for (int g = tid; g < NG; g += kBlock) {
+    GroupSpans sp = load_spans(p.group_rect_begin, p.group_rect_end, p.group_tail_end, g, p.F, chunk, p.cap);
+    const bool fused = p.group_fused[g] != 0;
+    const int mode = p.group_mode[g];
+    const int t = group_tokens(sp.sink_end, sp.band_begin, sp.new_end, sp.kv_len);
+    const bool shrt = p.fuse_tokens > 0 && t <= p.fuse_tokens;
+    if (t <= p.fuse_tokens) ++shorts;
+    else ++longs;
+    units += static_cast<uint32_t>((t + 63) >> 6);
+    const int na = (fused || shrt) ? 0 : full_band_pieces(sp);
+    const int nb = fused ? 0 : (shrt ? 1 : sp.n_sink + sp.n_band + sp.n_tail - na);
+    p.group_chunk_out[g] = sp.chunk;
+    p.group_ntasks[g] = na + nb;
+    p.group_rect_tiles[g] = sp.n_band;
+    p.group_tail_tiles[g] = sp.n_tail;
+    if (!fused && !shrt) tails += sp.n_tail;
+    if (mode != MAC_GROUP_MAC_HIT) {
+      ++nonhit;
+      // the reference's reduce condition with its default threshold: the
+      // band spans more than one tile of tile_tokens
+      if (sp.new_end - sp.band_begin > p.tile_tokens) ++red;
+    }
+    if (mode == MAC_GROUP_FULL_FALLBACK) {
+      ++ff;
+      max_ff = max(max_ff, sp.n_band);
+    }
+    if (mode == MAC_GROUP_MIXED) max_mixed = max(max_mixed, sp.n_band);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    nonhit += __shfl_xor(nonhit, off);
+    ff += __shfl_xor(ff, off);
+    red += __shfl_xor(red, off);
+    tails += __shfl_xor(tails, off);
+    shorts += __shfl_xor(shorts, off);
+    longs += __shfl_xor(longs, off);
+    units += __shfl_xor(units, off);
+    max_ff = max(max_ff, __shfl_xor(max_ff, off));
+    max_mixed = max(max_mixed, __shfl_xor(max_mixed, off));
+  }
+  __shared__ int s_cnt[kWaves][9];
+  if (lane == 0) {
+    s_cnt[wave][0] = nonhit;
+    s_cnt[wave][1] = ff;
+    s_cnt[wave][2] = red;
+    s_cnt[wave][3] = tails;
+    s_cnt[wave][4] = max_ff;
+    s_cnt[wave][5] = max_mixed;
+    s_cnt[wave][6] = shorts;
+    s_cnt[wave][7] = longs;
+    s_cnt[wave][8] = static_cast<int>(units);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int a[6] = {0, 0, 0, 0, 0, 0};
+    uint32_t f[3] = {0, 0, 0};
+    for (int w = 0; w < kWaves; ++w) {
+      for (int i = 0; i < 4; ++i) a[i] += s_cnt[w][i];
+      a[4] = max(a[4], s_cnt[w][4]);
+      a[5] = max(a[5], s_cnt[w][5]);
+      for (int i = 0; i < 3; ++i) f[i] += static_cast<uint32_t>(s_cnt[w][6 + i]);
+    }
+    if (p.fuse_sync != nullptr) {
+      for (int i = 0; i < 3; ++i) p.fuse_sync[i] = f[i];
+    }
+    p.task_counts[1] = a[3];
+    p.task_counts[2] = 0;
+    p.task_counts[3] = a[2];
+    p.task_counts[5] = a[0];
+    p.task_counts[6] = a[1];
+    p.task_counts[7] = a[4];
+    p.task_counts[8] = a[5];
+  }
+}
+
+// One workgroup per (group, query head) -- blockIdx.x = group + 1; the
+// workgroups of blockIdx.x = 0 count (publish_counts, y = 0) or return.
 template <int G>
 __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
   constexpr int kBatch = 8;
-  const int g = blockIdx.x;
+  if (blockIdx.x == 0) {
+    if (blockIdx.y == 0) publish_counts(p);
+    return;
+  }
+  const int g = blockIdx.x - 1;
   const int h = blockIdx.y;
   const int n = g / p.s.Hkv;
   const int hkv = g - n * p.s.Hkv;
@@ -1942,7 +1991,6 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
   const int d0 = 2 * lane;
   const bool stamp = p.phase_cycles != nullptr && g == 0 && h == 0 && tid == 0;
   if (stamp) p.phase_cycles[4] = static_cast<int64_t>(wall_clock64());
-  if (g == 0 && h == 0 && tid == 0) *p.long_groups = 0;  // read by span_attention, set again by match_decide
   // the group's descriptors are loaded with its finished flag (one round of
   // loads, not two; a finished group does not use them)
   const int M = p.s.M;
@@ -1955,15 +2003,17 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
   const int band_begin = p.group_rect_begin[g];
   const int new_end = p.group_rect_end[g];
   const int kv_len = p.group_tail_end[g];
-  const int chunk = p.group_chunk[g];
+  const int plan_chunk = p.task_counts[4];
   const int hit = p.head_hit[ho];
   const int mslot = p.head_match_slot[ho];
   const int sink_end = min(p.F, new_end);
-  const bool shrt = p.fuse_tokens > 0 && group_tokens(sink_end, band_begin, new_end, kv_len) <= p.fuse_tokens;
+  const int tokens = group_tokens(sink_end, band_begin, new_end, kv_len);
+  const bool shrt = p.fuse_tokens > 0 && tokens <= p.fuse_tokens;
   if (fused != 0 || shrt) {  // finished by match_decide or by a short task
     if (stamp) p.phase_cycles[5] = static_cast<int64_t>(wall_clock64());
     return;
   }
+  const int chunk = group_chunk(tokens, plan_chunk, p.cap);  // as span_attention's plan derives it
   const bool ready = request_ready(p.cache_ready, p.cache_epoch, p.request_epoch, req, p.s.R);
   const int dest = P % M;
   const int n_sink = ceil_div(sink_end, chunk);
@@ -2211,7 +2261,7 @@ int launch_all(const DecideParams& dp, const AttnParams& ap, const MergeParams& 
   hipLaunchKernelGGL(span_attention_mfma_kernel<G>, dim3(attn_grid), dim3(kBlock), plan_lds, stream, ap);
   MAC_HIP(hipGetLastError());
   if (ev) MAC_HIP(hipEventRecord(ev[2], stream));
-  hipLaunchKernelGGL(merge_write_kernel<G>, dim3(NG, G), dim3(kBlock), 0, stream, mp);
+  hipLaunchKernelGGL(merge_write_kernel<G>, dim3(NG + 1, G), dim3(kBlock), 0, stream, mp);
   MAC_HIP(hipGetLastError());
   if (ev) MAC_HIP(hipEventRecord(ev[3], stream));
   return MAC_OK;
@@ -2391,11 +2441,6 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   ap.group_rect_begin = a->group_rect_begin;
   ap.group_rect_end = a->group_rect_end;
   ap.group_tail_end = a->group_tail_end;
-  ap.group_mode = a->group_mode;
-  ap.group_rect_tiles = a->group_rect_tiles;
-  ap.group_tail_tiles = a->group_tail_tiles;
-  ap.group_chunk = a->complete_task_go;
-  ap.group_ntasks = a->complete_task_tile;
   ap.task_counts = a->task_counts;
   ap.task_counter = dp.task_counter;
   ap.partial_o = a->partial_o;
@@ -2405,13 +2450,11 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   ap.cap = cap;
   ap.F = dp.F;
   ap.q_scale = static_cast<float>(a->sm_scale) * kLog2e;
-  ap.tile_tokens = a->tile_tokens;
   ap.tasks_per_wg = tasks_per_wg();
   ap.min_chunk = min_chunk();
   ap.narrow_grid = cus;
   ap.narrow_min_tokens = narrow_min_tokens();
   ap.group_fused = dp.group_fused;
-  ap.fuse_sync = const_cast<uint32_t*>(dp.fuse_sync);
   ap.fuse_tokens = dp.fuse_tokens;
   ap.plan_bucket = plan_bucket;
   ap.long_groups = dp.long_groups;
@@ -2447,7 +2490,6 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   mp.group_rect_begin = a->group_rect_begin;
   mp.group_rect_end = a->group_rect_end;
   mp.group_tail_end = a->group_tail_end;
-  mp.group_chunk = a->complete_task_go;
   mp.partial_o = a->partial_o;
   mp.partial_lse = a->partial_lse;
   mp.partial_bf16 = ap.partial_bf16;
@@ -2458,6 +2500,14 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
   mp.long_groups = dp.long_groups;
   mp.phase_cycles = stamps;
   mp.fuse_tokens = dp.fuse_tokens;
+  mp.group_mode = a->group_mode;
+  mp.group_chunk_out = a->complete_task_go;
+  mp.group_ntasks = a->complete_task_tile;
+  mp.group_rect_tiles = a->group_rect_tiles;
+  mp.group_tail_tiles = a->group_tail_tiles;
+  mp.task_counts = a->task_counts;
+  mp.fuse_sync = const_cast<uint32_t*>(dp.fuse_sync);
+  mp.tile_tokens = a->tile_tokens;
 
   // Persistent grid: what the device keeps resident, but no more workgroups
   // than the largest task count the caller's max_context allows.
