@@ -291,6 +291,70 @@ def cpu_baseline(args, hit):
                 sample_head_hits=hits)
 
 
+def cpu_baseline_configs():
+    """The same FP32 torch restatement on BASELINE.json configs 0-2, on this
+    host's cores: config 0 (B=1, ctx 4096, GQA-4, 16 cached queries at
+    positions in [1024, 4000) of a 4096-slot ring, Bernoulli(0.5) hits, F=0)
+    and config 1 (B=1, ctx 32768, GQA-4, F=64, 16 cached queries at positions
+    in [ctx-3000, ctx-64), hit 0.5) are timed whole; config 2 (B=16, ctx
+    65536, GQA-8, F=128, positions in [0.5 ctx, ctx-512) of a 32768-slot ring,
+    hit 0.5) is timed on one request and scaled by 16 (requests are
+    independent).  Hits are planted as sqrt(1-eps^2) q + eps N(0,1), eps 0.3
+    (hit) / 0.9 (miss), as the GPU tests of these configs do.  A batch-1 step
+    is the faster of two runs (the first also warms torch up)."""
+    import numpy as np
+    import torch
+
+    from oracle import torch_oracle as tor
+
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    out = {}
+    specs = [  # name, Hkv, ctx, ring, F, (pos lo, pos hi), hit rate, requests in the config
+        ("config0", 8, 4096, 4096, 0, (1024, 4000), None, 1),
+        ("config1", 8, 32768, 4096, 64, (32768 - 3000, 32768 - 64), 0.5, 1),
+        ("config2", 4, 65536, 32768, 128, (32768, 65536 - 512), 0.5, 16),
+    ]
+    for name, hkv, ctx, m, f, (lo, hi), hit, batch in specs:
+        rng = np.random.default_rng(0)
+        g = torch.Generator().manual_seed(0)
+        hq, S = 32, 256
+        kv_len = ctx + 1
+        k = tor.bf16(torch.randn(kv_len, hkv, D, generator=g))
+        v = tor.bf16(torch.randn(kv_len, hkv, D, generator=g))
+        q_pre = tor.bf16(torch.randn(hq, D, generator=g))
+        q_post = tor.bf16(torch.randn(hq, D, generator=g))
+        ring_q = tor.bf16(torch.randn(m, hq, D, generator=g) + 10.0)
+        ring_o = tor.bf16(torch.randn(m, hq, D, generator=g))
+        ring_l = torch.full((m, hq), -math.inf)
+        positions = sorted(rng.choice(np.arange(lo, hi), size=16, replace=False).tolist())
+        hit_mask = rng.random(hq) < 0.5 if hit is None else np.isin(np.arange(hq), rng.choice(
+            hq, size=int(round(hit * hq)), replace=False))
+        for p_ in positions:
+            slot = p_ % m
+            ring_q[slot] = tor.bf16(torch.randn(hq, D, generator=g))
+            ring_l[slot] = torch.randn(hq, generator=g)
+        for h in range(hq):
+            eps = 0.3 if hit_mask[h] else 0.9
+            slot = int(rng.choice(positions)) % m
+            ring_q[slot, h] = tor.bf16(math.sqrt(1 - eps * eps) * q_pre[h] + eps * torch.randn(D, generator=g))
+        params = tor.StepParams(semantic_pos_ahead=S, front_sink_tokens=f, sm_scale=1.0 / math.sqrt(D))
+        one = math.inf
+        for _ in range(2 if batch == 1 else 1):  # small steps: the faster of two (the first warms torch up)
+            rq, ro, rl = ring_q.clone(), ring_o.clone(), ring_l.clone()
+            t0 = time.perf_counter()
+            r = tor.decode_request(q_post=q_post, q_pre=q_pre, k=k, v=v, r2t_row=torch.arange(kv_len), P=ctx,
+                                   cur_loc=ctx, ring_q=rq, ring_o=ro, ring_lse=rl, params=params)
+            one = min(one, time.perf_counter() - t0)
+        out[name] = dict(value=round(one * batch * 1e6, 1), unit="us/step", cores=cores, kind="port",
+                         precision="fp32", requests_timed=1, requests_in_step=batch,
+                         extrapolated=batch > 1, hit_heads=int(r["head_hit"].sum()),
+                         sample=(f"B={batch} Hq={hq} Hkv={hkv} ctx={ctx} ring={m} F={f}: "
+                                 + ("the whole step" if batch == 1 else
+                                    f"one request timed, x{batch} (requests are independent)")))
+    return out
+
+
 def stream_read_peak(torch):
     """The rate a plain streaming read of 8 GiB reaches on this GPU
     (mac_bench_stream_read: non-temporal 16-byte loads, eight in flight per
@@ -643,6 +707,8 @@ def main():
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU oracle sample")
         cpu = cpu_baseline(args, args.hit)
+        cpu["per_config"] = cpu_baseline_configs()
+        cpu["per_config"]["config3"] = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")}
         log(f"[bench] cpu {cpu}")
         if aux is not None:
             for name, base in aux_cpu_baselines().items():
