@@ -21,10 +21,14 @@ Targets, by group:
   * the ROCm backends (AiterAttnBackend, TritonAttnBackend; optional): the
     same four targets, with the ring update computing the kept rows' full
     prefill state itself, since these backends return no lse.
+  * decode graphs (FlashInfer and ROCm backends, optional): during capture
+    each layer records which decode path it captured; a replay of a graph
+    whose every layer is the MAC step skips the backend's replay metadata
+    (flashinfer_hooks.py:660-700, :835-899).
 Profiling-only and CUDA-graph-trace hooks of the reference are not part of
-this build, nor its decode-graph metadata skipping and the wait for
-side-stream ring updates before a graph replay: the ring update here runs
-on the compute stream, in order with the replay.
+this build, nor the wait for side-stream ring updates before a graph
+replay: the ring update here runs on the compute stream, in order with the
+replay.
 """
 
 from __future__ import annotations
@@ -67,7 +71,8 @@ class HookSpec:
 
 def iter_hook_specs() -> Iterable[HookSpec]:
     from . import model_hooks, schedule_hooks
-    from .persistent import flashinfer_forward_decode_around
+    from .persistent import (flashinfer_forward_decode_around, init_forward_metadata_capture_cuda_graph_around,
+                             init_forward_metadata_replay_cuda_graph_around)
     from .plugin import (server_args_add_cli_args_around, server_args_from_cli_args_after,
                          server_args_post_init_after)
 
@@ -102,6 +107,14 @@ def iter_hook_specs() -> Iterable[HookSpec]:
                        "around", True)
         yield HookSpec(f"{backend}.forward_extend", model_hooks.rocm_forward_extend_around, "around", True)
         yield HookSpec(f"{backend}.forward_decode", flashinfer_forward_decode_around, "around", True)
+
+    # decode graphs: skip the backend's replay metadata when every layer
+    # captured the MAC step (optional: SGLang builds without graph support)
+    for backend in (_FLASHINFER, *_ROCM_BACKENDS):
+        yield HookSpec(f"{backend}.init_forward_metadata_capture_cuda_graph",
+                       init_forward_metadata_capture_cuda_graph_around, "around", True)
+        yield HookSpec(f"{backend}.init_forward_metadata_replay_cuda_graph",
+                       init_forward_metadata_replay_cuda_graph_around, "around", True)
 
 
 def _resolve_target(target: str) -> tuple[Any, str]:

@@ -576,6 +576,7 @@ def flashinfer_forward_decode_around(original_fn: Any, self: Any, q: torch.Tenso
 
     config = getattr(layer, "mac_config", None) or getattr(self, "mac_config", None) or get_mac_config()
     if not supports_mac_backend(self, layer, forward_batch, config):
+        record_decode_graph_capture(self, forward_batch, persistent=False)
         return original_fn(self, q, k, v, layer, forward_batch, save_kv_cache=save_kv_cache, **kwargs)
     metadata: MacMetadata = layer.mac_metadata
     cache_loc = forward_batch.out_cache_loc
@@ -585,10 +586,91 @@ def flashinfer_forward_decode_around(original_fn: Any, self: Any, q: torch.Tenso
     k_buffer, v_buffer = forward_batch.token_to_kv_pool.get_kv_buffer(layer.layer_id)
     out = try_persistent_decode(self, forward_batch, config, metadata, q_input, k_buffer, v_buffer, cache_loc,
                                 layer)
+    record_decode_graph_capture(self, forward_batch, persistent=out is not None)
     if out is not None:
         return out.view(-1, layer.tp_q_head_num * layer.head_dim)
     invalidate_persistent_ready(metadata, metadata.req_ids[: int(forward_batch.batch_size)])
     return original_fn(self, q, k, v, layer, forward_batch, save_kv_cache=False, **kwargs)
+
+
+# ----------------------------------------------------- decode graphs ----
+#
+# flashinfer_hooks.py:660-700, :835-899.  While SGLang captures a decode
+# graph for a batch size, every layer's decode hook records whether it
+# captured the MAC step or the backend's own decode.  When every layer of
+# that graph is the MAC step, a replay needs none of the backend's decode
+# metadata (the MAC kernels read the request tables and lengths themselves,
+# and demote requests whose ring is not current inside the graph), so the
+# backend's per-replay metadata update is skipped
+# (MAC_CUDAGRAPH_SKIP_FLASHINFER_REPLAY_METADATA, default on, the
+# reference's switch).  The reference's other replay duty -- waiting for
+# prefill ring updates on a side stream -- has nothing to wait for here: the
+# ring update runs on the compute stream, in order with the replay.
+
+
+def skip_replay_metadata_enabled() -> bool:
+    raw = os.environ.get("MAC_CUDAGRAPH_SKIP_FLASHINFER_REPLAY_METADATA", "1")
+    return raw.strip().lower() in {"1", "true", "yes", "on"}
+
+
+def decode_graph_states(backend: Any) -> dict:
+    states = getattr(backend, "mac_cudagraph_decode_states", None)
+    if not isinstance(states, dict):
+        states = {}
+        backend.mac_cudagraph_decode_states = states
+    return states
+
+
+def record_decode_graph_capture(backend: Any, forward_batch: Any, *, persistent: bool) -> None:
+    """During a graph capture: which decode path this layer captured."""
+    if not is_graph_capturing():
+        return
+    try:
+        bs = int(getattr(forward_batch, "batch_size", 0))
+    except Exception:
+        return
+    if bs <= 0:
+        return
+    state = decode_graph_states(backend).setdefault(bs, {"persistent_seen": False, "fallback_seen": False})
+    state["persistent_seen" if persistent else "fallback_seen"] = True
+
+
+def _graph_args(args: tuple, kwargs: dict) -> tuple:
+    """(bs, forward_mode) of init_forward_metadata_capture/replay_cuda_graph:
+    SGLang passes bs first and forward_mode sixth."""
+    bs = args[0] if len(args) > 0 else kwargs.get("bs")
+    mode = args[5] if len(args) > 5 else kwargs.get("forward_mode")
+    try:
+        decode = bool(mode.is_decode_or_idle())
+    except Exception:
+        decode = False
+    return bs, decode
+
+
+def init_forward_metadata_capture_cuda_graph_around(original_fn: Any, self: Any, *args: Any, **kwargs: Any) -> Any:
+    """A decode graph is about to be captured for batch size bs: forget what
+    an earlier capture of that size recorded."""
+    from .config import get_mac_config
+
+    bs, decode = _graph_args(args, kwargs)
+    config = getattr(self, "mac_config", None) or get_mac_config()
+    if skip_replay_metadata_enabled() and config.enable_mac and decode and bs is not None:
+        decode_graph_states(self)[int(bs)] = {"persistent_seen": False, "fallback_seen": False}
+    return original_fn(self, *args, **kwargs)
+
+
+def init_forward_metadata_replay_cuda_graph_around(original_fn: Any, self: Any, *args: Any, **kwargs: Any) -> Any:
+    """Skip the backend's replay metadata for decode graphs whose every layer
+    captured the MAC step."""
+    from .config import get_mac_config
+
+    bs, decode = _graph_args(args, kwargs)
+    if skip_replay_metadata_enabled() and bs is not None and decode:
+        config = getattr(self, "mac_config", None) or get_mac_config()
+        state = getattr(self, "mac_cudagraph_decode_states", {}).get(int(bs), {})
+        if config.enable_mac and state.get("persistent_seen", False) and not state.get("fallback_seen", False):
+            return None
+    return original_fn(self, *args, **kwargs)
 
 
 # -------------------------------------------------------------- prefill ----

@@ -152,6 +152,14 @@ def install(monkeypatch, rocm: bool = True):
             calls.append("FlashInferAttnBackend.forward_decode (SGLang's own)")
             raise AssertionError("the MAC decode path was expected")
 
+        def init_forward_metadata_capture_cuda_graph(self, bs, num_tokens, req_pool_indices, seq_lens,
+                                                     encoder_lens, forward_mode, spec_info):
+            calls.append(("FlashInferAttnBackend.init_forward_metadata_capture_cuda_graph", bs))
+
+        def init_forward_metadata_replay_cuda_graph(self, bs, req_pool_indices, seq_lens, seq_lens_sum,
+                                                    encoder_lens, forward_mode, spec_info, seq_lens_cpu=None):
+            calls.append(("FlashInferAttnBackend.init_forward_metadata_replay_cuda_graph", bs))
+
     fi.FlashInferAttnBackend = FlashInferAttnBackend
 
     rocm_backends = {}
@@ -183,6 +191,15 @@ def install(monkeypatch, rocm: bool = True):
                 def forward_decode(self, q, k, v, layer, forward_batch, save_kv_cache=True):
                     calls.append(f"{cls_name}.forward_decode (SGLang's own)")
                     raise AssertionError("the MAC decode path was expected")
+
+                def init_forward_metadata_capture_cuda_graph(self, bs, num_tokens, req_pool_indices, seq_lens,
+                                                             encoder_lens, forward_mode, spec_info):
+                    calls.append((f"{cls_name}.init_forward_metadata_capture_cuda_graph", bs))
+
+                def init_forward_metadata_replay_cuda_graph(self, bs, req_pool_indices, seq_lens, seq_lens_sum,
+                                                            encoder_lens, forward_mode, spec_info,
+                                                            seq_lens_cpu=None):
+                    calls.append((f"{cls_name}.init_forward_metadata_replay_cuda_graph", bs))
 
             RocmAttnBackend.__name__ = RocmAttnBackend.__qualname__ = cls_name
             return RocmAttnBackend

@@ -37,7 +37,10 @@ REQUIRED = {
 }
 ROCM = {f"sglang.srt.layers.attention.{m}:{c}.{attr}"
         for m, c in (("triton_backend", "TritonAttnBackend"), ("aiter_backend", "AiterAttnBackend"))
-        for attr in ("__init__", "init_forward_metadata", "forward_extend", "forward_decode")}
+        for attr in ("__init__", "init_forward_metadata", "forward_extend", "forward_decode",
+                     "init_forward_metadata_capture_cuda_graph", "init_forward_metadata_replay_cuda_graph")}
+GRAPH = {f"sglang.srt.layers.attention.flashinfer_backend:FlashInferAttnBackend.{attr}"
+         for attr in ("init_forward_metadata_capture_cuda_graph", "init_forward_metadata_replay_cuda_graph")}
 CHILD_SITES = {
     "sglang.srt.entrypoints.engine:run_scheduler_process",
     "sglang.srt.entrypoints.http_server:run_scheduler_process",
@@ -60,6 +63,7 @@ def test_install_wraps_every_serving_target(sg):
     done = set(hook_installer.install_hooks(strict=True))
     assert REQUIRED <= done, REQUIRED - done
     assert ROCM <= done, ROCM - done  # the ROCm attention backends this SGLang has
+    assert GRAPH <= done, GRAPH - done
     assert CHILD_SITES <= done, CHILD_SITES - done
     assert not any("qwen" in t for t in done)  # optional classes this SGLang lacks are skipped
     assert getattr(sg.LlamaAttention.forward, "__mac_attention_hooked__", False)
@@ -236,3 +240,44 @@ def test_model_forward_hook_passes_through(sg, monkeypatch):
     out = model.forward(None, torch.zeros(1, dtype=torch.long), types.SimpleNamespace(batch_size=1), input_embeds=x)
     assert torch.equal(out, x[:, :8])  # CPU tensors: SGLang's own forward, no MAC state
     assert "LlamaModel.forward (SGLang's own)" in sg.calls
+
+
+@pytest.mark.parametrize("backend_name", ["FlashInferAttnBackend", "TritonAttnBackend"])
+def test_decode_graph_replays_skip_backend_metadata_when_every_layer_is_mac(sg, monkeypatch, backend_name):
+    """flashinfer_hooks.py:660-700, :835-899: a decode graph captured with the
+    MAC step in every layer replays without the backend's metadata update;
+    one layer on the backend's own decode, a prefill graph, or the switch
+    off, and the backend's update runs."""
+    from mac_attention.integrations.sglang import persistent
+
+    monkeypatch.setenv("MAC_ATTENTION_ENABLE", "1")
+    hook_installer.install_hooks(strict=True)
+    backend = getattr(sg, backend_name)()
+    assert backend.mac_config.enable_mac
+    decode, prefill = sglang_standin.ForwardMode(True), sglang_standin.ForwardMode(False)
+    fb = types.SimpleNamespace(batch_size=4)
+    monkeypatch.setattr(persistent, "is_graph_capturing", lambda: True)
+
+    def capture(bs, mode, paths):
+        backend.init_forward_metadata_capture_cuda_graph(bs, bs, None, None, None, mode, None)
+        for p in paths:  # what each layer's decode hook captured
+            persistent.record_decode_graph_capture(backend, types.SimpleNamespace(batch_size=bs), persistent=p)
+
+    def replayed(bs, mode):
+        n = len(sg.calls)
+        backend.init_forward_metadata_replay_cuda_graph(bs, None, None, 0, None, mode, None)
+        return (f"{backend_name}.init_forward_metadata_replay_cuda_graph", bs) in sg.calls[n:]
+
+    capture(4, decode, [True] * 3)
+    assert not replayed(4, decode)  # every layer MAC: the backend's update is skipped
+    capture(8, decode, [True, False, True])
+    assert replayed(8, decode)  # a layer fell back: the backend's metadata is needed
+    assert replayed(16, decode)  # never captured here
+    capture(4, prefill, [True])
+    assert replayed(4, prefill)
+    capture(4, decode, [True, True])  # a new capture of the same size starts afresh
+    assert not replayed(4, decode)
+    monkeypatch.setenv("MAC_CUDAGRAPH_SKIP_FLASHINFER_REPLAY_METADATA", "0")
+    assert replayed(4, decode)
+    assert (f"{backend_name}.init_forward_metadata_capture_cuda_graph", 4) in sg.calls
+    del fb
