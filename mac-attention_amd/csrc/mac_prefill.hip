@@ -347,12 +347,40 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
 #pragma unroll
   for (int h = 0; h < 2; ++h) pv[h] = v_row(8 * quad + 4 * h + (col >> 2)) * 8 + 4 * (col & 3);
 
-  for (int task = blockIdx.x; task < total_tasks; task += gridDim.x) {
+  // Task order, by form (measured at config 4's prefill shape):
+  //  * windowed (plain, window_left >= 0): (KV head, head chunk) major, row
+  //    block minor, and within each full round of the grid XCD x (the
+  //    workgroups w with w % 8 == x, as the dispatcher deals them) takes the
+  //    x-th contiguous eighth of the round's tasks: the row blocks sharing a
+  //    K/V row run together under one L2 (row-block order dealt round-robin
+  //    put them on different XCDs and fetched each K/V row about four times);
+  //  * fused: row-block order (the KV heads of a row block together), XCD
+  //    eighths as above (2-3% faster than round-robin; head-major was slower);
+  //  * causal (window_left < 0): row-block order dealt round-robin.  Its
+  //    tasks grow with the row block, and a workgroup keeps its offset within
+  //    every round, so a head-major order would give some workgroups only the
+  //    longest tasks.
+  const int grid = gridDim.x;
+  const int eighth = grid / 8;
+  const int nblocks = s_boff[B];
+  const bool head_major = !kRectify && wl >= 0;
+  const bool by_xcd = (kRectify || wl >= 0) && grid % 8 == 0;
+  for (int task = blockIdx.x; task < total_tasks; task += grid) {
     __syncthreads();  // the previous task's waves are done with the tiles
-    const int blk = task / (Hkv * nchunks);
-    const int rem = task - blk * Hkv * nchunks;
-    const int hkv = rem / nchunks;
-    const int hg0 = kHeadsPerTask * (rem - hkv * nchunks) + HPW * wave;  // first head of this wave in the group
+    const int round0 = task - static_cast<int>(blockIdx.x);
+    const int t = (by_xcd && round0 + grid <= total_tasks)
+                      ? round0 + (static_cast<int>(blockIdx.x) % 8) * eighth + static_cast<int>(blockIdx.x) / 8
+                      : task;
+    int blk, hc;  // row block; KV head * nchunks + head chunk
+    if (head_major) {
+      hc = t / nblocks;
+      blk = t - hc * nblocks;
+    } else {
+      blk = t / (Hkv * nchunks);
+      hc = t - blk * Hkv * nchunks;
+    }
+    const int hkv = hc / nchunks;
+    const int hg0 = kHeadsPerTask * (hc - hkv * nchunks) + HPW * wave;  // first head of this wave in the group
     int lo = 0, hi = B - 1;  // request of this row block: largest b with s_boff[b] <= blk
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
