@@ -1472,6 +1472,8 @@ __global__ void __launch_bounds__(W * 64, W == kWaves ? 2 : 1) match_decide_kern
 struct GroupSpans {
   int sink_end, band_begin, new_end, kv_len;
   int chunk, n_sink, n_band, n_tail;
+  int n_full;  // band pieces of a full chunk (the first ones)
+  int piece2;  // length of the band pieces after them
 };
 
 __device__ __forceinline__ int group_tokens(int sink_end, int band_begin, int new_end, int kv_len) {
@@ -1486,6 +1488,31 @@ __device__ __forceinline__ int group_chunk(int tokens, int chunk, int cap) {
   return max(chunk, need);
 }
 
+// Band pieces: a band of at least kTierChunks full chunks ends in pieces of
+// half a chunk (a multiple of 64 tokens) covering its last quarter, when its
+// group's pieces still fit `cap` partial slots; other bands are cut into full
+// chunks and one shorter remainder.  Span attention fetches the full pieces
+// first and the shorter ones after them, so the last tasks of a step are
+// short and the workgroups end close together.
+constexpr int kTierChunks = 4;
+
+__device__ __forceinline__ void band_layout(GroupSpans& s, int cap) {
+  const int len = s.new_end - s.band_begin;
+  s.n_full = len / s.chunk;
+  s.piece2 = s.chunk;
+  s.n_band = ceil_div(len, s.chunk);
+  if (s.n_full >= kTierChunks) {
+    const int half = ((s.chunk >> 1) + 63) & ~63;
+    const int f = (len - len / 4) / s.chunk;
+    const int n = f + ceil_div(len - f * s.chunk, half);
+    if (s.n_sink + n + s.n_tail <= cap) {
+      s.n_full = f;
+      s.piece2 = half;
+      s.n_band = n;
+    }
+  }
+}
+
 __device__ __forceinline__ GroupSpans load_spans(const int32_t* rect_begin, const int32_t* rect_end,
                                                  const int32_t* tail_end, int g, int F, int chunk,
                                                  int cap) {
@@ -1496,16 +1523,13 @@ __device__ __forceinline__ GroupSpans load_spans(const int32_t* rect_begin, cons
   s.sink_end = min(F, s.new_end);
   s.chunk = group_chunk(group_tokens(s.sink_end, s.band_begin, s.new_end, s.kv_len), chunk, cap);
   s.n_sink = ceil_div(s.sink_end, s.chunk);
-  s.n_band = ceil_div(s.new_end - s.band_begin, s.chunk);
   s.n_tail = ceil_div(s.kv_len - s.new_end, s.chunk);
+  band_layout(s, cap);
   return s;
 }
 
-// Band pieces of a group that span a full chunk (the first ones; only the
-// last band piece can be shorter).
-__device__ __forceinline__ int full_band_pieces(const GroupSpans& s) {
-  return (s.new_end - s.band_begin) / s.chunk;
-}
+// Band pieces of a group that span a full chunk (the first ones).
+__device__ __forceinline__ int full_band_pieces(const GroupSpans& s) { return s.n_full; }
 
 // A group of at most fuse_tokens tokens is short: its whole computation is
 // short_group, wherever it runs (the same rule as match_decide's).
@@ -1744,8 +1768,10 @@ __device__ __forceinline__ TaskInfo decode_task(const AttnParams& p, const int* 
     ti.a = ti.j * sp.chunk;
     ti.b = min(ti.a + sp.chunk, sp.sink_end);
   } else if (ti.j < sp.n_sink + sp.n_band) {
-    ti.a = sp.band_begin + (ti.j - sp.n_sink) * sp.chunk;
-    ti.b = min(ti.a + sp.chunk, sp.new_end);
+    const int k2 = ti.j - sp.n_sink;  // band piece: n_full of a chunk, then of piece2
+    ti.a = k2 < sp.n_full ? sp.band_begin + k2 * sp.chunk
+                          : sp.band_begin + sp.n_full * sp.chunk + (k2 - sp.n_full) * sp.piece2;
+    ti.b = min(ti.a + (k2 < sp.n_full ? sp.chunk : sp.piece2), sp.new_end);
     ti.band = true;
   } else {
     ti.a = sp.new_end + (ti.j - sp.n_sink - sp.n_band) * sp.chunk;
@@ -2016,9 +2042,17 @@ __global__ void __launch_bounds__(kBlock) merge_write_kernel(MergeParams p) {
   const int chunk = group_chunk(tokens, plan_chunk, p.cap);  // as span_attention's plan derives it
   const bool ready = request_ready(p.cache_ready, p.cache_epoch, p.request_epoch, req, p.s.R);
   const int dest = P % M;
-  const int n_sink = ceil_div(sink_end, chunk);
-  const int n_band = ceil_div(new_end - band_begin, chunk);
-  const int n_tail = ceil_div(kv_len - new_end, chunk);
+  // the group's pieces, as span_attention's plan cuts them
+  GroupSpans sp;
+  sp.sink_end = sink_end;
+  sp.band_begin = band_begin;
+  sp.new_end = new_end;
+  sp.kv_len = kv_len;
+  sp.chunk = chunk;
+  sp.n_sink = ceil_div(sink_end, chunk);
+  sp.n_tail = ceil_div(kv_len - new_end, chunk);
+  band_layout(sp, p.cap);
+  const int n_sink = sp.n_sink, n_band = sp.n_band, n_tail = sp.n_tail;
 
   __shared__ float s_o[2][kWaves][kHeadDim];
   __shared__ float s_l[2][kWaves];
