@@ -486,6 +486,32 @@ def _time_us(torch, fn, reps):
     return a.elapsed_time(b) * 1e3 / reps
 
 
+def _time_graph_us(torch, fn, per_graph=20, replays=5):
+    """GPU µs per fn() call: per_graph calls captured in one graph, replayed
+    `replays` times between HIP events (how serving runs these ops, under
+    graph capture; an eager Python call of a few-µs kernel measures the host's
+    call overhead instead)."""
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(per_graph):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(replays):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    del graph
+    return a.elapsed_time(b) * 1e3 / (replays * per_graph)
+
+
 def measure_aux(torch):
     """The rows beside the decode step, at BASELINE config 4's prefill shape:
     64 requests, one 8192-token chunk each, GQA-8, S = 256, ring 32.
@@ -538,7 +564,8 @@ def measure_aux(torch):
         merge.mac_update_then_downdate_bf16_inplace(o_full, lse_full, wo, wl)
         cache.mac_prefill_update_cache(qc, ac, lc, rl[:B], req, src_q, wo, wl, qo, lens, M, hq, D, empty)
 
-    fused_us = _time_us(torch, fused, 20)
+    fused_us = _time_graph_us(torch, fused)
+    fused_eager_us = _time_us(torch, fused, 20)
     comp_us = _time_us(torch, composed, 5)
     # the window attention of every row on its own (the dominant call of the
     # three): row i of a chunk attends keys max(0, i - S + 1) .. i.  Per launch
@@ -554,8 +581,8 @@ def measure_aux(torch):
     hbm_s, mfma_s = win_bytes / 8e12, win_flop / 2.5e15
     # mac_prefill_update_cache alone (the last M rows of every chunk into the
     # ring): q and attention rows (2 * Hq * D bf16) + lse read and written per row
-    upd_us = _time_us(torch, lambda: cache.mac_prefill_update_cache(qc, ac, lc, rl[:B], req, src_q, wo, wl, qo, lens,
-                                                                    M, hq, D, empty), 20)
+    upd_us = _time_graph_us(torch, lambda: cache.mac_prefill_update_cache(qc, ac, lc, rl[:B], req, src_q, wo, wl, qo, lens,
+                                                                    M, hq, D, empty))
     upd_bytes = 2 * B * M * hq * (2 * 2 * D + 4)
     # algorithmic bytes of the fused op: per (request, kv head) the K/V rows
     # of the window of the kept rows (M + S - 1 tokens), per kept row and
@@ -567,7 +594,10 @@ def measure_aux(torch):
         "workload": f"B={B} requests x {chunk}-token chunk, GQA-8 (Hq={hq}, Hkv={hkv}), S={S}, ring={M}",
         "fused_us": round(fused_us, 2), "reference_three_calls_us": round(comp_us, 2),
         "speedup": round(comp_us / fused_us, 1), "fused_algorithmic_bytes": fused_bytes,
-        "fused_gbs": round(fused_bytes / fused_us / 1e3, 1)},
+        "fused_gbs": round(fused_bytes / fused_us / 1e3, 1),
+        "fused_eager_call_us": round(fused_eager_us, 2),
+        "timing": "fused_us: graph-replayed calls (as under serving's graph capture); fused_eager_call_us: "
+                  "back-to-back eager calls from Python"},
         "prefill_update_cache": {
             "workload": f"B={B} batch rows x {chunk} source rows, ring={M}, Hq={hq}",
             "us": round(upd_us, 2), "algorithmic_bytes": upd_bytes,
@@ -593,11 +623,15 @@ def measure_aux(torch):
     cs = torch.cat([ang.cos(), ang.sin()], dim=1).contiguous()
     pos = torch.randint(0, 131072, (n,), device=dev, generator=g)
     loc = torch.randperm(pool, device=dev, generator=g)[:n].contiguous()
-    rope_us = _time_us(torch, lambda: rope.mac_decode_rope_preserve_q_bf16(qv, kv_, vv, q_pre, kb, vb, cs, pos, loc,
-                                                                             D, True), 50)
+    rope_call = lambda: rope.mac_decode_rope_preserve_q_bf16(qv, kv_, vv, q_pre, kb, vb, cs, pos, loc, D, True)
+    rope_us = _time_graph_us(torch, rope_call)
+    rope_eager_us = _time_us(torch, rope_call, 50)
     rope_bytes = n * ((hq4 + 2 * hkv4) * D * 2 + (2 * hq4 + 3 * hkv4) * D * 2)
     out["decode_rope"] = {"workload": f"{n} decode tokens, Hq={hq4}, Hkv={hkv4}, rotary_dim {D}, NeoX",
-                          "us": round(rope_us, 2), "algorithmic_bytes": rope_bytes}
+                          "us": round(rope_us, 2), "algorithmic_bytes": rope_bytes,
+                          "eager_call_us": round(rope_eager_us, 2),
+                          "timing": "us: graph-replayed calls; eager_call_us: back-to-back eager calls from "
+                                    "Python (host-bound for this few-µs kernel)"}
     return out
 
 
