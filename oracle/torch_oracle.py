@@ -85,7 +85,8 @@ def bf16(x: torch.Tensor) -> torch.Tensor:
 def decode_request(*, q_post: torch.Tensor, q_pre: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                    r2t_row: torch.Tensor, P: int, cur_loc: int, ring_q: torch.Tensor, ring_o: torch.Tensor,
                    ring_lse: torch.Tensor, params: StepParams, ready: bool = True) -> dict:
-    """One request's decode step.  q_post/q_pre [Hq, D]; k/v [pool, Hkv, D];
+    """One request's decode step.  q_post/q_pre [Hq, D]; k/v [pool, Hkv, D]
+    (float32, or bf16, whose gathered rows are widened to float32);
     r2t_row [>= P] pool rows; ring_q/ring_o [M, Hq, D], ring_lse [M, Hq] (the
     request's ring, updated in place at slot P % M when ready).  Returns the
     head decisions, group modes and the output (o [Hq, D], lse [Hq])."""
@@ -140,7 +141,7 @@ def decode_request(*, q_post: torch.Tensor, q_pre: torch.Tensor, k: torch.Tensor
         toks = torch.cat([torch.arange(0, sink_end), torch.arange(rb, new_end), torch.arange(new_end, P + 1)])
         is_band = (toks >= rb) & (toks < new_end)
         phys = torch.where(toks == P, torch.tensor(cur_loc), r2t_row[torch.clamp(toks, max=max(P - 1, 0))].long())
-        kg, vg_ = k[phys, g], v[phys, g]  # [T, D]
+        kg, vg_ = k[phys, g].float(), v[phys, g].float()  # [T, D] (bf16 pools: only the rows used are widened)
         heads = slice(g * G, (g + 1) * G)
         sc = (q_post[heads] @ kg.T) * params.sm_scale  # [G, T]
         band_ok = is_band[None, :] & (toks[None, :] >= rect_start[heads, None])

@@ -15,6 +15,7 @@ as sqrt(1-eps^2) q + eps N(0,1) with eps = 0.3 (hit) or 0.9 (miss).
 """
 
 import math
+import os
 import time
 
 import numpy as np
@@ -216,9 +217,63 @@ def config3(request):
     dev = syn.device_case(torch, batch=64, hq=32, hkv=hkv, ctx=130048, capacity=32, seed=3)
     pristine = {k: dev[k].clone() for k in RING_ROWS}
     torch.cuda.synchronize()
-    yield hkv, dev, pristine
-    del dev, pristine
+    # the bf16 K/V pools on the host, for the all-request check (17 or 34 GB)
+    host = dict(k=dev["k"].cpu(), v=dev["v"].cpu())
+    yield hkv, dev, pristine, host
+    del dev, pristine, host
     torch.cuda.empty_cache()
+
+
+def _check_all_torch(dev, host, ring0, out, out_lse, ws, S, what, tol=1e-2):
+    """Every request of a step against the FP32 torch restatement of the
+    oracle (oracle/torch_oracle.py, pinned against the C oracle in
+    test_torch_oracle.py), from the ring as it was before the step: head
+    decisions, matched positions and group modes exact (heads whose best
+    distance is within 1e-6 relative of the threshold distance logged and
+    excused), out and the ring row within tol relative L2, ring q bit for
+    bit.  Request n's K/V rows are rows [n kv_len, (n + 1) kv_len) of the
+    pools (device_case's layout)."""
+    from oracle import torch_oracle as tor
+
+    torch.set_num_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    n_req, hq, d = dev["q_post"].shape
+    kv_len = int(dev["req_to_token"].shape[1])
+    past = [int(x) for x in dev["past_lens"].cpu().tolist()]
+    assert dev["req_ids"].cpu().tolist() == list(range(n_req)), "expects request n in ring row n"
+    qpost, qpre = dev["q_post"].float().cpu(), dev["q_pre"].float().cpu()
+    ring_q, ring_o, ring_l = (ring0["query_cache"].float(), ring0["attn_cache"].float(),
+                              ring0["lse_cache"].clone())
+    params = tor.StepParams(semantic_pos_ahead=S, front_sink_tokens=0, sm_scale=1.0 / math.sqrt(d))
+    thr_d = 2.0 * d * (1.0 - params.threshold) ** 2
+    hit_g, pos_g, mode_g = _np(ws[3]), _np(ws[5]), _np(ws[15])
+    out_g, lse_g = _np(out), _np(out_lse)
+    rq_g, ro_g, rl_g = (syn.to_bits(_np(dev["query_cache"])), _np(dev["attn_cache"]), _np(dev["lse_cache"]))
+    t0, excused, worst = time.time(), 0, 0.0
+    for n in range(n_req):
+        tag = f"{what} request {n} (torch oracle)"
+        rows = slice(n * kv_len, (n + 1) * kv_len)
+        r = tor.decode_request(q_post=qpost[n], q_pre=qpre[n], k=host["k"][rows], v=host["v"][rows],
+                               r2t_row=torch.arange(kv_len), P=past[n], cur_loc=past[n], ring_q=ring_q[n],
+                               ring_o=ring_o[n], ring_lse=ring_l[n], params=params)
+        near = (r["best_dist"] - thr_d).abs().numpy() <= 1e-6 * thr_d
+        if near.any():  # a decision on the threshold: logged, not compared
+            excused += 1
+            print(f"{tag}: heads {np.nonzero(near)[0].tolist()} within 1e-6 of the threshold", flush=True)
+            continue
+        np.testing.assert_array_equal(hit_g[n], r["head_hit"].numpy(), err_msg=f"{tag} head_hit")
+        np.testing.assert_array_equal(pos_g[n], r["head_match_pos"].numpy(), err_msg=f"{tag} match_pos")
+        np.testing.assert_array_equal(mode_g[n], r["group_mode"].numpy(), err_msg=f"{tag} group_mode")
+        err = rel_l2(out_g[n], r["out"].numpy())
+        worst = max(worst, err)
+        assert err < tol, f"{tag} out rel_l2 {err:.3e}"
+        assert_close(lse_g[n], r["out_lse"].numpy(), 2e-2, f"{tag} out_lse")
+        dest = past[n] % ring_q.shape[1]
+        np.testing.assert_array_equal(rq_g[n, dest], syn.to_bits(ring_q[n, dest].numpy()), err_msg=f"{tag} ring q")
+        exp_o = ring_o[n, dest].numpy()
+        assert rel_l2(ro_g[n, dest], exp_o) < tol or np.abs(exp_o).max() == 0, f"{tag} ring o"
+        assert_close(rl_g[n, dest], ring_l[n, dest].numpy(), 2e-2, f"{tag} ring lse")
+    print(f"{what}: all {n_req} requests against the torch oracle in {time.time() - t0:.1f}s "
+          f"(worst out rel_l2 {worst:.2e}, {excused} excused)", flush=True)
 
 
 def _restore(dev, pristine):
@@ -251,7 +306,7 @@ def _bench_step(ext, dev, pristine, hit, S, max_context, ws=None):
                 bench=dict(bench_mode=1, bench_hit_rate=hit, bench_match_lag_mean=64.0))
 
 
-def _timed_path_point(ext, dev, pristine, hit, check, what, S=256, max_context=131072):
+def _timed_path_point(ext, dev, pristine, hit, check, what, S=256, max_context=131072, host=None):
     """The exact path bench.py times at one sweep point, with its default
     short-group rule in its steady state: a warm-up step on the workspace
     leaves the counts the rule reads, as the bench's warm-up replays do.
@@ -270,9 +325,12 @@ def _timed_path_point(ext, dev, pristine, hit, check, what, S=256, max_context=1
     syn.plant_synthetic_hits(torch, dev, hit_rate=hit, bench_mode=1, semantic_pos_ahead=S)
     sub = host_subset(torch, dev, check, semantic_pos_ahead=S)
     res = oracle_run(sub)
+    ring0 = {k: dev[k].cpu() for k in RING_ROWS} if host is not None else None
     out, out_lse, ws = _run(ext, dev, S=S, F=0, max_context=max_context, ws=ws)
     torch.cuda.synchronize()
     _check_subset(dev, out, out_lse, ws, sub, res, check, what)
+    if host is not None:
+        _check_all_torch(dev, host, ring0, out, out_lse, ws, S, what)
     assert int(ws[3].sum()) == round(hit * n * hq)
     ng = n * hkv
     fused = _np(ws[16])[ng:2 * ng].reshape(n, hkv) != 0
@@ -296,11 +354,12 @@ def _timed_path_point(ext, dev, pristine, hit, check, what, S=256, max_context=1
 def test_config3_hit_sweep(ext, config3, hit):
     """Every hit ratio bench.py times at the headline shape, GQA-4 and GQA-8,
     through the path the bench times (its default short-group rule in steady
-    state, see _timed_path_point): the real scan against the oracle on two
-    requests, then the override bit for bit on all 64."""
-    hkv, dev, pristine = config3
+    state, see _timed_path_point): the real scan against the C oracle on two
+    requests and against its FP32 torch restatement on all 64, then the
+    override bit for bit on all 64."""
+    hkv, dev, pristine, host = config3
     print(f"config3 sweep hkv={hkv} hit={hit}", flush=True)
-    _timed_path_point(ext, dev, pristine, hit, [0, 37], f"config3 hkv {hkv} hit {hit}")
+    _timed_path_point(ext, dev, pristine, hit, [0, 37], f"config3 hkv {hkv} hit {hit}", host=host)
 
 
 @pytest.fixture(scope="module", params=[8, 4], ids=["gqa4", "gqa8"])
@@ -310,8 +369,9 @@ def ring2048(request):
     dev = syn.device_case(torch, batch=64, hq=32, hkv=hkv, ctx=126976, capacity=2048, seed=0)
     pristine = {k: dev[k].clone() for k in RING_ROWS}
     torch.cuda.synchronize()
-    yield hkv, dev, pristine
-    del dev, pristine
+    host = dict(k=dev["k"].cpu(), v=dev["v"].cpu())  # for the all-request check
+    yield hkv, dev, pristine, host
+    del dev, pristine, host
     torch.cuda.empty_cache()
 
 
@@ -319,11 +379,12 @@ def ring2048(request):
 def test_reference_shape_hit_sweep(ext, ring2048, hit):
     """Every hit ratio of bench.py's reference_shape leg (ring 2048: the
     range-split, probe-pruned scan) through the path the bench times: scan
-    decisions and values against the oracle on two requests, the override's
-    decisions, placement and bits equal to the scan's."""
-    hkv, dev, pristine = ring2048
+    decisions and values against the C oracle on two requests and against its
+    FP32 torch restatement on all 64, the override's decisions, placement and
+    bits equal to the scan's."""
+    hkv, dev, pristine, host = ring2048
     print(f"ring2048 hkv={hkv} hit={hit}", flush=True)
-    _timed_path_point(ext, dev, pristine, hit, [5, 60], f"ring2048 hkv {hkv} hit {hit}")
+    _timed_path_point(ext, dev, pristine, hit, [5, 60], f"ring2048 hkv {hkv} hit {hit}", host=host)
 
 
 # ------------------------------------------------------------- config 4 ----

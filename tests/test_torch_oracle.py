@@ -71,3 +71,26 @@ def test_torch_restatement_readiness_gate():
         assert rel_l2(r["out"].numpy(), bits(exp.out[n])) < 2e-3
     np.testing.assert_array_equal(ring_o[1].numpy(), bits(c.attn_cache[1]) if c.attn_cache.dtype == np.uint16
                                   else c.attn_cache[1])
+
+
+def test_torch_restatement_takes_bf16_pools():
+    """K/V pools passed as bf16 tensors (only the gathered rows are widened)
+    give the same results as the same values passed as float32."""
+    c = syn.random_case(batch=2, hq=32, hkv=8, kv_lens=[700, 1500], capacity=32, semantic_pos_ahead=64,
+                        front_sink_tokens=0, hit_rate=0.5, match_lag=16, seed=17)
+    f = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))  # noqa: E731
+    params = tor.StepParams(semantic_pos_ahead=64, threshold=c.threshold, sm_scale=c.sm_scale)
+    for n in range(2):
+        req = int(c.req_ids[n])
+        kw = dict(q_post=f(c.q_post[n]), q_pre=f(c.q_pre[n]),
+                  r2t_row=torch.from_numpy(c.req_to_token[req].astype(np.int64)), P=int(c.past_lens[n]),
+                  cur_loc=int(c.out_cache_loc[n]), params=params)
+        rings = [(f(c.query_cache[req]).clone(), f(c.attn_cache[req]).clone(), f(c.lse_cache[req]).clone())
+                 for _ in range(2)]  # (from_numpy shares the case's arrays; the step writes its ring row)
+        a = tor.decode_request(k=f(c.k), v=f(c.v), ring_q=rings[0][0], ring_o=rings[0][1], ring_lse=rings[0][2], **kw)
+        b = tor.decode_request(k=f(c.k).to(torch.bfloat16), v=f(c.v).to(torch.bfloat16), ring_q=rings[1][0],
+                               ring_o=rings[1][1], ring_lse=rings[1][2], **kw)
+        for key in ("head_hit", "head_match_pos", "group_mode", "out", "out_lse"):
+            assert torch.equal(a[key], b[key]), key
+        for x, y in zip(rings[0], rings[1]):
+            assert torch.equal(x, y)
