@@ -166,7 +166,8 @@ def test_config1_llama8b_hit_sweep(ext, hit):
 @pytest.mark.parametrize("hit", [0.0, 0.25, 0.5, 0.75, 0.9, 1.0])
 def test_config2_qwen3_gqa8(ext, hit):
     """B=16, GQA-8 (Hkv=4), context 65536, match positions uniform in
-    [0.5 ctx, ctx-512), F=128; two requests checked against the oracle."""
+    [0.5 ctx, ctx-512), F=128; two requests checked against the C oracle, all
+    16 against its FP32 torch restatement."""
     rng = np.random.default_rng(200 + int(hit * 10))
     b, m, ctx, S, F = 16, 32768, 65536, 256, 128
     dev = syn.device_ragged_case(torch, kv_lens=[ctx + 1] * b, hq=32, hkv=4, capacity=m, seed=2)
@@ -177,9 +178,12 @@ def test_config2_qwen3_gqa8(ext, hit):
     check = [0, 11]
     sub = host_subset(torch, dev, check, semantic_pos_ahead=S, front_sink_tokens=F)
     res = oracle_run(sub)
+    ring0 = {k: dev[k].cpu() for k in RING_ROWS}
     out, out_lse, ws = _run(ext, dev, S=S, F=F, max_context=ctx + 8)
     torch.cuda.synchronize()
     _check_subset(dev, out, out_lse, ws, sub, res, check, f"config2 hit {hit}")
+    _check_all_torch(dev, dict(k=dev["k"].cpu(), v=dev["v"].cpu()), ring0, out, out_lse, ws, S,
+                     f"config2 hit {hit}", F=F)
 
 
 # ------------------------------------------------------------- config 3 ----
@@ -224,37 +228,47 @@ def config3(request):
     torch.cuda.empty_cache()
 
 
-def _check_all_torch(dev, host, ring0, out, out_lse, ws, S, what, tol=1e-2):
+def _check_all_torch(dev, host, ring0, out, out_lse, ws, S, what, F=0, tol=1e-2):
     """Every request of a step against the FP32 torch restatement of the
     oracle (oracle/torch_oracle.py, pinned against the C oracle in
-    test_torch_oracle.py), from the ring as it was before the step: head
-    decisions, matched positions and group modes exact (heads whose best
-    distance is within 1e-6 relative of the threshold distance logged and
-    excused), out and the ring row within tol relative L2, ring q bit for
-    bit.  Request n's K/V rows are rows [n kv_len, (n + 1) kv_len) of the
-    pools (device_case's layout)."""
+    test_torch_oracle.py), from the ring as it was before the step (ring0,
+    host tensors): head decisions, matched positions and group modes exact
+    (heads whose best distance is within 1e-6 relative of the threshold
+    distance logged and excused), out and the ring row within tol relative
+    L2, ring q bit for bit, and the ring untouched where the readiness gate
+    closes.  Request n's K/V rows must be one contiguous run of the pools
+    (the synthetic cases' layout; checked)."""
     from oracle import torch_oracle as tor
 
     torch.set_num_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
     n_req, hq, d = dev["q_post"].shape
-    kv_len = int(dev["req_to_token"].shape[1])
     past = [int(x) for x in dev["past_lens"].cpu().tolist()]
     assert dev["req_ids"].cpu().tolist() == list(range(n_req)), "expects request n in ring row n"
+    r2t = dev["req_to_token"].cpu()
+    ocl = [int(x) for x in dev["out_cache_loc"].cpu().tolist()]
+    ready = [True] * n_req
+    if dev["cache_ready"].numel() > 0:
+        ready = [bool(x) for x in dev["cache_ready"].cpu().tolist()]
+        if dev["cache_epoch"].numel() > 0 and dev["request_epoch"].numel() > 0:
+            same = (dev["cache_epoch"] == dev["request_epoch"]).cpu().tolist()
+            ready = [r and bool(e) for r, e in zip(ready, same)]
     qpost, qpre = dev["q_post"].float().cpu(), dev["q_pre"].float().cpu()
-    ring_q, ring_o, ring_l = (ring0["query_cache"].float(), ring0["attn_cache"].float(),
-                              ring0["lse_cache"].clone())
-    params = tor.StepParams(semantic_pos_ahead=S, front_sink_tokens=0, sm_scale=1.0 / math.sqrt(d))
+    params = tor.StepParams(semantic_pos_ahead=S, front_sink_tokens=F, sm_scale=1.0 / math.sqrt(d))
     thr_d = 2.0 * d * (1.0 - params.threshold) ** 2
     hit_g, pos_g, mode_g = _np(ws[3]), _np(ws[5]), _np(ws[15])
     out_g, lse_g = _np(out), _np(out_lse)
-    rq_g, ro_g, rl_g = (syn.to_bits(_np(dev["query_cache"])), _np(dev["attn_cache"]), _np(dev["lse_cache"]))
     t0, excused, worst = time.time(), 0, 0.0
     for n in range(n_req):
         tag = f"{what} request {n} (torch oracle)"
-        rows = slice(n * kv_len, (n + 1) * kv_len)
+        kv = past[n] + 1
+        base = int(r2t[n, 0])
+        assert torch.equal(r2t[n, :past[n]], torch.arange(base, base + past[n], dtype=r2t.dtype)), tag
+        assert ocl[n] == base + past[n], tag
+        rows = slice(base, base + kv)
+        rq, ro, rl = ring0["query_cache"][n].float(), ring0["attn_cache"][n].float(), ring0["lse_cache"][n].clone()
         r = tor.decode_request(q_post=qpost[n], q_pre=qpre[n], k=host["k"][rows], v=host["v"][rows],
-                               r2t_row=torch.arange(kv_len), P=past[n], cur_loc=past[n], ring_q=ring_q[n],
-                               ring_o=ring_o[n], ring_lse=ring_l[n], params=params)
+                               r2t_row=torch.arange(kv), P=past[n], cur_loc=past[n], ring_q=rq, ring_o=ro,
+                               ring_lse=rl, params=params, ready=ready[n])
         near = (r["best_dist"] - thr_d).abs().numpy() <= 1e-6 * thr_d
         if near.any():  # a decision on the threshold: logged, not compared
             excused += 1
@@ -267,11 +281,18 @@ def _check_all_torch(dev, host, ring0, out, out_lse, ws, S, what, tol=1e-2):
         worst = max(worst, err)
         assert err < tol, f"{tag} out rel_l2 {err:.3e}"
         assert_close(lse_g[n], r["out_lse"].numpy(), 2e-2, f"{tag} out_lse")
-        dest = past[n] % ring_q.shape[1]
-        np.testing.assert_array_equal(rq_g[n, dest], syn.to_bits(ring_q[n, dest].numpy()), err_msg=f"{tag} ring q")
-        exp_o = ring_o[n, dest].numpy()
-        assert rel_l2(ro_g[n, dest], exp_o) < tol or np.abs(exp_o).max() == 0, f"{tag} ring o"
-        assert_close(rl_g[n, dest], ring_l[n, dest].numpy(), 2e-2, f"{tag} ring lse")
+        dest = past[n] % rq.shape[0]
+        gq = syn.to_bits(_np(dev["query_cache"][n, dest]))
+        go, gl = _np(dev["attn_cache"][n, dest]), _np(dev["lse_cache"][n, dest])
+        np.testing.assert_array_equal(gq, syn.to_bits(rq[dest].numpy()), err_msg=f"{tag} ring q")
+        exp_o = ro[dest].numpy()
+        if ready[n]:
+            assert rel_l2(go, exp_o) < tol or np.abs(exp_o).max() == 0, f"{tag} ring o"
+            assert_close(gl, rl[dest].numpy(), 2e-2, f"{tag} ring lse")
+        else:  # the gate closed: the row keeps its bits
+            np.testing.assert_array_equal(syn.to_bits(go), syn.to_bits(exp_o), err_msg=f"{tag} ring o (gated)")
+            np.testing.assert_array_equal(gl.view(np.int32), rl[dest].numpy().view(np.int32),
+                                          err_msg=f"{tag} ring lse (gated)")
     print(f"{what}: all {n_req} requests against the torch oracle in {time.time() - t0:.1f}s "
           f"(worst out rel_l2 {worst:.2e}, {excused} excused)", flush=True)
 
@@ -394,7 +415,9 @@ def test_config4_ragged_serving_mix(ext, cache_ext):
     """B=64 GQA-8, contexts log-uniform in [16K, 127K], F=128; 20% of the
     requests not ready and 10% with an epoch mismatch (both must run exact
     attention and leave their ring rows alone), hit 0.8 among ready ones; a
-    mac_prefill_update_cache call on 8192-row chunks between two decode steps."""
+    mac_prefill_update_cache call on 8192-row chunks between two decode steps.
+    Four requests (three in step 2) against the C oracle, all 64 in both steps
+    against its FP32 torch restatement."""
     rng = np.random.default_rng(4)
     b, m, S, F = 64, 32, 256, 128
     kv_lens = np.exp(rng.uniform(np.log(16384), np.log(130048), b)).astype(int) + 1
@@ -422,9 +445,12 @@ def test_config4_ragged_serving_mix(ext, cache_ext):
     # step 1
     sub1 = host_subset(torch, dev, check, semantic_pos_ahead=S, front_sink_tokens=F)
     res1 = oracle_run(sub1)
+    host = dict(k=dev["k"].cpu(), v=dev["v"].cpu())
+    ring0 = {k: dev[k].cpu() for k in RING_ROWS}
     out, out_lse, ws = _run(ext, dev, S=S, F=F, max_context=131072)
     torch.cuda.synchronize()
     _check_subset(dev, out, out_lse, ws, sub1, res1, check, "config4 step1")
+    _check_all_torch(dev, host, ring0, out, out_lse, ws, S, "config4 step1", F=F)
     after = _np(dev["attn_cache"])
     for n in not_ready | mismatch:
         np.testing.assert_array_equal(after[n], before[n])
@@ -455,9 +481,11 @@ def test_config4_ragged_serving_mix(ext, cache_ext):
     check2 = [int(order[40]), int(order[50]), int(order[63])]
     sub2 = host_subset(torch, dev, check2, semantic_pos_ahead=S, front_sink_tokens=F)
     res2 = oracle_run(sub2)
+    ring0 = {k: dev[k].cpu() for k in RING_ROWS}
     out2, out_lse2, ws2 = _run(ext, dev, S=S, F=F, max_context=131072, ws=ws)
     torch.cuda.synchronize()
     _check_subset(dev, out2, out_lse2, ws2, sub2, res2, check2, "config4 step2")
+    _check_all_torch(dev, host, ring0, out2, out_lse2, ws2, S, "config4 step2", F=F)
 
 
 def test_config4_graph_replays_follow_host_flips(ext, cache_ext):
