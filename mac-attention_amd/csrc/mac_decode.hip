@@ -1647,6 +1647,15 @@ __device__ void plan_tasks(const AttnParams& p, int* s_off, int* s_tmp, int& tot
   int chunk = static_cast<int>((tok + target_tasks - 1) / target_tasks);
   chunk = ceil_div(max(chunk, p.min_chunk), 64) * 64;
   chunk = min(chunk, kMaxChunk);
+  if (tok == 0) {  // nothing to attend (only workgroup 0 is here): publish an empty plan
+    if (tid == 0) {
+      p.task_counts[0] = 0;
+      p.task_counts[4] = chunk;
+    }
+    total_tasks_out = 0;
+    chunk_out = chunk;
+    return;
+  }
   // Offset table: entry b of class A (s_off) / class B (s_offb) is the
   // first task of bucket b (groups b gpb .. b gpb + gpb - 1; one group per
   // bucket unless the batch has more groups than the table has entries).
@@ -1887,7 +1896,7 @@ __global__ void __launch_bounds__(kBlock, 2) span_attention_mfma_kernel(AttnPara
   plan_tasks(p, s_off, s_tmp, total_tasks, chunk, active_wgs);
   if (p.phase_cycles != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
     p.phase_cycles[3] = static_cast<int64_t>(wall_clock64());
-  if (static_cast<int>(blockIdx.x) >= active_wgs) return;
+  if (static_cast<int>(blockIdx.x) >= active_wgs || total_tasks == 0) return;
 
   __shared__ int s_task;
   for (int t = next_task(p, s_task); t < total_tasks; t = next_task(p, s_task)) {
