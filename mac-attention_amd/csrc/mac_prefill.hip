@@ -583,13 +583,17 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
           for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) sv[4 * t + r] = c4[h][t][r];
+          // lazy move of the reference point: p <= 2^8 stays exact in fp32.
+          // The vote runs on each lane's own maximum (the four lanes of a
+          // row share m[h], so any lane exceeding it is the row maximum
+          // exceeding it): the row reduction is only needed when the point
+          // moves.  On the first block every present key moves it (acc and
+          // l are still zero, and the rescale by 2^(kNegBig - m_new) = 0
+          // leaves them zero).
           float bmax = max8_nonan(sv);
-          bmax = quad_max(bmax);
-          // lazy move of the reference point: p <= 2^8 stays exact in fp32;
-          // on the first block acc and l are still zero, nothing to rescale
-          // (a select, so that the branch below is the only one)
-          m[h] = fresh ? max3_nonan(m[h], bmax, bmax) : m[h];
-          if (__any(bmax * p.q_scale > m[h] * p.q_scale + 8.0f)) {
+          const float vote = fresh ? -INFINITY : m[h] * p.q_scale + 8.0f;
+          if (__any(bmax * p.q_scale > vote)) {
+            bmax = quad_max(bmax);
             const float m_new = max3_nonan(m[h], bmax, bmax);
             const float alpha = fast_exp2((m[h] - m_new) * p.q_scale);
             m[h] = m_new;
@@ -603,7 +607,7 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const float pe = fast_exp2(fmaf(sv[e], p.q_scale, mo));
-            if (!kRectify) psum += pe;
+            if (!kRectify) psum = e == 0 ? pe : psum + pe;  // (0 + pe = pe: no add)
             pb[h][e] = static_cast<__bf16>(pe);
             // The fused form also feeds the bf16 rounding residual of P
             // through a second MFMA (P = hi + lo, ~16 significant bits): the
