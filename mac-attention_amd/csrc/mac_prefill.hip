@@ -318,6 +318,10 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
   const int Hq = p.Hq, Hkv = p.Hkv;
   const int G = Hq / Hkv;
   constexpr int kHeadsPerTask = 4 * HPW;
+  // fused form: the full state's o rows of the task (row r, task head hh,
+  // 16-byte part c at r * kOfRow + 16 hh + c; rows padded by one part)
+  constexpr int kOfRow = kHeadsPerTask * 16 + 1;
+  __shared__ uint4 s_of[kRectify ? kRows * kOfRow : 1];
   const int nchunks = ceil_div(G, kHeadsPerTask);
   const int total_tasks = s_boff[B] * Hkv * nchunks;
   const uint32_t row_bytes = static_cast<uint32_t>(Hkv) * kHeadDim * 2;  // one pool row of K or V
@@ -411,6 +415,48 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
       for (int i = 0; i < HPW; ++i) lse_full[i] = p.lse_full[grow * Hq + hkv * G + min(hg0 + i, G - 1)];
     }
     const int nheads = __builtin_amdgcn_readfirstlane(max(0, min(HPW, G - hg0)));  // heads this wave computes
+    // Fused form: the task's pre-RoPE query rows (copied into the ring with
+    // the q_post NaN marker) and the full state's o rows (into s_of for the
+    // epilogue) -- 16 rows x kHeadsPerTask heads x 16 parts of 16 bytes,
+    // kHeadsPerTask rounds of one part per thread -- move with the K/V
+    // stream, so that this traffic overlaps the compute-bound key blocks
+    // instead of adding an HBM-bound load round after them (every workgroup
+    // runs its task in step with the others).  A round's loads go out behind
+    // a block's K/V loads; its query part is stored when the next block is
+    // staged, and its o part is copied straight into LDS
+    // (global_load_lds_dwordx4: no registers; waited for at the next
+    // block's staging and barrier).  Round k, thread t: row (16 k + t / 16) /
+    // kHeadsPerTask, task head (t / 16) % kHeadsPerTask, part t % 16 -- the
+    // 64 lanes of a wave take 4 heads x 16 parts of one row, a contiguous
+    // 1 KiB run of s_of, which is the run a wave's copy fills.
+    const int cq_hh = (tid >> 4) % kHeadsPerTask;
+    const int cq_part = tid & 15;
+    const int cq_h = kHeadsPerTask * (hc - hkv * nchunks) + cq_hh;  // its head in the group
+    const bool cq_req = kRectify && req >= 0 && req < p.R;
+    int cq = 0;               // rounds issued (uniform)
+    bool cq_pending = false;  // round cq - 1 loaded, its query part not yet stored
+    uint4 cq_src = make_uint4(0, 0, 0, 0);
+    auto cq_row = [&](int k) { return (16 * k + (tid >> 4)) / kHeadsPerTask; };
+    auto cq_issue = [&](int k) {
+      const int r = min(cq_row(k), nrows - 1);  // (rows past the block: a valid address, not stored)
+      const int64_t e = ((static_cast<int64_t>(s_qo[b]) + r_local + r) * Hq + hkv * G + min(cq_h, G - 1)) * kHeadDim +
+                        8 * cq_part;
+      cq_src = *reinterpret_cast<const uint4*>(p.src_q + e);
+      // the wave's run: row (16 k + 4 wave) / kHeadsPerTask, heads from (4 wave) % kHeadsPerTask
+      uint4* run = &s_of[((16 * k + 4 * wave) / kHeadsPerTask) * kOfRow + 16 * ((4 * wave) % kHeadsPerTask)];
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(p.o_full + e),
+                                       (__attribute__((address_space(3))) void*)(run), 16, 0, 0);
+    };
+    auto cq_store = [&](int k) {
+      const int r = cq_row(k);
+      if (cq_req && r < nrows && cq_h < G) {
+        const int slot = static_cast<int>((static_cast<int64_t>(max(before, 0)) + r_local + r) % p.M);
+        const int64_t e = ((static_cast<int64_t>(req) * p.M + slot) * Hq + hkv * G + cq_h) * kHeadDim + 8 * cq_part;
+        *reinterpret_cast<uint4*>(p.q_cache + e) = cq_src;
+        if (p.q_post_cache != nullptr)
+          *reinterpret_cast<uint4*>(p.q_post_cache + e) = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
+      }
+    };
 
     // Q rows of the wave's heads (B operands): lane (quad, col) holds
     // Q[row col][8 (4s + quad) .. +8]; rows of absent heads are zero
@@ -503,6 +549,10 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
           }
           s_v[buf][ld_pv0] = vq0;
           s_v[buf][ld_pv1] = vq1;
+          if (kRectify && cq_pending) {
+            cq_store(cq - 1);
+            cq_pending = false;
+          }
           if (lane == 0) {
             // lanes 16 r hold keys 8 wave + 2 r and 8 wave + 2 r + 1
             uint32_t bits = 0;
@@ -523,6 +573,11 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
           vq1 = ld(vbase, rc1);
           rn0 = index_of(i + 2, 0);  // clamped: harmless past the last block
           rn1 = index_of(i + 2, 1);
+        }
+        if (kRectify && cq < kHeadsPerTask) {
+          cq_issue(cq);
+          ++cq;
+          cq_pending = true;
         }
         if (nheads == 0) continue;
         const int base = seg_lo + i * kBlk;
@@ -638,6 +693,14 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
       }
       if (seg == 0) __syncthreads();  // the sink's last tiles are read before the window stages into them
     }
+    if (kRectify) {  // the rounds the blocks did not carry; then s_of is complete for every wave
+      if (cq_pending) cq_store(cq - 1);
+      for (; cq < kHeadsPerTask; ++cq) {
+        cq_issue(cq);
+        cq_store(cq);
+      }
+      __syncthreads();
+    }
     if (nheads == 0 || !row_ok) continue;
 
     if (!kRectify) {
@@ -667,28 +730,17 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
     const int slot = static_cast<int>((static_cast<int64_t>(before) + local) % p.M);
     const int64_t drow = static_cast<int64_t>(req) * p.M + slot;
     const bool empty = pos + 1 - p.S <= (sink ? p.F : 0);  // nothing left after the downdate
-    // every load of the epilogue (the full state's o and the pre-RoPE query
-    // of the wave's heads) is issued before its math: one round of latency,
-    // not two per head
-    uint32_t fow[HPW][16], sqw[HPW][16];
+    // the full state's o of the lane's row, dims 16 dt + 4 quad .. + 3 of
+    // each of the wave's heads, from s_of
+    uint32_t fow[HPW][16];
+    const uint2* of2 = reinterpret_cast<const uint2*>(s_of);
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) {
-      const int h = hkv * G + min(hg0 + hh, G - 1);
-      const uint16_t* of = p.o_full + (grow * Hq + h) * kHeadDim + 4 * quad;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const uint2 f = *reinterpret_cast<const uint2*>(of + 16 * dt);
+        const uint2 f = of2[2 * (col * kOfRow + 16 * (HPW * wave + hh) + 2 * dt + (quad >> 1)) + (quad & 1)];
         fow[hh][2 * dt] = f.x;
         fow[hh][2 * dt + 1] = f.y;
-      }
-      const uint16_t* sq = p.src_q + (grow * Hq + h) * kHeadDim;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const uint4 w = *reinterpret_cast<const uint4*>(sq + 8 * (4 * s + quad));
-        sqw[hh][4 * s] = w.x;
-        sqw[hh][4 * s + 1] = w.y;
-        sqw[hh][4 * s + 2] = w.z;
-        sqw[hh][4 * s + 3] = w.w;
       }
     }
 #pragma unroll
@@ -720,18 +772,8 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
         *reinterpret_cast<uint2*>(ap + 16 * dt) = w;
       }
       if (quad == 0) p.lse_cache[drow * Hq + h] = (p.sink_mode == 0 && p.F > 0) ? -INFINITY : c.lse;
-      // pre-RoPE query row and the NaN marker of the unknown post-RoPE row (PREFILL:251-262)
-      uint16_t* dq = p.q_cache + (drow * Hq + h) * kHeadDim;
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        *reinterpret_cast<uint4*>(dq + 8 * (4 * s + quad)) =
-            make_uint4(sqw[hh][4 * s], sqw[hh][4 * s + 1], sqw[hh][4 * s + 2], sqw[hh][4 * s + 3]);
-      if (p.q_post_cache != nullptr) {
-        uint16_t* pq = p.q_post_cache + (drow * Hq + h) * kHeadDim;
-        const uint4 nan4 = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
-#pragma unroll
-        for (int s = 0; s < 4; ++s) *reinterpret_cast<uint4*>(pq + 8 * (4 * s + quad)) = nan4;
-      }
+      // (the pre-RoPE query row and the NaN marker of the unknown post-RoPE
+      // row, PREFILL:251-262, went into the ring with the key blocks)
     }
   }
 }
