@@ -300,6 +300,24 @@ def test_rectify_by_batch_request_length_and_bad_request(rect_ext):
     np.testing.assert_array_equal(g["rl"].cpu().numpy(), [5, 6, 7])
 
 
+@pytest.mark.parametrize("hq", [8, 16])
+def test_rectify_many_requests(rect_ext, hq):
+    """4096 requests (the planner's maximum: its per-request tables take 49 KB
+    of LDS beside the fused form's own tiles and full-state rows; hq 8 and 16
+    over 2 KV heads run the one- and the two-head-per-wave form), most a few
+    rows long, some empty, one longer than the ring, in permuted ring rows."""
+    rng = np.random.default_rng(31 + hq)
+    B, M = 4096, 4
+    qo = rng.integers(0, 4, B)
+    qo[5] = 40
+    kv = qo + rng.integers(0, 20, B)
+    case = syn.prefill_case(qo_lens=qo.tolist(), kv_lens=kv.tolist(), hq=hq, hkv=2, seed=31 + hq)
+    e, g, _ = _run_rectify(rect_ext, case, S=8, F=0, sink_mode=0, M=M, R=B + 1,
+                           req_ids=rng.permutation(B).tolist(),
+                           request_length=rng.integers(0, 50, B + 1).tolist(), q_post_cache=True, seed=hq)
+    _compare_ring(e, g, f"4096 requests, hq={hq}")
+
+
 def test_rectify_skips_requests_outside_the_buffers(rect_ext):
     """The fused rectification skips a request with fewer keys than queries
     and one whose key range runs past kv_indices, as the window pass does:
