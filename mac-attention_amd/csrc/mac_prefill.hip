@@ -403,6 +403,23 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
     const int pos = pos0 + col;  // this lane's row position
     const int64_t grow = static_cast<int64_t>(s_qo[b]) + r_local + (row_ok ? col : 0);
     const int w_lo = wl < 0 ? 0 : max(pos - wl, 0);  // this row's window [w_lo, pos]
+    // this request's kv_indices; entry offsets fit 32 bits (fewer than 2^30
+    // entries, checked on the host), so a load is a uniform base plus a
+    // 32-bit lane offset
+    const char* kvi = reinterpret_cast<const char*>(p.kv_indices + kv_begin);
+    auto index_at = [&](int key) -> int {  // entry of a key, clamped into the request
+      return *reinterpret_cast<const int*>(kvi + min(static_cast<uint32_t>(key), static_cast<uint32_t>(kvlen - 1)) * 4u);
+    };
+    // The entries of the first segment's first two blocks (the loader's keys)
+    // go out first, ahead of the Q rows and the epilogue's inputs: the first
+    // K/V loads then wait for these entries only, not for everything issued
+    // before them (the memory counter retires loads in order).
+    const int seg_first = sink ? 0 : 1;
+    const int lo_first = seg_first == 0 ? 0 : (wl < 0 ? 0 : max(pos0 - wl, 0));
+    int pre_raw[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) pre_raw[t] = index_at(lo_first + (t >> 1) * kBlk + ld_key + (t & 1));
+    __builtin_amdgcn_sched_barrier(0);  // (kept ahead of the loads below)
     // fused form: the epilogue's inputs that do not depend on the attention,
     // loaded now so that their latency hides behind it
     int req = 0, before = 0;
@@ -459,19 +476,19 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
     };
 
     // Q rows of the wave's heads (B operands): lane (quad, col) holds
-    // Q[row col][8 (4s + quad) .. +8]; rows of absent heads are zero
+    // Q[row col][8 (4s + quad) .. +8].  A lane past the block's rows reads
+    // the block's first row and an absent head reads the group's first head
+    // (valid data, never zeroed): every score of such a lane is masked
+    // (kmask 0), an absent head is never stored, and each head keeps its own
+    // softmax state.  With no select on the loaded values no wait follows
+    // the loads: the Q rows and the first entries are one round of loads.
     uint4 qreg[HPW][4];
 #pragma unroll
     for (int i = 0; i < HPW; ++i) {
-      const bool hv = hg0 + i < G;
-      const int h = hkv * G + (hv ? hg0 + i : 0);
+      const int h = hkv * G + (hg0 + i < G ? hg0 + i : 0);
       const uint16_t* qp = p.q + (grow * Hq + h) * kHeadDim;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        uint4 w = *reinterpret_cast<const uint4*>(qp + 8 * (4 * s + quad));
-        if (!row_ok || !hv) w = make_uint4(0, 0, 0, 0);
-        qreg[i][s] = w;
-      }
+      for (int s = 0; s < 4; ++s) qreg[i][s] = *reinterpret_cast<const uint4*>(qp + 8 * (4 * s + quad));
     }
 
     // l[h]: the softmax row sums.  Plain form: the lane's fp32 partial sums
@@ -492,14 +509,34 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
 
     const char* kbase = reinterpret_cast<const char*>(p.k + static_cast<int64_t>(hkv) * kHeadDim + ld_chunk * 8);
     const char* vbase = reinterpret_cast<const char*>(p.v + static_cast<int64_t>(hkv) * kHeadDim + ld_chunk * 8);
-    // this request's kv_indices; entry offsets fit 32 bits (fewer than 2^30
-    // entries, checked on the host), so a load is a uniform base plus a
-    // 32-bit lane offset
-    const char* kvi = reinterpret_cast<const char*>(p.kv_indices + kv_begin);
     bool fresh = true;  // no block computed yet: the first sets m without a rescale
+    auto ld = [&](const char* base, int r) -> uint4 {  // one v_mad_u64_u32 per address
+      return *reinterpret_cast<const uint4*>(base + static_cast<uint64_t>(static_cast<uint32_t>(max(r, 0))) * row_bytes);
+    };
+    // the loader's K/V chunks of the block in flight (rc0/rc1: their rows,
+    // -1: masked) and the raw indices of the block after it
+    int rc0 = -1, rc1 = -1, rn0 = 0, rn1 = 0;
+    uint4 kq0 = make_uint4(0, 0, 0, 0), kq1 = kq0, vq0 = kq0, vq1 = kq0;
+    {
+      // the first segment's block 0 goes in flight here, right behind the Q
+      // rows (issued in the segment loop, its loads would wait for every
+      // load before them: the loop's entry joins the counts)
+      const int hi_first = seg_first == 0 ? min(p.F, max(pos_last - wl, 0)) : pos_last + 1;
+      if (hi_first > lo_first) {
+        const int k0 = lo_first + ld_key;
+        rc0 = (k0 < hi_first && static_cast<unsigned>(pre_raw[0]) < pool_rows) ? pre_raw[0] : -1;
+        rc1 = (k0 + 1 < hi_first && static_cast<unsigned>(pre_raw[1]) < pool_rows) ? pre_raw[1] : -1;
+        kq0 = ld(kbase, rc0);
+        kq1 = ld(kbase, rc1);
+        vq0 = ld(vbase, rc0);
+        vq1 = ld(vbase, rc1);
+        rn0 = pre_raw[2];
+        rn1 = pre_raw[3];
+      }
+    }
     // segment 0: the front sink [0, min(F, w_lo)) of each row (fused form,
     // sink_mode 1); segment 1: the window [w_lo, pos]
-    for (int seg = sink ? 0 : 1; seg < 2; ++seg) {
+    for (int seg = seg_first; seg < 2; ++seg) {
       const int seg_lo = seg == 0 ? 0 : (wl < 0 ? 0 : max(pos0 - wl, 0));
       const int seg_hi = seg == 0 ? min(p.F, max(pos_last - wl, 0)) : pos_last + 1;
       const int r_lo = seg == 0 ? 0 : w_lo;  // this row's keys in the segment: [r_lo, r_hi)
@@ -510,22 +547,12 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
       // (-1: masked).  An index is loaded one block before it is checked, so
       // the wait for it never includes K/V loads issued after it (the memory
       // counter retires in order).
-      auto index_of = [&](int i, int t) -> int {
-        const uint32_t key = static_cast<uint32_t>(seg_lo + i * kBlk + ld_key + t);
-        return *reinterpret_cast<const int*>(kvi + min(key, static_cast<uint32_t>(kvlen - 1)) * 4u);
-      };
+      auto index_of = [&](int i, int t) -> int { return index_at(seg_lo + i * kBlk + ld_key + t); };
       auto row_of = [&](int i, int t, int raw) -> int {
         const int key = seg_lo + i * kBlk + ld_key + t;
         return (key < seg_hi && static_cast<unsigned>(raw) < pool_rows) ? raw : -1;
       };
-      auto ld = [&](const char* base, int r) -> uint4 {  // one v_mad_u64_u32 per address
-        return *reinterpret_cast<const uint4*>(base + static_cast<uint64_t>(static_cast<uint32_t>(max(r, 0))) * row_bytes);
-      };
-      // the loader's K/V chunks of the block in flight (rc0/rc1: their rows)
-      // and the raw indices of the block after it
-      int rc0 = -1, rc1 = -1, rn0 = 0, rn1 = 0;
-      uint4 kq0 = make_uint4(0, 0, 0, 0), kq1 = kq0, vq0 = kq0, vq1 = kq0;
-      if (nblk > 0) {
+      if (seg != seg_first && nblk > 0) {  // (the first segment's block 0 is in flight)
         rc0 = row_of(0, 0, index_of(0, 0));
         rc1 = row_of(0, 1, index_of(0, 1));
         kq0 = ld(kbase, rc0);
@@ -606,7 +633,7 @@ __global__ void __launch_bounds__(256, (HPW == 1 && !kRectify) ? 3 : 2) window_k
         // blocks inside every row's range with every key present need no masks
         const bool full = !__any(kmask != 0xffu);
         // raw scores of both tiles and every head, the four accumulation chains
-        // interleaved (an absent head has zero Q rows and is never stored)
+        // interleaved (an absent head is computed but never stored)
         f32x4_t c4[HPW][2];
 #pragma unroll
         for (int h = 0; h < HPW; ++h)
