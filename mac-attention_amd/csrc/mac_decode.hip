@@ -2368,6 +2368,13 @@ int mac::decode_impl(const MacDecodeArgs* a, void* stream_ptr, hipEvent_t* ev) {
                   a->complete_task_go && a->complete_task_tile && a->task_counts && a->partial_o &&
                   a->partial_lse,
               "a required pointer is NULL");
+  // the kernels move these with 16-, 8- and 4-byte vector accesses
+  auto aligned = [](const void* ptr, uintptr_t n) { return (reinterpret_cast<uintptr_t>(ptr) & (n - 1)) == 0; };
+  MAC_REQUIRE(aligned(a->q_post, 16) && aligned(a->q_pre, 16) && aligned(a->k_buffer, 16) &&
+                  aligned(a->v_buffer, 16) && aligned(a->query_cache, 16),
+              "q_post, q_pre, k_buffer, v_buffer and query_cache must be 16-byte aligned");
+  MAC_REQUIRE(aligned(a->attn_cache, 4) && aligned(a->out, 4) && aligned(a->partial_o, 8),
+              "attn_cache and out must be 4-byte aligned, partial_o 8-byte aligned");
 
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   int dev = 0;

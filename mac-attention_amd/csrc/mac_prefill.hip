@@ -888,6 +888,9 @@ extern "C" int mac_update_then_downdate_bf16_inplace(const void* out1, const voi
 
 namespace {
 
+// the kernels move bf16 rows with 16-byte vector accesses
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
 int check_window_common(int B, int Hq, int Hkv, int D, int64_t total_q, int64_t pool, const void* q,
                         const void* k, const void* v, const int32_t* qo, const int32_t* kvp, const int32_t* kvi,
                         int64_t kv_len) {
@@ -897,6 +900,7 @@ int check_window_common(int B, int Hq, int Hkv, int D, int64_t total_q, int64_t 
   REQUIRE(total_q >= 0 && total_q <= INT_MAX && pool > 0, "bad total_q / pool_tokens");
   REQUIRE(total_q * Hq <= static_cast<int64_t>(INT_MAX) * 64, "total_q too large");
   REQUIRE(q && k && v && qo && kvp && kvi, "null pointer argument");
+  REQUIRE(aligned16(q) && aligned16(k) && aligned16(v), "q, k and v must be 16-byte aligned");
   // the window kernel addresses a request's kv_indices with 32-bit byte offsets
   REQUIRE(kv_len >= 0 && kv_len < (int64_t{1} << 30), "kv_indices must hold fewer than 2^30 entries");
   return MAC_OK;
@@ -913,6 +917,7 @@ extern "C" int mac_prefill_window_attention_bf16(const MacWindowAttentionArgs* a
                                    a->v_buffer, a->qo_indptr, a->kv_indptr, a->kv_indices, a->kv_indices_len))
     return rc;
   REQUIRE(a->out && a->out_lse, "out / out_lse must not be NULL");
+  REQUIRE(aligned16(a->out), "out must be 16-byte aligned");
   if (a->B == 0 || a->total_q == 0) return MAC_OK;
   WindowParams p{};
   p.q = static_cast<const uint16_t*>(a->q);
@@ -955,6 +960,9 @@ extern "C" int mac_prefill_rectify_update_cache_bf16(const MacRectifyArgs* a, vo
   REQUIRE(a->src_q && a->o_full && a->lse_full && a->q_cache && a->attn_cache && a->lse_cache &&
               a->request_length && a->req_ids,
           "null pointer argument");
+  REQUIRE(aligned16(a->src_q) && aligned16(a->o_full) && aligned16(a->q_cache) && aligned16(a->attn_cache) &&
+              (a->q_post_cache == nullptr || aligned16(a->q_post_cache)),
+          "src_q, o_full, q_cache, attn_cache and q_post_cache must be 16-byte aligned");
   if (a->B == 0 || a->total_q == 0) return MAC_OK;
   WindowParams p{};
   p.q = static_cast<const uint16_t*>(a->q_post);

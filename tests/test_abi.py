@@ -150,6 +150,49 @@ def test_prefill_entry_points_reject_bad_arguments(bridge):
     assert b"struct_size mismatch" in lib.mac_last_error()
 
 
+def _pointers(args, base=0x10000):
+    """Every pointer field of an argument struct set to its own 256-byte
+    aligned dummy address (validation fails before anything is read)."""
+    for i, (name, typ) in enumerate(args._fields_):
+        if typ is ctypes.c_void_p:
+            setattr(args, name, base + 256 * i)
+
+
+def test_entry_points_reject_misaligned_pointers(bridge):
+    """The kernels move rows with 16-byte (and 8-/4-byte) vector accesses: a
+    misaligned pointer is refused with a message, before any GPU work."""
+    lib = bridge.load_library()
+    a = bridge.MacDecodeArgs()
+    a.struct_size, a.abi_version = ctypes.sizeof(a), bridge.ABI_VERSION
+    a.N, a.Hq, a.Hkv, a.D, a.M, a.R = 1, 8, 2, 128, 8, 1
+    a.workspace_rows, a.tile_tokens, a.match_tile_slots, a.max_match_tiles = 1, 256, 8, 1
+    a.max_context, a.max_tiles_context, a.complete_task_len = 1024, 4, 64
+    a.req_to_token_rows, a.req_to_token_stride = 1, 1024
+    for field, offset, msg in (("k_buffer", 8, b"16-byte aligned"), ("query_cache", 4, b"16-byte aligned"),
+                               ("out", 2, b"4-byte aligned"), ("partial_o", 4, b"8-byte aligned")):
+        _pointers(a)
+        setattr(a, field, getattr(a, field) + offset)
+        assert lib.mac_persistent_decode_bf16(ctypes.byref(a), None) == 1, field
+        assert msg in lib.mac_last_error(), (field, lib.mac_last_error())
+    w = bridge.MacWindowAttentionArgs()
+    w.struct_size, w.abi_version = ctypes.sizeof(w), bridge.ABI_VERSION
+    w.B, w.Hq, w.Hkv, w.D, w.total_q, w.pool_tokens, w.kv_indices_len = 1, 8, 2, 128, 4, 16, 4
+    for field in ("q", "v_buffer", "out"):
+        _pointers(w)
+        setattr(w, field, getattr(w, field) + 2)
+        assert lib.mac_prefill_window_attention_bf16(ctypes.byref(w), None) == 1, field
+        assert b"16-byte aligned" in lib.mac_last_error(), (field, lib.mac_last_error())
+    r = bridge.MacRectifyArgs()
+    r.struct_size, r.abi_version = ctypes.sizeof(r), bridge.ABI_VERSION
+    r.B, r.Hq, r.Hkv, r.D, r.total_q, r.pool_tokens, r.kv_indices_len = 1, 8, 2, 128, 4, 16, 4
+    r.M, r.R, r.semantic_pos_ahead, r.request_length_len = 4, 1, 8, 1
+    for field in ("o_full", "src_q", "q_post_cache"):
+        _pointers(r)
+        setattr(r, field, getattr(r, field) + 8)
+        assert lib.mac_prefill_rectify_update_cache_bf16(ctypes.byref(r), None) == 1, field
+        assert b"16-byte aligned" in lib.mac_last_error(), (field, lib.mac_last_error())
+
+
 def test_binding_rejects_host_tensors(bridge):
     torch = pytest.importorskip("torch")
     ext = bridge.PersistentDecodeExtension(bridge.load_library())
