@@ -8,6 +8,15 @@
  * null stream).  No entry point allocates device memory or synchronises the
  * host, so every call may be captured into a hipGraph.
  *
+ * Alignment: tensors of 128-element bf16 rows that the kernels move with
+ * 16-byte vector accesses (decode: q_post, q_pre, k_buffer, v_buffer,
+ * query_cache; window attention: q, k_buffer, v_buffer, out; rectification:
+ * those of the window plus src_q, o_full, q_cache, attn_cache,
+ * q_post_cache) must start on a 16-byte boundary, the decode step's
+ * attn_cache and out on 4 bytes and partial_o on 8; a misaligned pointer is
+ * refused with MAC_ERR_INVALID_ARGUMENT.  Framework allocations and row
+ * views of them always qualify.
+ *
  * Return value: 0 on success, otherwise a MAC_ERR_* code; mac_last_error()
  * then returns a NUL-terminated message for the calling thread.
  *
