@@ -300,6 +300,18 @@ def test_rectify_by_batch_request_length_and_bad_request(rect_ext):
     np.testing.assert_array_equal(g["rl"].cpu().numpy(), [5, 6, 7])
 
 
+@pytest.mark.parametrize("hq,hkv", [(6, 2), (12, 2)])
+def test_rectify_group_with_absent_heads(rect_ext, hq, hkv):
+    """GQA groups of 3 and 6 heads: a task covers 4 (one head per wave) or
+    8 (two) heads, so its last heads are absent -- their query and full-state
+    rows are read from the group's first head and never stored -- with the
+    front sink as its own key segment."""
+    case = syn.prefill_case(qo_lens=[40, 7, 33], kv_lens=[70, 7, 90], hq=hq, hkv=hkv, seed=71 + hq)
+    e, g, _ = _run_rectify(rect_ext, case, S=16, F=4, sink_mode=1, M=20, R=4, req_ids=[3, 0, 1],
+                           request_length=[5, 0, 13, 2], q_post_cache=True, seed=hq)
+    _compare_ring(e, g, f"G={hq // hkv}")
+
+
 @pytest.mark.parametrize("hq", [8, 16])
 def test_rectify_many_requests(rect_ext, hq):
     """4096 requests (the planner's maximum: its per-request tables take 49 KB
