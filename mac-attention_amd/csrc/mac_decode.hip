@@ -232,11 +232,11 @@ struct MergeParams {
 // saves), so it reads the previous step's, which span_attention's workgroup
 // 0 leaves in fuse_sync: [0] short groups, [1] long groups, [2] tokens / 64.
 // Decode steps of a batch change slowly, so the previous step's counts are
-// the usual case; the rule only moves work between kernels, and every group
-// gets the same results either way, up to rounding (the two paths sum in
-// different orders), so two calls on the same inputs can differ in the last
-// bits when their previous steps differed (MAC_AMD_FUSE_POLICY=always pins
-// the choice).
+// the usual case.  The rule only moves work between kernels: both run a short
+// group through short_group with the same states, combine order and merges,
+// so its results are the same bits either way, and a step's results do not
+// depend on the steps before it (MAC_AMD_FUSE_POLICY pins the choice, for
+// measurements).
 __device__ __forceinline__ int step_fuse_rule(const DecideParams& p, const uint32_t (&c)[3]) {
   const uint32_t n_short = c[0], n_long = c[1];
   const long long all_tokens = static_cast<long long>(c[2]) << 6;
@@ -2267,7 +2267,7 @@ int attn_residency(int dev, int G, size_t dyn_lds, int* cus, int* per_cu) {
 
 // Waves per match_decide workgroup when a step has at most one group per CU
 // (MAC_AMD_MATCH_WAVES, read per call: 8, the default, or 4; the two give the
-// same results up to the order the waves' states are combined).
+// same bits: the blocks go to four virtual waves either way).
 int match_waves() {
   const char* e = std::getenv("MAC_AMD_MATCH_WAVES");
   return (e != nullptr && std::atoi(e) == 4) ? 4 : 8;
