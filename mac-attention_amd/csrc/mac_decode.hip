@@ -229,8 +229,9 @@ struct MergeParams {
 // long tasks first.  The counts the rule needs are the whole step's, which a
 // workgroup cannot know when it decides (a device-wide count and wait, or
 // even just counting with atomics on shared words, cost more than the rule
-// saves), so it reads the previous step's, which span_attention's workgroup
-// 0 leaves in fuse_sync: [0] short groups, [1] long groups, [2] tokens / 64.
+// saves), so it reads the previous step's, which merge_write's counting
+// workgroup leaves in fuse_sync: [0] short groups, [1] long groups, [2]
+// tokens / 64.
 // Decode steps of a batch change slowly, so the previous step's counts are
 // the usual case.  The rule only moves work between kernels: both run a short
 // group through short_group with the same states, combine order and merges,
