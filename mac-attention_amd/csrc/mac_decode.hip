@@ -1,38 +1,49 @@
 // mac_decode.hip -- MAC-Attention fused decode step for MI355X (gfx950).
 //
-// One decode step is three kernels on the caller's stream (graph-capturable,
-// no host synchronisation, no allocation):
+// One decode step is three kernels on the caller's stream (four for rings
+// scanned in slot ranges; graph-capturable, no host synchronisation, no
+// allocation):
 //
-//  1. match_decide  (one workgroup per (request, KV head) group)
+//  1. match_decide  (one workgroup per (request, KV head) group, four or
+//     eight waves; for rings of three or more 256-slot ranges, a range-split
+//     probe scan over (group, range) workgroups, then the decision kernel)
 //     Scans the request's ring of cached pre-RoPE queries for every query head
 //     of the group (squared L2, best = smallest distance, ties to the smaller
 //     logical position), applies the readiness gate and the optional synthetic
 //     bench override, and turns the per-head results into the group's mode and
 //     its KV spans: sink [0, min(F, new_end)), band [rect_begin, new_end) and
-//     tail [new_end, kv_len).  Reference: DECODE:942-1099, :1101-1402.
+//     tail [new_end, kv_len).  A short group (at most fuse_tokens tokens: in
+//     practice the all-hit groups, whose band is at most the ring capacity) is
+//     finished here when the short-group rule says so (short_group: its
+//     attention, the merge with the cached entry, the ring row and out).
+//     Reference: DECODE:942-1099, :1101-1402.
 //
 //  2. span_attention  (persistent grid sized to the device's residency)
-//     Every workgroup plans the same task list from the group spans: the
-//     spans are cut into chunks of C tokens (C picked from the total token
-//     count so that the grid gets ~12 tasks per workgroup), and workgroups
-//     fetch tasks through an atomic counter.  A task streams the K/V rows of its chunk once
-//     for all G query heads of the group (16 lanes per token row, 16-byte
-//     loads, two tokens per row in flight plus a one-iteration prefetch),
-//     masks band positions that precede a head's own band start, and keeps an
-//     online log2-domain softmax per head.  The task writes one partial
-//     (o, lse) per head.  Reference producers: DECODE:1870-3423.
+//     Every workgroup plans the same task list from the group spans: the long
+//     groups' spans are cut into chunks of C tokens (C picked from the total
+//     token count so that the grid gets ~12 tasks per workgroup; the last
+//     quarter of a long band in half chunks where the partial slots allow),
+//     a short group left to this kernel is one task, and workgroups claim
+//     tasks through an atomic counter, full chunks first.  A task streams its
+//     K/V rows in 32-token blocks for all G query heads of the group (S^T =
+//     K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x32_bf16, the blocks dealt
+//     to four waves, an online log2-domain softmax per head) and writes one
+//     partial (o, lse) per head.  Reference producers: DECODE:1870-3423.
 //
-//  3. merge_write  (one workgroup per group)
+//  3. merge_write  (one workgroup per (group, query head); those of groups
+//     already finished return at once; one more workgroup counts)
 //     Per head: cached entry (hit heads) + band partials -> ring row at
 //     past_len % M (only for ready requests) -> + sink and tail partials ->
-//     out / out_lse.  Reference: DECODE:4280-4685.
+//     out / out_lse.  The counting workgroup writes the per-group task
+//     descriptors and the step's counters.  Reference: DECODE:4280-4685.
 //
 // Workspace use (caller-owned, reference names):
 //   head_*, group_mode, group_rect_begin/end, group_tail_begin/end: same
 //     meaning as in the reference (DECODE:1270-1402);
 //   group_rect_tiles / group_tail_tiles: number of band / tail tasks;
 //   complete_task_go[g]: chunk size C_g of group g; complete_task_tile[g]:
-//     number of tasks of group g (written by workgroup 0 of span_attention);
+//     number of tasks of group g (written by merge_write's counting
+//     workgroup);
 //     complete_task_go[NG + g]: 1 if match_decide finished group g;
 //     complete_task_go[2 NG]: 1 if any group was left to span_attention;
 //     complete_task_go[2 NG + 2 .. + 4]: the previous step's short groups,
