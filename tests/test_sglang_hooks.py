@@ -6,7 +6,6 @@ scheduler processes install the hooks themselves.  Reference behaviour:
 hook_installer.py:46-372, schedule_hooks.py:8-66, child_process.py:1-21,
 plugin.py:37-69, pyproject.toml:27-28."""
 
-import argparse
 import enum
 import os
 import sys
