@@ -820,7 +820,7 @@ EXPORT void mac_oracle_rectify_update_cache(
     float* lse_cache, uint16_t* q_post_cache, int32_t* request_length, int request_length_len,
     const int32_t* req_ids, int B, int R, int M, int Hq, int Hkv, int D, int S, int F,
     int sink_mode, double sm_scale, int64_t total_q, int64_t kv_indices_len) {
-  if (M <= 0 || B == 0) return;
+  if (M <= 0 || B <= 0) return;
   const int G = Hq / Hkv;
   const int by_batch = request_length_len == B;
   const size_t rowsz = (size_t)Hq * D;
