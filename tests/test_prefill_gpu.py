@@ -300,6 +300,32 @@ def test_rectify_by_batch_request_length_and_bad_request(rect_ext):
     np.testing.assert_array_equal(g["rl"].cpu().numpy(), [5, 6, 7])
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_rectify_random_shapes(rect_ext, seed):
+    """Random batches against the oracle: request and prefix lengths (empty
+    chunks, chunks shorter and longer than the ring, prefixes shorter and
+    longer than the window), GQA shapes of both kernel instances, window,
+    front sink, sink mode and ring size drawn per seed."""
+    rng = np.random.default_rng(100 + seed)
+    B = int(rng.integers(1, 9))
+    hq, hkv = [(8, 2), (16, 2), (6, 2), (32, 4), (4, 1), (12, 4)][seed % 6]
+    qo = rng.integers(0, 70, B)
+    kv = qo + rng.integers(0, 120, B)
+    S = int(rng.choice([8, 16, 64]))
+    F = int(rng.choice([0, 4, 20]))
+    sink_mode = int(rng.integers(0, 2)) if F > 0 else 0
+    M = int(rng.choice([4, 12, 32]))
+    R = B + 2
+    print(f"rectify random shapes: seed={seed} B={B} G={hq // hkv} S={S} F={F} sink_mode={sink_mode} M={M}",
+          flush=True)
+    case = syn.prefill_case(qo_lens=qo.tolist(), kv_lens=kv.tolist(), hq=hq, hkv=hkv, seed=200 + seed)
+    e, g, _ = _run_rectify(rect_ext, case, S=S, F=F, sink_mode=sink_mode, M=M, R=R,
+                           req_ids=rng.permutation(R)[:B].tolist(),
+                           request_length=rng.integers(0, 40, R).tolist(), q_post_cache=bool(seed % 2),
+                           seed=seed)
+    _compare_ring(e, g, f"random seed={seed}")
+
+
 @pytest.mark.parametrize("hq,hkv", [(6, 2), (12, 2)])
 def test_rectify_group_with_absent_heads(rect_ext, hq, hkv):
     """GQA groups of 3 and 6 heads: a task covers 4 (one head per wave) or
