@@ -129,6 +129,32 @@ def test_window_attention_matches_oracle(rect_ext, window_left, hq, hkv):
     np.testing.assert_allclose(lse.cpu().numpy(), el, atol=2e-4, rtol=1e-5)
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_window_attention_random_shapes(rect_ext, seed):
+    """Random batches against the oracle: chunk and prefix lengths (row
+    blocks cut short, empty chunks), GQA shapes of both kernel instances
+    with absent heads, causal and windowed."""
+    rng = np.random.default_rng(300 + seed)
+    B = int(rng.integers(1, 7))
+    hq, hkv = [(8, 2), (12, 2), (6, 2), (32, 4), (3, 1), (16, 2)][seed % 6]
+    qo = rng.integers(0, 90, B)
+    kv = qo + rng.integers(0, 150, B)
+    window_left = int(rng.choice([-1, 0, 7, 63, 200]))
+    print(f"window random shapes: seed={seed} B={B} G={hq // hkv} window_left={window_left}", flush=True)
+    case = syn.prefill_case(qo_lens=qo.tolist(), kv_lens=kv.tolist(), hq=hq, hkv=hkv, seed=400 + seed)
+    d = _dev_case(case)
+    out, lse = rect_ext.window_attention_return_lse(d["q"], d["k"], d["v"], d["qo"], d["kv"], d["idx"],
+                                                    window_left, case.sm_scale)
+    torch.cuda.synchronize()
+    eo, el = orc.window_attention(_bf(case.q), _bf(case.k), _bf(case.v), case.qo_indptr,
+                                  case.kv_indptr, case.kv_indices, window_left=window_left,
+                                  sm_scale=case.sm_scale)
+    got = bits(_host_bits(out))
+    for r in range(got.shape[0]):
+        assert rel_l2(got[r], bits(eo[r])) < 1e-2, r
+    np.testing.assert_allclose(lse.cpu().numpy(), el, atol=2e-4, rtol=1e-5)
+
+
 @pytest.mark.parametrize("hkv", [16, 8, 4])
 def test_window_attention_is_deterministic(rect_ext, hkv):
     """The same inputs give the same bits on every call, for both kernel
