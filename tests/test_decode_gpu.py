@@ -182,6 +182,35 @@ def test_random_vs_oracle(cfg, fuse, ext, monkeypatch):
     _check_against_oracle(c, dev, out, out_lse, ws, res, what=str(cfg))
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_random_shapes_vs_oracle(seed, ext, monkeypatch):
+    """Seeded random steps against the oracle: batch, GQA shape (G = 1..8),
+    context lengths (short and long, odd), ring size, window S, front sink,
+    hit rate and the short-group policy drawn per seed."""
+    rng = np.random.default_rng(500 + seed)
+    b = int(rng.integers(1, 6))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    g = int(rng.integers(1, 9))
+    hq = hkv * g
+    m = int(rng.choice([8, 16, 32, 64]))
+    s = int(rng.choice([8, 32, 128, 256]))
+    f = int(rng.choice([0, 0, 4, 64]))
+    kv_lens = [int(x) for x in rng.integers(2, 3000, b)]
+    hit_rate = float(rng.choice([0.0, 0.5, 0.8, 1.0]))
+    fuse = list(FUSE)[seed % len(FUSE)]
+    cfg = (b, hq, hkv, kv_lens, m, s, f, hit_rate, seed)
+    _set_fuse(monkeypatch, fuse)
+    print(f"random shapes {cfg} fuse={fuse}", flush=True)
+    c = syn.random_case(batch=b, hq=hq, hkv=hkv, kv_lens=kv_lens, capacity=m, semantic_pos_ahead=s,
+                        front_sink_tokens=f, hit_rate=hit_rate, match_lag=max(m // 2, 1), seed=600 + seed)
+    res = oracle_run(c)
+    dev = syn.to_device(torch, c, out_cache_loc_dtype=torch.int32 if seed % 2 else torch.int64)
+    out, out_lse, ws = syn.run_decode(torch, ext, dev, c, max_context=max(kv_lens) + 8,
+                                      tile_tokens=16, match_tile_slots=8)
+    torch.cuda.synchronize()
+    _check_against_oracle(c, dev, out, out_lse, ws, res, what=str(cfg))
+
+
 def _bits(dev, out, out_lse):
     return [out.view(torch.int16).clone(), out_lse.view(torch.int32).clone(),
             dev["attn_cache"].view(torch.int16).clone(), dev["lse_cache"].view(torch.int32).clone(),
