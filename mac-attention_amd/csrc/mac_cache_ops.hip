@@ -37,6 +37,7 @@ struct PrefillParams {
   const int32_t* lens;
   int R, M, H, D, B, src_rows;
   int by_batch;
+  int vec16;  // rows move as 16-byte vectors (H D % 8 == 0, every row buffer 16-byte aligned)
 };
 
 // Validity of batch row b and its kept rows [start, ni) (PREFILL:201-230):
@@ -64,7 +65,7 @@ __device__ __forceinline__ void copy_prefill_row(const PrefillParams& p, int b, 
   const int64_t srow = static_cast<int64_t>(p.offsets[b]) + start + i;
   const int64_t row = static_cast<int64_t>(p.H) * p.D;
   const int tid = threadIdx.x;
-  if (row % 8 == 0) {
+  if (p.vec16) {
     const int64_t n16 = row / 8;
     const uint4* sq = reinterpret_cast<const uint4*>(p.src_q + srow * row);
     const uint4* sa = reinterpret_cast<const uint4*>(p.src_attn + srow * row);
@@ -199,6 +200,9 @@ extern "C" int mac_prefill_update_cache(void* q_cache, void* attn_cache, float* 
   p.B = B;
   p.src_rows = src_rows;
   p.by_batch = request_length_len == B ? 1 : 0;
+  auto aligned16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  p.vec16 = (static_cast<int64_t>(num_heads) * head_dim) % 8 == 0 && aligned16(q_cache) && aligned16(attn_cache) &&
+            aligned16(src_q) && aligned16(src_attn);
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(prefill_update_cache_kernel, dim3(capacity, B < 65535 ? B : 65535), dim3(kThreads), 0, st, p);
   HIP_OK(hipGetLastError());

@@ -95,3 +95,61 @@ def test_ready_ops(ext):
     np.testing.assert_array_equal(req_len.cpu().numpy(), e_rl)
     np.testing.assert_array_equal(mrl.cpu().numpy(), e_mrl)
     np.testing.assert_array_equal(cl.cpu().numpy(), e_cl)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_prefill_update_cache_random_shapes(ext, seed):
+    """Seeded random batches: head dims whose rows are not a whole number of
+    16-byte vectors, rings of 1 to 16 slots, empty chunks, a request id
+    outside [0, R), both request_length forms, with and without the q_post
+    ring, and (odd seeds) source rows in views one element off 16-byte
+    alignment, which take the element-wise path; bit for bit."""
+    rng = np.random.default_rng(700 + seed)
+    R = int(rng.integers(2, 8))
+    B = int(rng.integers(1, R + 1))
+    M = int(rng.choice([1, 3, 16]))
+    H = int(rng.choice([1, 3, 8]))
+    D = int(rng.choice([128, 64, 100, 7]))
+    by_batch = bool(rng.integers(0, 2)) and B != R
+    with_qpost = bool(seed % 3)
+    req_ids = rng.permutation(R)[:B].astype(np.int32)
+    if B > 1:
+        req_ids[-1] = R + 3  # outside the ring: skipped
+    lens = rng.integers(0, 40, B).astype(np.int32)
+    offsets = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)
+    rows = int(lens.sum())
+    src_q = syn.to_bits(rng.standard_normal((rows, H, D)))
+    src_a = syn.to_bits(rng.standard_normal((rows, H, D)))
+    src_l = rng.standard_normal((rows, H)).astype(np.float32)
+    qc = syn.to_bits(rng.standard_normal((R, M, H, D)))
+    ac = syn.to_bits(rng.standard_normal((R, M, H, D)))
+    lc = rng.standard_normal((R, M, H)).astype(np.float32)
+    rl = rng.integers(0, 50, B if by_batch else R).astype(np.int32)
+    qp = syn.to_bits(rng.standard_normal((R, M, H, D))) if with_qpost else None
+    print(f"prefill update random: seed={seed} R={R} B={B} M={M} H={H} D={D} by_batch={by_batch}", flush=True)
+    e_qc, e_ac, e_lc, e_rl = qc.copy(), ac.copy(), lc.copy(), rl.copy()
+    e_qp = qp.copy() if qp is not None else None
+    orc.prefill_update_cache(e_qc, e_ac, e_lc, e_rl, req_ids, src_q, src_a, src_l,
+                             np.concatenate([offsets, [rows]]).astype(np.int32), lens, M, H, D, e_qp)
+    dev = "cuda"
+    tb = lambda a: torch.from_numpy(a.view(np.int16)).to(dev).view(torch.bfloat16)  # noqa: E731
+    t = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+
+    def src(a):
+        if seed % 2 == 0:
+            return tb(a)
+        flat = torch.empty(a.size + 1, device=dev, dtype=torch.bfloat16)  # one element off alignment
+        flat[1:] = tb(a).reshape(-1)
+        return flat[1:].view(a.shape)
+
+    g_qc, g_ac, g_lc, g_rl = tb(qc.copy()), tb(ac.copy()), t(lc.copy()), t(rl.copy())
+    g_qp = tb(qp.copy()) if qp is not None else torch.empty(0, device=dev, dtype=torch.bfloat16)
+    ext.mac_prefill_update_cache(g_qc, g_ac, g_lc, g_rl, t(req_ids), src(src_q), src(src_a), t(src_l),
+                                 t(np.concatenate([offsets, [rows]]).astype(np.int32)), t(lens), M, H, D, g_qp)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_bits(g_qc), e_qc)
+    np.testing.assert_array_equal(_bits(g_ac), e_ac)
+    np.testing.assert_array_equal(g_lc.cpu().numpy(), e_lc)
+    np.testing.assert_array_equal(g_rl.cpu().numpy(), e_rl)
+    if qp is not None:
+        np.testing.assert_array_equal(_bits(g_qp), e_qp)
